@@ -1,0 +1,263 @@
+/*
+ * tensor-ash C ABI, MI355X (gfx950) implementation.
+ *
+ * Drop-in for the reference's C header (gusahlg/tensor-ash
+ * include/tensor_ash.h:1-244): same symbol names, argument order, struct
+ * layouts, 0 / -1 / NULL return convention and thread-local
+ * ta_last_error().  Every declaration below cites the reference line it
+ * replaces; the additive extensions at the end have no reference C
+ * counterpart (they expose Rust-API features the reference's C ABI leaves
+ * out, capi/src/api/ops.rs:65-69) and never change an existing layout.
+ */
+#ifndef TENSOR_ASH_H
+#define TENSOR_ASH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ta_context ta_context;   /* ref tensor_ash.h:11 */
+typedef struct ta_executor ta_executor; /* ref tensor_ash.h:12 */
+typedef struct ta_tensor ta_tensor;     /* ref tensor_ash.h:13 */
+typedef struct ta_prepared ta_prepared; /* ref tensor_ash.h:14 */
+
+/* ref tensor_ash.h:16-22.  gpu_time_ns is measured with hipEvents around
+ * the submission on its stream. */
+typedef struct ta_run_stats {
+  uint32_t has_gpu_time;
+  uint64_t gpu_time_ns;
+  size_t n_calls;
+  uint64_t total_flops;
+  double tflops;
+} ta_run_stats;
+
+/* ref tensor_ash.h:24-30.  C <- alpha * A @ B (+ C if accumulate). */
+typedef struct ta_matmul_call {
+  const ta_tensor *a;
+  const ta_tensor *b;
+  const ta_tensor *c;
+  float alpha;
+  uint32_t accumulate;
+} ta_matmul_call;
+
+/* ref tensor_ash.h:33-38. */
+enum {
+  TA_ACTIVATION_NONE = 0,
+  TA_ACTIVATION_RELU = 1,
+  TA_ACTIVATION_SILU = 2, /* x * sigmoid(x) */
+  TA_ACTIVATION_GELU = 3  /* tanh-approximated GELU */
+};
+
+/* ref tensor_ash.h:41-45. */
+enum {
+  TA_BINARY_NONE = 0,
+  TA_BINARY_ADD_SCALED = 1, /* out = act_result + beta * D */
+  TA_BINARY_MUL = 2         /* out = act_result * D */
+};
+
+/* ref tensor_ash.h:47-59.  Applied while the output tile is in
+ * registers: +bias -> activation -> binary op with D.  bias is [N] or
+ * [B, N]; d must be non-null iff binary_kind != 0 and has C's shape. */
+typedef struct ta_epilogue {
+  const ta_tensor *bias;
+  uint32_t activation;  /* TA_ACTIVATION_* */
+  uint32_t binary_kind; /* TA_BINARY_* */
+  const ta_tensor *d;
+  float beta; /* used by TA_BINARY_ADD_SCALED */
+} ta_epilogue;
+
+/* ref tensor_ash.h:61-65. */
+typedef struct ta_matmul_op {
+  ta_matmul_call call;
+  ta_epilogue epilogue;
+} ta_matmul_op;
+
+/* ref tensor_ash.h:67-74. */
+enum {
+  TA_SOFTMAX_MASK_FULL = 0,
+  TA_SOFTMAX_MASK_PREFIX = 1,
+  TA_SOFTMAX_MASK_CAUSAL = 2
+};
+
+/* ref tensor_ash.h:76-85. */
+typedef struct ta_rope_desc {
+  uint32_t heads;
+  uint32_t head_dim;
+  uint32_t rot_dim;
+  uint32_t pos_base;
+} ta_rope_desc;
+
+/* ref tensor_ash.h:87-94. */
+typedef struct ta_copy_desc {
+  uint32_t extent[3];
+  uint32_t src_offset;
+  uint32_t src_strides[3];
+  uint32_t dst_offset;
+  uint32_t dst_strides[3];
+} ta_copy_desc;
+
+/* ref tensor_ash.h:96-104. */
+typedef struct ta_dispatch_info {
+  const char *kernel;
+  uint32_t tile[3];
+  uint32_t has_split_k2;
+  uint32_t split_k2_splits;
+} ta_dispatch_info;
+
+const char *ta_version(void);    /* ref tensor_ash.h:106 */
+const char *ta_last_error(void); /* ref tensor_ash.h:107 */
+
+/* ref tensor_ash.h:109-111.  device_preference: NULL/"auto"/"discrete"
+ * (HIP device 0), "N" or "index:N", "name:<substr>" or "<substr>"
+ * matched against the device name and gfx arch. */
+ta_context *ta_context_create(uint32_t enable_validation,
+                              const char *device_preference);
+void ta_context_destroy(ta_context *ctx); /* ref tensor_ash.h:112 */
+
+/* ref tensor_ash.h:114-116: 1 on HIP devices, 0 for null. */
+uint32_t ta_context_supports_f16(const ta_context *ctx);
+uint32_t ta_context_supports_bda(const ta_context *ctx);
+
+/* ref tensor_ash.h:118-120.  kernel_selection: NULL/"auto" or an
+ * ML_KERNEL name (see ta_kernel_name). */
+ta_executor *ta_executor_create(const ta_context *ctx, size_t n_slots,
+                                uint32_t max_calls_per_submit,
+                                const char *kernel_selection);
+/* ref tensor_ash.h:121-129. */
+ta_executor *ta_executor_create_v2(const ta_context *ctx, size_t n_slots,
+                                   uint32_t max_calls_per_submit,
+                                   const char *kernel_selection,
+                                   uint32_t tune);
+void ta_executor_destroy(ta_executor *exec); /* ref tensor_ash.h:130 */
+
+/* ref tensor_ash.h:132-145. */
+ta_tensor *ta_tensor_create(const ta_context *ctx, const uint32_t *shape,
+                            size_t rank);
+ta_tensor *ta_tensor_create_on_executor(const ta_executor *exec,
+                                        const uint32_t *shape, size_t rank);
+ta_tensor *ta_tensor_create_f16(const ta_context *ctx, const uint32_t *shape,
+                                size_t rank);
+ta_tensor *ta_tensor_create_f16_on_executor(const ta_executor *exec,
+                                            const uint32_t *shape, size_t rank);
+void ta_tensor_destroy(ta_tensor *tensor);          /* ref :146 */
+uint64_t ta_tensor_len(const ta_tensor *tensor);        /* ref :147 */
+uint64_t ta_tensor_size_bytes(const ta_tensor *tensor); /* ref :148 */
+uint32_t ta_tensor_is_f16(const ta_tensor *tensor);     /* ref :149 */
+
+/* ref tensor_ash.h:151-154.  f32 host data; f16 tensors round (RNE) on
+ * upload and widen on download. */
+int ta_upload(const ta_executor *exec, const ta_tensor *dst, const float *src,
+              size_t len);
+int ta_download(const ta_executor *exec, const ta_tensor *src, float *dst,
+                size_t len);
+
+/* ref tensor_ash.h:156-160. */
+int ta_matmul(const ta_executor *exec, const ta_tensor *a, const ta_tensor *b,
+              const ta_tensor *c, float alpha, uint32_t accumulate,
+              ta_run_stats *stats);
+int ta_matmul_batch(const ta_executor *exec, const ta_matmul_call *calls,
+                    size_t n_calls, ta_run_stats *stats);
+
+/* ref tensor_ash.h:162-165: independent ops, one submission. */
+int ta_run_ops(const ta_executor *exec, const ta_matmul_op *ops, size_t n_ops,
+               ta_run_stats *stats);
+/* ref tensor_ash.h:166-170: dependent chain, one submission. */
+int ta_run_op_graph(const ta_executor *exec, const ta_matmul_op *ops,
+                    size_t n_ops, ta_run_stats *stats);
+
+/* ref tensor_ash.h:172-208: model ops.  Outside this build's scope (the
+ * fused-epilogue GEMM path): they validate exec and return -1 with an
+ * "unsupported" error. */
+int ta_softmax_rows(const ta_executor *exec, const ta_tensor *input,
+                    const ta_tensor *output, float scale, uint32_t mask_kind,
+                    uint32_t valid_or_prefix, uint32_t rows_per_group,
+                    ta_run_stats *stats);
+int ta_rms_norm(const ta_executor *exec, const ta_tensor *input,
+                const ta_tensor *weight, const ta_tensor *output, float eps,
+                ta_run_stats *stats);
+int ta_layer_norm(const ta_executor *exec, const ta_tensor *input,
+                  const ta_tensor *weight, const ta_tensor *bias,
+                  const ta_tensor *output, float eps, ta_run_stats *stats);
+int ta_rope(const ta_executor *exec, const ta_tensor *input,
+            const ta_tensor *table, const ta_tensor *output,
+            const ta_rope_desc *desc, ta_run_stats *stats);
+int ta_copy_strided(const ta_executor *exec, const ta_tensor *src,
+                    const ta_tensor *dst, const ta_copy_desc *desc,
+                    ta_run_stats *stats);
+
+/* ref tensor_ash.h:210-233: validate, route and record once (a hipGraph),
+ * replay with one launch per call.  The executor and every tensor must
+ * outlive the handle; destroy waits for in-flight work. */
+ta_prepared *ta_prepared_create(const ta_executor *exec,
+                                const ta_matmul_op *ops, size_t n_ops,
+                                uint32_t as_graph);
+int ta_prepared_run(ta_prepared *prepared, ta_run_stats *stats);
+int ta_prepared_submit(ta_prepared *prepared);
+int ta_prepared_wait(ta_prepared *prepared, ta_run_stats *stats);
+void ta_prepared_destroy(ta_prepared *prepared);
+
+/* ref tensor_ash.h:235-240. */
+int ta_dispatch_info_for(const ta_executor *exec, uint32_t batch, uint32_t m,
+                         uint32_t n, uint32_t k, uint32_t b_f16,
+                         ta_dispatch_info *out);
+/* ref tensor_ash.h:241-244. */
+int ta_tune_shape(const ta_executor *exec, uint32_t batch, uint32_t m,
+                  uint32_t n, uint32_t k);
+
+/* ------------------------------------------------------------------ */
+/* Additive extensions (no reference C symbol; Rust-API counterparts). */
+
+/* Executor::run_matmuls_split_k2 (src/executor/reduction.rs:21-70):
+ * deterministic two-stage split-K.  splits == 0 picks a default;
+ * accumulate is not supported. */
+int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a,
+                       const ta_tensor *b, const ta_tensor *c, float alpha,
+                       uint32_t splits, ta_run_stats *stats);
+
+/* MatmulOp::with_packed_b (src/matmul/api.rs:260-265): B holds the packed
+ * decode layout produced by ta_pack_f16w_row_tiles with
+ * ta_f16w_row_tile_n(K, N).  Packed ops take M <= 8, batch 1, f16 B. */
+typedef struct ta_matmul_op_v2 {
+  ta_matmul_op base;
+  uint32_t packed_b;
+  uint32_t reserved[3]; /* must be zero */
+} ta_matmul_op_v2;
+int ta_run_ops_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops,
+                  size_t n_ops, ta_run_stats *stats);
+int ta_run_op_graph_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops,
+                       size_t n_ops, ta_run_stats *stats);
+ta_prepared *ta_prepared_create_v2(const ta_executor *exec,
+                                   const ta_matmul_op_v2 *ops, size_t n_ops,
+                                   uint32_t as_graph);
+
+/* pack_f16w_row_tiles (src/matmul/api.rs:324-344): row-major [K, N] ->
+ * [N/tile_n][K][tile_n]; dst holds K*N floats. */
+int ta_pack_f16w_row_tiles(const float *src, size_t k, size_t n,
+                           size_t tile_n, float *dst);
+/* f16w_row_tile_n (src/pipeline/routing.rs:17-23): the packing tile the
+ * decode GEMV expects for this shape (64 when N % 64 == 0, else 32). */
+uint32_t ta_f16w_row_tile_n(uint32_t k, uint32_t n);
+
+/* Executor::upload_f16 (src/executor/transfer.rs:41-55): raw binary16
+ * bits into an f16 tensor. */
+int ta_upload_f16(const ta_executor *exec, const ta_tensor *dst,
+                  const uint16_t *src, size_t len);
+
+/* KERNEL_SPECS introspection (src/pipeline/catalog.rs:129-197). */
+size_t ta_kernel_count(void);
+/* Name of registry entry i (NULL past the end); valid for the process. */
+const char *ta_kernel_name(size_t index);
+/* Tile of entry i into tile[3]; -1 past the end. */
+int ta_kernel_tile(size_t index, uint32_t *tile);
+
+/* Device facts for reporting: compute-unit count, or 0 for null. */
+uint32_t ta_context_cu_count(const ta_context *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,174 @@
+"""ctypes binding of the CPU oracle (oracle/oracle.c -> oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() (as the
+checker) and bench.py's cpu_baseline leg (as the timed CPU baseline).  The
+shipped library never loads it.  See oracle.c for what each function restates
+and how it is pinned.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+_SO = Path(__file__).resolve().parent / "liboracle.so"
+if not _SO.exists():
+    raise ImportError(f"{_SO} is missing: build it with `python tensor-ash_amd/build.py`")
+_lib = C.CDLL(str(_SO))
+
+_F = C.POINTER(C.c_float)
+_U16 = C.POINTER(C.c_uint16)
+_U32 = C.POINTER(C.c_uint32)
+
+
+def _sig(name, res, *args):
+    f = getattr(_lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+
+
+_sig("ta_oracle_fill_det", None, _F, C.c_size_t, C.c_uint64)
+_sig("ta_oracle_fill_normal", None, _F, C.c_size_t, C.c_uint64, C.c_float)
+_sig("ta_oracle_lcg_range", C.c_int, C.c_uint64, C.c_uint32, C.c_uint32, _U32, C.c_size_t)
+_sig("ta_oracle_cpu_bmm", C.c_int, _F, C.c_size_t, _F, C.c_size_t, _F, C.c_uint32, C.c_uint32,
+     C.c_uint32, C.c_uint32, C.c_float, C.c_int, _F)
+_sig("ta_oracle_cpu_bmm_rows", C.c_int, _F, C.c_size_t, _F, C.c_size_t, C.c_uint32, C.c_uint32,
+     C.c_uint32, C.c_uint32, C.c_float, _F, C.c_uint64, C.c_uint64, C.c_int)
+_sig("ta_oracle_max_threads", C.c_int)
+_sig("ta_oracle_max_abs_err", C.c_float, _F, _F, C.c_size_t, C.POINTER(C.c_size_t))
+_sig("ta_oracle_tolerance", C.c_float, C.c_uint32)
+_sig("ta_oracle_f32_to_f16", C.c_uint16, C.c_float)
+_sig("ta_oracle_f16_to_f32", C.c_float, C.c_uint16)
+_sig("ta_oracle_f32_to_f16_array", None, _F, _U16, C.c_size_t)
+_sig("ta_oracle_f16_to_f32_array", None, _U16, _F, C.c_size_t)
+_sig("ta_oracle_round_via_f16", None, _F, C.c_size_t)
+_sig("ta_oracle_pack_row_tiles", C.c_int, _F, C.c_size_t, C.c_size_t, C.c_size_t, _F)
+_sig("ta_oracle_epilogue", None, _F, C.c_size_t, C.c_uint32, C.c_size_t, _F, C.c_uint32,
+     C.c_uint32, C.c_uint32, _F, C.c_float)
+_sig("ta_oracle_split_window", None, C.c_uint32, C.c_uint32, C.c_uint32, _U32, _U32)
+
+
+def _f(a: np.ndarray):
+    return a.ctypes.data_as(_F)
+
+
+def _c32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+
+
+def fill_det(n: int, seed: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _lib.ta_oracle_fill_det(_f(out), n, seed)
+    return out
+
+
+def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _lib.ta_oracle_fill_normal(_f(out), n, seed, std)
+    return out
+
+
+def lcg_range(seed: int, lo: int, hi: int, count: int) -> np.ndarray:
+    out = np.empty(count, dtype=np.uint32)
+    if _lib.ta_oracle_lcg_range(seed, lo, hi, out.ctypes.data_as(_U32), count) != 0:
+        raise ValueError(f"LcgRng::range_u32 lo {lo} > hi {hi}")
+    return out
+
+
+def cpu_bmm(a, b, c_init, batch: int, m: int, n: int, k: int, alpha: float = 1.0,
+            accumulate: bool = False) -> np.ndarray:
+    a = _c32(a)
+    b = _c32(b)
+    out = np.empty(batch * m * n, dtype=np.float32)
+    cp = None
+    if c_init is not None:
+        c_init = _c32(c_init)
+        if c_init.size != out.size:
+            raise ValueError("cpu_bmm: C init has wrong length")
+        cp = _f(c_init)
+    rc = _lib.ta_oracle_cpu_bmm(_f(a), a.size, _f(b), b.size, cp, batch, m, n, k, alpha,
+                                int(accumulate), _f(out))
+    if rc != 0:
+        raise ValueError("cpu_bmm: A/B length matches neither broadcast nor batched")
+    return out
+
+
+def cpu_bmm_rows(a, b, batch, m, n, k, alpha, out, row_begin, row_end, threads=0) -> None:
+    rc = _lib.ta_oracle_cpu_bmm_rows(_f(a), a.size, _f(b), b.size, batch, m, n, k, alpha, _f(out),
+                                     row_begin, row_end, threads)
+    if rc != 0:
+        raise ValueError("cpu_bmm_rows: bad shapes")
+
+
+def max_threads() -> int:
+    return int(_lib.ta_oracle_max_threads())
+
+
+def max_abs_err(a, b):
+    a = _c32(a)
+    b = _c32(b)
+    if a.size != b.size:
+        raise ValueError("max_abs_err: slice lengths differ")
+    idx = C.c_size_t(0)
+    e = _lib.ta_oracle_max_abs_err(_f(a), _f(b), a.size, C.byref(idx))
+    return float(e), int(idx.value)
+
+
+def tolerance(k: int) -> float:
+    return float(_lib.ta_oracle_tolerance(k))
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = _c32(x)
+    out = np.empty(x.size, dtype=np.uint16)
+    _lib.ta_oracle_f32_to_f16_array(_f(x), out.ctypes.data_as(_U16), x.size)
+    return out
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16).reshape(-1)
+    out = np.empty(h.size, dtype=np.float32)
+    _lib.ta_oracle_f16_to_f32_array(h.ctypes.data_as(_U16), _f(out), h.size)
+    return out
+
+
+def round_via_f16(x) -> np.ndarray:
+    out = _c32(x).copy()
+    _lib.ta_oracle_round_via_f16(_f(out), out.size)
+    return out
+
+
+def pack_row_tiles(src, k: int, n: int, tile: int) -> np.ndarray:
+    src = _c32(src)
+    out = np.empty_like(src)
+    if _lib.ta_oracle_pack_row_tiles(_f(src), k, n, tile, _f(out)) != 0:
+        raise ValueError(f"N={n} is not a multiple of tile_n={tile}")
+    return out
+
+
+def epilogue(c, n: int, mn: int, bias=None, bias_batch_stride: int = 0, act: int = 0,
+             binary: int = 0, d=None, beta: float = 0.0) -> np.ndarray:
+    out = _c32(c).copy()
+    bias_p = _f(_c32(bias)) if bias is not None else None
+    bias_keep = _c32(bias) if bias is not None else None
+    if bias_keep is not None:
+        bias_p = _f(bias_keep)
+    d_keep = _c32(d) if d is not None else None
+    _lib.ta_oracle_epilogue(_f(out), out.size, n, mn, bias_p, bias_batch_stride, act, binary,
+                            _f(d_keep) if d_keep is not None else None, beta)
+    return out
+
+
+def split_window(k: int, splits: int, s: int):
+    lo, hi = C.c_uint32(0), C.c_uint32(0)
+    _lib.ta_oracle_split_window(k, splits, s, C.byref(lo), C.byref(hi))
+    return lo.value, hi.value
+
+
+def reference_gemm(a, b, batch, m, n, k, alpha=1.0, c_init=None, accumulate=False, bias=None,
+                   bias_batch_stride=0, act=0, binary=0, d=None, beta=0.0) -> np.ndarray:
+    """cpu_bmm followed by the f64 epilogue: the full fused-op reference."""
+    c = cpu_bmm(a, b, c_init, batch, m, n, k, alpha, accumulate)
+    return epilogue(c, n, m * n, bias, bias_batch_stride, act, binary, d, beta)

@@ -1,0 +1,99 @@
+// Kernel argument blocks shared by the host runtime and the gfx950 code
+// objects.  Every kernel takes exactly one of these structs by value; the
+// host passes it through hipModuleLaunchKernel's kernelParams.  Plain C
+// layout: no pointers to host memory, no torch or HIP types.
+//
+// The fields play the role of the reference's 144-byte push-constant block
+// (src/pipeline/abi.rs:15-53), laid out for HIP kernargs: 64-bit element
+// strides instead of u32 so batched planes past 4 GiB need no special path.
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Epilogue flag bits (GemmArgs.flags / GemvArgs.flags).
+enum {
+  TA_FLAG_ACCUMULATE = 1u << 0, // v += C_old (after alpha)
+  TA_FLAG_BIAS = 1u << 1,       // v += bias[batch * bias_batch_stride + col]
+  TA_GEMV_PACKED = 1u << 2,     // GEMV weights in the [N/TW][K][TW] layout
+};
+
+// Activation codes (shaders/matmul_epilogue_common.glsl:24-26 numbering).
+enum { TA_ACT_NONE = 0, TA_ACT_RELU = 1, TA_ACT_SILU = 2, TA_ACT_GELU = 3 };
+// Binary codes: 1 = += beta * D, 2 = *= D.
+enum { TA_BIN_NONE = 0, TA_BIN_ADD_SCALED = 1, TA_BIN_MUL = 2 };
+
+// Dense GEMM: C[b] = epilogue(alpha * A[b] @ B[b] (+ C[b])).
+// A is [M, K] row-major, B is [K, N] row-major (f32 or f16 storage),
+// C and D are [M, N] row-major f32.  A stride of 0 broadcasts one plane.
+// Split-K stage 1 (num_splits > 1): grid.z = batch * num_splits, split s
+// of batch b owns its K window and stores alpha * partial to plane
+// (b * num_splits + s) of `c` (the scratch), with no epilogue.
+typedef struct GemmArgs {
+  const void *a;
+  const void *b;
+  float *c;
+  const float *d;
+  const float *bias;
+  uint64_t stride_a; // elements between batch planes (0 = broadcast)
+  uint64_t stride_b;
+  uint64_t stride_c;
+  uint32_t m, n, k;
+  uint32_t flags;
+  uint32_t act;
+  uint32_t binary;
+  uint32_t bias_batch_stride; // 0 for [N] bias, N for [B, N]
+  uint32_t num_splits;        // 1 = plain GEMM
+  float alpha;
+  float beta;
+  uint32_t tiles_n; // ceil(N / BN): for the blockIdx -> tile remap
+  uint32_t tiles_m; // ceil(M / BM)
+} GemmArgs;
+
+// Fixed-order reduction of split-K partial planes:
+// C[b][e] = sum_{s=0}^{S-1} scratch[(b * S + s) * mn + e].
+typedef struct SplitReduceArgs {
+  const float *scratch;
+  float *c;
+  uint64_t total; // batch * mn
+  uint64_t mn;
+  uint32_t num_splits;
+  uint32_t pad;
+} SplitReduceArgs;
+
+// Decode GEMV over packed f16 weights W[N/64][K][64]:
+// Y[m, :] = epilogue(alpha * X[m, :] @ W) for m < rows (rows <= 8).
+// With `w2` set (dual mode) the same launch also computes
+// U = X @ W2 and stores U to `y2` and Y = act(X @ W) * U to `y`
+// (SwiGLU gating); then `binary` must be TA_BIN_NONE.
+// K is cut into `kchunks` windows of `kchunk` rows; every (tile, chunk)
+// workgroup writes its partial to `partial`, and the last workgroup of a
+// tile to finish (counted in `counters[tile]`) sums the chunks in chunk
+// order and applies the epilogue.  The counter is reset by that
+// workgroup, so the buffer stays zero between launches.
+typedef struct GemvArgs {
+  const float *x; // [rows, K] f32
+  const uint16_t *w;
+  const uint16_t *w2;
+  float *y;  // [rows, N]
+  float *y2; // dual mode only
+  const float *d;
+  const float *bias;
+  float *partial;     // [kchunks][tiles][ways][rows][64]
+  uint32_t *counters; // [tiles]
+  uint32_t rows, n, k;
+  uint32_t kchunk;
+  uint32_t kchunks;
+  uint32_t flags;
+  uint32_t act;
+  uint32_t binary;
+  float alpha;
+  float beta;
+  uint32_t pad0, pad1;
+} GemvArgs;
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,487 @@
+// The C ABI of include/tensor_ash.h over the C++ runtime.
+// Conventions of the reference capi crate (capi/src/error.rs:8-121,
+// capi/src/handles.rs): 0 / -1 / NULL returns, a thread-local error
+// string cleared at every call, no exception crosses the boundary,
+// destroying NULL is a no-op, "<fn>: <arg> is null" messages.
+#include <cstring>
+#include <functional>
+
+#include "../../../include/tensor_ash.h"
+#include "internal.hpp"
+
+using namespace tensor_ash;
+
+struct ta_context {
+  std::shared_ptr<Context> ctx;
+};
+struct ta_executor {
+  std::shared_ptr<Context> ctx;
+  std::unique_ptr<Executor> exec;
+};
+struct ta_tensor {
+  std::shared_ptr<Context> ctx;
+  Tensor tensor;
+};
+struct ta_prepared {
+  std::unique_ptr<PreparedOps> prepared;
+  std::shared_ptr<Context> ctx;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+void set_error(const std::string &e) { g_last_error = e; }
+
+int ffi_status(const std::function<void()> &f) {
+  g_last_error.clear();
+  try {
+    f();
+    return 0;
+  } catch (const std::exception &e) {
+    set_error(e.what());
+  } catch (...) {
+    set_error("panic crossed tensor-ash C ABI boundary");
+  }
+  return -1;
+}
+
+template <typename T> T *ffi_create(const std::function<T *()> &f) {
+  g_last_error.clear();
+  try {
+    return f();
+  } catch (const std::exception &e) {
+    set_error(e.what());
+  } catch (...) {
+    set_error("panic crossed tensor-ash C ABI boundary");
+  }
+  return nullptr;
+}
+
+template <typename T> const T &checked_ref(const T *p, const std::string &msg) {
+  if (!p)
+    fail(msg);
+  return *p;
+}
+
+std::string opt_str(const char *p, const char *dflt) { return p ? std::string(p) : dflt; }
+
+const Tensor *checked_tensor(const ta_executor &e, const ta_tensor *t, const std::string &op,
+                             const char *operand) {
+  if (!t)
+    fail(op + ": " + operand + " is null");
+  if (t->ctx != e.ctx)
+    fail(op + ": " + operand + " belongs to a different HIP context");
+  return &t->tensor;
+}
+
+MatmulCall checked_call(const ta_executor &e, const ta_matmul_call &raw, const std::string &op) {
+  MatmulCall c;
+  c.a = checked_tensor(e, raw.a, op, "a");
+  c.b = checked_tensor(e, raw.b, op, "b");
+  c.c = checked_tensor(e, raw.c, op, "c");
+  c.alpha = raw.alpha;
+  c.accumulate = raw.accumulate != 0;
+  return c;
+}
+
+// capi/src/api/ops.rs:15-71.
+MatmulOp checked_op(const ta_executor &e, const ta_matmul_op &raw, const std::string &op) {
+  MatmulOp o(checked_call(e, raw.call, op));
+  const ta_epilogue &ep = raw.epilogue;
+  if (ep.bias)
+    o.epilogue.bias = checked_tensor(e, ep.bias, op, "epilogue.bias");
+  if (ep.activation > 3)
+    fail(op + ": epilogue.activation " + std::to_string(ep.activation) +
+         " is invalid (0=none 1=relu 2=silu 3=gelu)");
+  o.epilogue.activation = (Activation)ep.activation;
+  switch (ep.binary_kind) {
+  case 0:
+    if (ep.d)
+      fail(op + ": epilogue.d is set but binary_kind is 0 (none)");
+    break;
+  case 1:
+    o.epilogue.binary = EpilogueBinary::add_scaled(*checked_tensor(e, ep.d, op, "epilogue.d"),
+                                                   ep.beta);
+    break;
+  case 2:
+    o.epilogue.binary = EpilogueBinary::mul(*checked_tensor(e, ep.d, op, "epilogue.d"));
+    break;
+  default:
+    fail(op + ": epilogue.binary_kind " + std::to_string(ep.binary_kind) +
+         " is invalid (0=none 1=add_scaled 2=mul)");
+  }
+  return o;
+}
+
+std::vector<MatmulOp> checked_ops(const ta_executor &e, const ta_matmul_op *ops, size_t n,
+                                  const std::string &op) {
+  if (n > 0 && !ops)
+    fail(op + ": ops is null");
+  std::vector<MatmulOp> out;
+  for (size_t i = 0; i < n; ++i)
+    out.push_back(checked_op(e, ops[i], op + ": op " + std::to_string(i)));
+  return out;
+}
+
+std::vector<MatmulOp> checked_ops_v2(const ta_executor &e, const ta_matmul_op_v2 *ops, size_t n,
+                                     const std::string &op) {
+  if (n > 0 && !ops)
+    fail(op + ": ops is null");
+  std::vector<MatmulOp> out;
+  for (size_t i = 0; i < n; ++i) {
+    const std::string where = op + ": op " + std::to_string(i);
+    if (ops[i].reserved[0] || ops[i].reserved[1] || ops[i].reserved[2])
+      fail(where + ": reserved fields must be zero");
+    MatmulOp o = checked_op(e, ops[i].base, where);
+    o.packed_b = ops[i].packed_b != 0;
+    out.push_back(o);
+  }
+  return out;
+}
+
+// capi/src/api/matmul.rs:86-103.
+void write_stats(ta_run_stats *out, const RunStats &s) {
+  if (!out)
+    return;
+  out->has_gpu_time = s.gpu_time_ns ? 1 : 0;
+  out->gpu_time_ns = s.gpu_time_ns.value_or(0);
+  out->n_calls = s.n_calls;
+  out->total_flops = s.total_flops;
+  out->tflops = s.tflops().value_or(__builtin_nan(""));
+}
+
+std::vector<uint32_t> checked_shape(const uint32_t *shape, size_t rank, const std::string &op) {
+  if (rank > 0 && !shape)
+    fail(op + ": shape is null");
+  return std::vector<uint32_t>(shape, shape + rank);
+}
+
+template <typename T> void destroy_handle(T *p) {
+  if (!p)
+    return;
+  g_last_error.clear();
+  try {
+    delete p;
+  } catch (...) {
+    set_error("panic crossed tensor-ash C ABI boundary");
+  }
+}
+
+int unsupported(const ta_executor *exec, const char *fn) {
+  return ffi_status([&] {
+    checked_ref(exec, std::string(fn) + ": exec is null");
+    fail(std::string(fn) +
+         ": unsupported: model ops are outside this build's fused-epilogue GEMM path");
+  });
+}
+
+} // namespace
+
+extern "C" {
+
+const char *ta_version(void) { return "2.0.0-gfx950"; }
+const char *ta_last_error(void) { return g_last_error.c_str(); }
+
+ta_context *ta_context_create(uint32_t enable_validation, const char *device_preference) {
+  return ffi_create<ta_context>([&] {
+    auto ctx = Context::create(enable_validation != 0, opt_str(device_preference, "auto"));
+    return new ta_context{ctx};
+  });
+}
+
+void ta_context_destroy(ta_context *ctx) { destroy_handle(ctx); }
+
+uint32_t ta_context_supports_f16(const ta_context *ctx) { return ctx ? 1u : 0u; }
+uint32_t ta_context_supports_bda(const ta_context *ctx) { return ctx ? 1u : 0u; }
+uint32_t ta_context_cu_count(const ta_context *ctx) { return ctx ? ctx->ctx->cu_count() : 0u; }
+
+static ta_executor *make_executor(const ta_context *ctx, size_t n_slots, uint32_t max_calls,
+                                  const char *sel, std::optional<bool> tune, const char *fn) {
+  return ffi_create<ta_executor>([&] {
+    const ta_context &c = checked_ref(ctx, std::string(fn) + ": ctx is null");
+    KernelSelection s = KernelSelection::parse(opt_str(sel, "auto"));
+    std::unique_ptr<Executor> e;
+    if (tune)
+      e.reset(new Executor(c.ctx, s, ExecutorConfig{n_slots, max_calls, *tune}));
+    else
+      e.reset(new Executor(c.ctx, s, n_slots, max_calls));
+    return new ta_executor{c.ctx, std::move(e)};
+  });
+}
+
+ta_executor *ta_executor_create(const ta_context *ctx, size_t n_slots,
+                                uint32_t max_calls_per_submit, const char *kernel_selection) {
+  return make_executor(ctx, n_slots, max_calls_per_submit, kernel_selection, std::nullopt,
+                       "ta_executor_create");
+}
+
+ta_executor *ta_executor_create_v2(const ta_context *ctx, size_t n_slots,
+                                   uint32_t max_calls_per_submit, const char *kernel_selection,
+                                   uint32_t tune) {
+  return make_executor(ctx, n_slots, max_calls_per_submit, kernel_selection, tune != 0,
+                       "ta_executor_create_v2");
+}
+
+void ta_executor_destroy(ta_executor *exec) { destroy_handle(exec); }
+
+static ta_tensor *make_tensor(const std::shared_ptr<Context> &ctx, const uint32_t *shape,
+                              size_t rank, bool f16, const std::string &fn) {
+  auto s = checked_shape(shape, rank, fn);
+  Tensor t = f16 ? Tensor::uninit_device_f16(ctx, s) : Tensor::uninit_device(ctx, s);
+  return new ta_tensor{ctx, t};
+}
+
+ta_tensor *ta_tensor_create(const ta_context *ctx, const uint32_t *shape, size_t rank) {
+  return ffi_create<ta_tensor>([&] {
+    const ta_context &c = checked_ref(ctx, "ta_tensor_create: ctx is null");
+    return make_tensor(c.ctx, shape, rank, false, "ta_tensor_create");
+  });
+}
+ta_tensor *ta_tensor_create_on_executor(const ta_executor *exec, const uint32_t *shape,
+                                        size_t rank) {
+  return ffi_create<ta_tensor>([&] {
+    const ta_executor &e = checked_ref(exec, "ta_tensor_create_on_executor: exec is null");
+    return make_tensor(e.ctx, shape, rank, false, "ta_tensor_create_on_executor");
+  });
+}
+ta_tensor *ta_tensor_create_f16(const ta_context *ctx, const uint32_t *shape, size_t rank) {
+  return ffi_create<ta_tensor>([&] {
+    const ta_context &c = checked_ref(ctx, "ta_tensor_create_f16: ctx is null");
+    return make_tensor(c.ctx, shape, rank, true, "ta_tensor_create_f16");
+  });
+}
+ta_tensor *ta_tensor_create_f16_on_executor(const ta_executor *exec, const uint32_t *shape,
+                                            size_t rank) {
+  return ffi_create<ta_tensor>([&] {
+    const ta_executor &e = checked_ref(exec, "ta_tensor_create_f16_on_executor: exec is null");
+    return make_tensor(e.ctx, shape, rank, true, "ta_tensor_create_f16_on_executor");
+  });
+}
+
+void ta_tensor_destroy(ta_tensor *t) { destroy_handle(t); }
+uint64_t ta_tensor_len(const ta_tensor *t) { return t ? t->tensor.len() : 0; }
+uint64_t ta_tensor_size_bytes(const ta_tensor *t) { return t ? t->tensor.size_bytes() : 0; }
+uint32_t ta_tensor_is_f16(const ta_tensor *t) {
+  return t && t->tensor.dtype() == DType::F16 ? 1u : 0u;
+}
+
+int ta_upload(const ta_executor *exec, const ta_tensor *dst, const float *src, size_t len) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_upload: exec is null");
+    const Tensor *t = checked_tensor(e, dst, "ta_upload", "dst");
+    if (len > 0 && !src)
+      fail("ta_upload: src is null");
+    e.exec->upload(src, len, *t);
+  });
+}
+
+int ta_upload_f16(const ta_executor *exec, const ta_tensor *dst, const uint16_t *src, size_t len) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_upload_f16: exec is null");
+    const Tensor *t = checked_tensor(e, dst, "ta_upload_f16", "dst");
+    if (len > 0 && !src)
+      fail("ta_upload_f16: src is null");
+    e.exec->upload_f16(src, len, *t);
+  });
+}
+
+int ta_download(const ta_executor *exec, const ta_tensor *src, float *dst, size_t len) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_download: exec is null");
+    const Tensor *t = checked_tensor(e, src, "ta_download", "src");
+    if (len > 0 && !dst)
+      fail("ta_download: dst is null");
+    e.exec->download(*t, dst, len);
+  });
+}
+
+int ta_matmul(const ta_executor *exec, const ta_tensor *a, const ta_tensor *b,
+              const ta_tensor *c, float alpha, uint32_t accumulate, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_matmul: exec is null");
+    ta_matmul_call raw{a, b, c, alpha, accumulate};
+    write_stats(stats, e.exec->run_matmuls({checked_call(e, raw, "ta_matmul")}));
+  });
+}
+
+int ta_matmul_batch(const ta_executor *exec, const ta_matmul_call *calls, size_t n_calls,
+                    ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_matmul_batch: exec is null");
+    if (n_calls > 0 && !calls)
+      fail("ta_matmul_batch: calls is null");
+    std::vector<MatmulCall> cs;
+    for (size_t i = 0; i < n_calls; ++i)
+      cs.push_back(checked_call(e, calls[i], "ta_matmul_batch: call " + std::to_string(i)));
+    write_stats(stats, e.exec->run_matmuls(cs));
+  });
+}
+
+int ta_run_ops(const ta_executor *exec, const ta_matmul_op *ops, size_t n_ops,
+               ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_ops: exec is null");
+    write_stats(stats, e.exec->run_ops(checked_ops(e, ops, n_ops, "ta_run_ops")));
+  });
+}
+
+int ta_run_op_graph(const ta_executor *exec, const ta_matmul_op *ops, size_t n_ops,
+                    ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_op_graph: exec is null");
+    write_stats(stats, e.exec->run_op_graph(checked_ops(e, ops, n_ops, "ta_run_op_graph")));
+  });
+}
+
+int ta_run_ops_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops, size_t n_ops,
+                  ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_ops_v2: exec is null");
+    write_stats(stats, e.exec->run_ops(checked_ops_v2(e, ops, n_ops, "ta_run_ops_v2")));
+  });
+}
+
+int ta_run_op_graph_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops, size_t n_ops,
+                       ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_op_graph_v2: exec is null");
+    write_stats(stats,
+                e.exec->run_op_graph(checked_ops_v2(e, ops, n_ops, "ta_run_op_graph_v2")));
+  });
+}
+
+int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a, const ta_tensor *b,
+                       const ta_tensor *c, float alpha, uint32_t splits, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_matmul_split_k2: exec is null");
+    ta_matmul_call raw{a, b, c, alpha, 0};
+    write_stats(stats,
+                e.exec->run_matmuls_split_k2(checked_call(e, raw, "ta_matmul_split_k2"), splits));
+  });
+}
+
+int ta_softmax_rows(const ta_executor *exec, const ta_tensor *, const ta_tensor *, float, uint32_t,
+                    uint32_t, uint32_t, ta_run_stats *) {
+  return unsupported(exec, "ta_softmax_rows");
+}
+int ta_rms_norm(const ta_executor *exec, const ta_tensor *, const ta_tensor *, const ta_tensor *,
+                float, ta_run_stats *) {
+  return unsupported(exec, "ta_rms_norm");
+}
+int ta_layer_norm(const ta_executor *exec, const ta_tensor *, const ta_tensor *, const ta_tensor *,
+                  const ta_tensor *, float, ta_run_stats *) {
+  return unsupported(exec, "ta_layer_norm");
+}
+int ta_rope(const ta_executor *exec, const ta_tensor *, const ta_tensor *, const ta_tensor *,
+            const ta_rope_desc *, ta_run_stats *) {
+  return unsupported(exec, "ta_rope");
+}
+int ta_copy_strided(const ta_executor *exec, const ta_tensor *, const ta_tensor *,
+                    const ta_copy_desc *, ta_run_stats *) {
+  return unsupported(exec, "ta_copy_strided");
+}
+
+static ta_prepared *make_prepared(const ta_executor *exec, std::vector<MatmulOp> (*conv)(
+                                                                const ta_executor &, const void *,
+                                                                size_t, const std::string &),
+                                  const void *ops, size_t n_ops, uint32_t as_graph,
+                                  const char *fn) {
+  return ffi_create<ta_prepared>([&] {
+    const ta_executor &e = checked_ref(exec, std::string(fn) + ": exec is null");
+    auto v = conv(e, ops, n_ops, fn);
+    auto p = as_graph ? e.exec->prepare_op_graph(v) : e.exec->prepare_ops(v);
+    return new ta_prepared{std::move(p), e.ctx};
+  });
+}
+
+ta_prepared *ta_prepared_create(const ta_executor *exec, const ta_matmul_op *ops, size_t n_ops,
+                                uint32_t as_graph) {
+  return make_prepared(
+      exec,
+      [](const ta_executor &e, const void *o, size_t n, const std::string &fn) {
+        return checked_ops(e, static_cast<const ta_matmul_op *>(o), n, fn);
+      },
+      ops, n_ops, as_graph, "ta_prepared_create");
+}
+
+ta_prepared *ta_prepared_create_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops,
+                                   size_t n_ops, uint32_t as_graph) {
+  return make_prepared(
+      exec,
+      [](const ta_executor &e, const void *o, size_t n, const std::string &fn) {
+        return checked_ops_v2(e, static_cast<const ta_matmul_op_v2 *>(o), n, fn);
+      },
+      ops, n_ops, as_graph, "ta_prepared_create_v2");
+}
+
+int ta_prepared_run(ta_prepared *prepared, ta_run_stats *stats) {
+  return ffi_status([&] {
+    if (!prepared)
+      fail("ta_prepared_run: prepared is null");
+    write_stats(stats, prepared->prepared->run());
+  });
+}
+int ta_prepared_submit(ta_prepared *prepared) {
+  return ffi_status([&] {
+    if (!prepared)
+      fail("ta_prepared_submit: prepared is null");
+    prepared->prepared->submit();
+  });
+}
+int ta_prepared_wait(ta_prepared *prepared, ta_run_stats *stats) {
+  return ffi_status([&] {
+    if (!prepared)
+      fail("ta_prepared_wait: prepared is null");
+    write_stats(stats, prepared->prepared->wait());
+  });
+}
+void ta_prepared_destroy(ta_prepared *prepared) { destroy_handle(prepared); }
+
+int ta_dispatch_info_for(const ta_executor *exec, uint32_t batch, uint32_t m, uint32_t n,
+                         uint32_t k, uint32_t b_f16, ta_dispatch_info *out) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_dispatch_info_for: exec is null");
+    if (!out)
+      fail("ta_dispatch_info_for: out is null");
+    DispatchInfo info = e.exec->dispatch_info_for(batch, m, n, k, b_f16 != 0);
+    out->kernel = info.kernel; // registry names are static strings
+    out->tile[0] = info.tile[0];
+    out->tile[1] = info.tile[1];
+    out->tile[2] = info.tile[2];
+    out->has_split_k2 = info.split_k2_splits ? 1u : 0u;
+    out->split_k2_splits = info.split_k2_splits.value_or(0);
+  });
+}
+
+int ta_tune_shape(const ta_executor *exec, uint32_t batch, uint32_t m, uint32_t n, uint32_t k) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_tune_shape: exec is null");
+    e.exec->tune_shape(batch, m, n, k);
+  });
+}
+
+int ta_pack_f16w_row_tiles(const float *src, size_t k, size_t n, size_t tile_n, float *dst) {
+  return ffi_status([&] {
+    if (k * n > 0 && (!src || !dst))
+      fail("ta_pack_f16w_row_tiles: src or dst is null");
+    auto v = pack_f16w_row_tiles(src, k, n, tile_n);
+    if (!v.empty())
+      std::memcpy(dst, v.data(), v.size() * sizeof(float));
+  });
+}
+
+uint32_t ta_f16w_row_tile_n(uint32_t k, uint32_t n) { return f16w_row_tile_n(k, n); }
+
+size_t ta_kernel_count(void) { return KERNEL_SPECS_LEN; }
+const char *ta_kernel_name(size_t i) { return i < KERNEL_SPECS_LEN ? KERNEL_SPECS[i].name : nullptr; }
+int ta_kernel_tile(size_t i, uint32_t *tile) {
+  if (i >= KERNEL_SPECS_LEN || !tile)
+    return -1;
+  tile[0] = KERNEL_SPECS[i].tile_m;
+  tile[1] = KERNEL_SPECS[i].tile_n;
+  tile[2] = KERNEL_SPECS[i].tile_k;
+  return 0;
+}
+
+} // extern "C"

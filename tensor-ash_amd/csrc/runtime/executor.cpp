@@ -1,0 +1,928 @@
+// Executor: validation -> routing -> HIP launches on a slot's stream.
+//
+// Replaces src/executor/{mod,dispatch,validation,recording,splitk2,
+// reduction,tuning,prepared,submission,slot,transfer}.rs.  Vulkan command
+// buffers, fences and timestamp queries become a HIP stream per slot,
+// hipEvents and, for prepared replay, an instantiated hipGraph.  Stream
+// order already serialises the ops of one submission, which is exactly
+// the hazard rule of run_op_graph (recording/graph.rs:40-137): a later op
+// sees every earlier op's writes.
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <condition_variable>
+#include <cstdio>
+#include <cstdlib>
+#include <deque>
+#include <fstream>
+#include <sstream>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "internal.hpp"
+
+namespace tensor_ash {
+
+namespace {
+
+uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// Device scratch owned by a slot or by a prepared graph.  Ops of one
+// submission run in stream order, so they can share one region.
+struct Scratch {
+  void *splitk = nullptr;
+  uint64_t splitk_bytes = 0;
+  void *partial = nullptr;
+  uint64_t partial_bytes = 0;
+  uint32_t *counters = nullptr;
+  uint64_t counters_len = 0;
+
+  void release() {
+    if (splitk)
+      (void)hipFree(splitk);
+    if (partial)
+      (void)hipFree(partial);
+    if (counters)
+      (void)hipFree(counters);
+    splitk = partial = nullptr;
+    counters = nullptr;
+    splitk_bytes = partial_bytes = counters_len = 0;
+  }
+  // Grow to at least the given sizes.  Counters start at zero (the GEMV
+  // kernels reset them themselves after use).
+  void ensure(uint64_t sk_bytes, uint64_t part_bytes, uint64_t n_counters) {
+    if (sk_bytes > splitk_bytes) {
+      if (splitk)
+        hip_check(hipFree(splitk), "hipFree");
+      splitk = nullptr;
+      hip_check(hipMalloc(&splitk, sk_bytes), "hipMalloc (split-K scratch)");
+      splitk_bytes = sk_bytes;
+    }
+    if (part_bytes > partial_bytes) {
+      if (partial)
+        hip_check(hipFree(partial), "hipFree");
+      partial = nullptr;
+      hip_check(hipMalloc(&partial, part_bytes), "hipMalloc (GEMV partials)");
+      partial_bytes = part_bytes;
+    }
+    if (n_counters > counters_len) {
+      if (counters)
+        hip_check(hipFree(counters), "hipFree");
+      counters = nullptr;
+      hip_check(hipMalloc(reinterpret_cast<void **>(&counters), n_counters * 4),
+                "hipMalloc (GEMV counters)");
+      hip_check(hipMemset(counters, 0, n_counters * 4), "hipMemset (GEMV counters)");
+      counters_len = n_counters;
+    }
+  }
+};
+
+struct Slot {
+  hipStream_t stream = nullptr;
+  hipEvent_t start = nullptr, end = nullptr;
+  Scratch scratch;
+};
+
+// Complete route for one op (src/executor/mod.rs:125-139).
+struct OpPlan {
+  size_t kernel = 0;
+  std::optional<uint32_t> splitk2;
+  // Launch role: 0 = normal, 1 = fused into the next op's dual GEMV,
+  // 2 = dual GEMV that also produces the previous op's output.
+  int role = 0;
+};
+
+uint32_t gemm_threads(const KernelSpec &s) { return s.tile_m == 256 && s.tile_n == 256 ? 512 : 256; }
+
+struct ScratchNeed {
+  uint64_t splitk = 0, partial = 0, counters = 0;
+  void merge(const ScratchNeed &o) {
+    splitk = std::max(splitk, o.splitk);
+    partial = std::max(partial, o.partial);
+    counters = std::max(counters, o.counters);
+  }
+};
+
+} // namespace
+
+struct ExecutorImpl {
+  std::shared_ptr<Context> ctx;
+  KernelSelection selection;
+  ExecutorConfig config;
+  std::mutex slots_mu;
+  std::condition_variable slot_cv;
+  std::deque<Slot *> free_slots;
+  std::vector<Slot *> all_slots;
+
+  mutable std::mutex tuned_mu;
+  std::map<TuneKey, TuneEntry> tuned;
+  std::string header;
+
+  // ---- slots (src/executor/submission.rs:37-55) ----
+  Slot *checkout() {
+    std::unique_lock<std::mutex> lock(slots_mu);
+    slot_cv.wait(lock, [&] { return !free_slots.empty(); });
+    Slot *s = free_slots.front();
+    free_slots.pop_front();
+    return s;
+  }
+  void give_back(Slot *s) {
+    {
+      std::lock_guard<std::mutex> lock(slots_mu);
+      free_slots.push_back(s);
+    }
+    slot_cv.notify_one();
+  }
+  struct Lease {
+    ExecutorImpl *e;
+    Slot *s;
+    explicit Lease(ExecutorImpl *ex) : e(ex), s(ex->checkout()) {}
+    ~Lease() { e->give_back(s); }
+  };
+
+  // ---- validation (src/executor/validation.rs) ----
+  void validate_tensor(const Tensor *t, const char *role) const {
+    if (!t)
+      fail(std::string(role) + " tensor is null");
+    if (!t->belongs_to(ctx.get()))
+      fail(std::string(role) + " tensor belongs to a different HIP context");
+  }
+  void validate_call(const MatmulCall &c) const {
+    validate_tensor(c.a, "A");
+    validate_tensor(c.b, "B");
+    validate_tensor(c.c, "C");
+    if (c.c->buffer_id() == c.a->buffer_id() || c.c->buffer_id() == c.b->buffer_id())
+      fail("C must not alias A or B; in-place matmul is not supported");
+  }
+  void validate_op(const MatmulOp &op) const {
+    validate_call(op.call);
+    if (op.epilogue.bias)
+      validate_tensor(op.epilogue.bias, "bias");
+    if (op.epilogue.binary.kind != EpilogueBinary::Kind::None)
+      validate_tensor(op.epilogue.binary.d, "D");
+  }
+
+  // ---- routing (src/pipeline/mod.rs:259-288, executor/mod.rs:179-315) ----
+  std::optional<TuneEntry> tuned_entry(const TuneKey &key) const {
+    std::lock_guard<std::mutex> lock(tuned_mu);
+    auto it = tuned.find(key);
+    if (it == tuned.end())
+      return std::nullopt;
+    return it->second;
+  }
+
+  OpPlan plan_shape(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, bool b_f16,
+                    bool splitk_eligible) const {
+    OpPlan plan;
+    std::optional<std::optional<uint32_t>> tuned_splits;
+    if (selection.index) {
+      plan.kernel = *selection.index;
+    } else if (auto e = tuned_entry(TuneKey{batch, m, n, k, b_f16})) {
+      plan.kernel = e->kernel;
+      tuned_splits = e->splitk2_splits;
+    } else {
+      plan.kernel = heuristic_kernel_index(ctx->cu_count(), batch, m, n, k, b_f16, false);
+    }
+    if (splitk_eligible && !b_f16 && selection.is_auto()) {
+      std::optional<uint32_t> splits =
+          tuned_splits ? *tuned_splits : heuristic_splits(ctx->cu_count(), batch, m, n, k);
+      if (splits && auto_route_fits(batch, m, n, k, *splits))
+        plan.splitk2 = splits;
+    }
+    return plan;
+  }
+
+  OpPlan plan_matmul(const ResolvedMatmul &d, bool splitk_eligible) const {
+    if (d.packed_b) {
+      OpPlan p;
+      p.kernel = heuristic_kernel_index(ctx->cu_count(), d.batch, d.m, d.n, d.k, true, true);
+      return p;
+    }
+    if (d.a_f16)
+      fail("matmul with f16 A storage is not supported by this build's kernels yet");
+    return plan_shape(d.batch, d.m, d.n, d.k, d.b_f16, splitk_eligible);
+  }
+
+  // ---- launches ----
+  void launch(const std::string &symbol, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t threads,
+              void *args, hipStream_t stream) const {
+    hipFunction_t f = static_cast<hipFunction_t>(ctx->function(symbol));
+    void *params[] = {args};
+    hip_check(hipModuleLaunchKernel(f, gx, gy, gz, threads, 1, 1, 0, stream, params, nullptr),
+              ("launch " + symbol).c_str());
+  }
+
+  ScratchNeed scratch_need(const ResolvedMatmul &d, const OpPlan &p) const {
+    ScratchNeed need;
+    const KernelSpec &s = KERNEL_SPECS[p.kernel];
+    if (p.splitk2) {
+      need.splitk = (uint64_t)d.batch * d.m * d.n * *p.splitk2 * 4;
+    } else if (s.is_gemv()) {
+      GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, p.role == 2);
+      need.partial = g.partial_bytes;
+      need.counters = g.tiles;
+    }
+    return need;
+  }
+
+  void launch_gemm(const KernelSpec &s, const ResolvedMatmul &d, const MatmulOp &op,
+                   uint32_t splits, void *splitk_scratch, hipStream_t stream) const {
+    GemmArgs a{};
+    a.a = op.call.a->device_ptr();
+    a.b = op.call.b->device_ptr();
+    a.c = static_cast<float *>(splits > 1 ? splitk_scratch : op.call.c->device_ptr());
+    a.stride_a = d.batch_stride_a;
+    a.stride_b = d.batch_stride_b;
+    a.stride_c = d.batch_stride_c;
+    a.m = d.m;
+    a.n = d.n;
+    a.k = d.k;
+    a.alpha = op.call.alpha;
+    a.num_splits = std::max(1u, splits);
+    if (splits <= 1) {
+      a.flags = op.call.accumulate ? TA_FLAG_ACCUMULATE : 0;
+      if (op.epilogue.bias) {
+        a.flags |= TA_FLAG_BIAS;
+        a.bias = static_cast<const float *>(op.epilogue.bias->device_ptr());
+        a.bias_batch_stride = op.epilogue.bias->shape().size() == 2 ? d.n : 0;
+      }
+      a.act = (uint32_t)op.epilogue.activation;
+      a.binary = (uint32_t)op.epilogue.binary.kind;
+      if (const Tensor *dt = op.epilogue.d_tensor())
+        a.d = static_cast<const float *>(dt->device_ptr());
+      a.beta = op.epilogue.binary.beta;
+    }
+    a.tiles_m = div_ceil(d.m, s.tile_m);
+    a.tiles_n = div_ceil(d.n, s.tile_n);
+    const uint64_t gz = (uint64_t)d.batch * a.num_splits;
+    const uint64_t gx = (uint64_t)a.tiles_m * a.tiles_n;
+    if (gz > 65535 || gx > 0x7fffffffull)
+      fail("matmul grid (" + std::to_string(gx) + ", 1, " + std::to_string(gz) +
+           ") exceeds the HIP launch limits");
+    const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
+    launch(std::string(s.symbol) + (vec ? "_vec" : "_gen"), (uint32_t)gx, 1, (uint32_t)gz,
+           gemm_threads(s), &a, stream);
+    if (splits > 1) {
+      SplitReduceArgs r{};
+      r.scratch = static_cast<const float *>(splitk_scratch);
+      r.c = static_cast<float *>(op.call.c->device_ptr());
+      r.mn = (uint64_t)d.m * d.n;
+      r.total = r.mn * d.batch;
+      r.num_splits = splits;
+      const uint64_t quads = (r.total + 3) / 4;
+      const uint64_t groups =
+          std::min<uint64_t>((quads + kReduceThreads - 1) / kReduceThreads, 8ull * ctx->cu_count());
+      launch("ta_splitk_reduce", (uint32_t)std::max<uint64_t>(groups, 1), 1, 1, kReduceThreads,
+             &r, stream);
+    }
+  }
+
+  // `up` set: dual SwiGLU launch computing `up` (plain) and `op` (gate
+  // with activation and Mul{d = up.C}) in one pass.
+  void launch_gemv(const KernelSpec &s, const ResolvedMatmul &d, const MatmulOp &op,
+                   const MatmulOp *up, Scratch &scratch, hipStream_t stream) const {
+    const bool dual = up != nullptr;
+    GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, dual);
+    GemvArgs a{};
+    a.x = static_cast<const float *>(op.call.a->device_ptr());
+    a.w = static_cast<const uint16_t *>(op.call.b->device_ptr());
+    a.y = static_cast<float *>(op.call.c->device_ptr());
+    a.rows = d.m;
+    a.n = d.n;
+    a.k = d.k;
+    a.kchunk = g.kchunk;
+    a.kchunks = g.kchunks;
+    a.alpha = op.call.alpha;
+    a.flags = s.packed() ? TA_GEMV_PACKED : 0;
+    if (op.call.accumulate)
+      a.flags |= TA_FLAG_ACCUMULATE;
+    if (op.epilogue.bias) {
+      a.flags |= TA_FLAG_BIAS;
+      a.bias = static_cast<const float *>(op.epilogue.bias->device_ptr());
+    }
+    a.act = (uint32_t)op.epilogue.activation;
+    if (dual) {
+      a.w2 = static_cast<const uint16_t *>(up->call.b->device_ptr());
+      a.y2 = static_cast<float *>(up->call.c->device_ptr());
+      a.binary = TA_BIN_NONE;
+    } else {
+      a.binary = (uint32_t)op.epilogue.binary.kind;
+      if (const Tensor *dt = op.epilogue.d_tensor())
+        a.d = static_cast<const float *>(dt->device_ptr());
+      a.beta = op.epilogue.binary.beta;
+    }
+    if (g.kchunks > 1) {
+      if (scratch.partial_bytes < g.partial_bytes || scratch.counters_len < g.tiles)
+        fail("internal: GEMV scratch not reserved");
+      a.partial = static_cast<float *>(scratch.partial);
+      a.counters = scratch.counters;
+    }
+    std::string sym = std::string(s.symbol) + (dual ? "_dual" : "") + "_m" + std::to_string(g.mr);
+    launch(sym, g.tiles * g.kchunks, 1, 1, 256, &a, stream);
+  }
+
+  // Dual SwiGLU fusion in a dependent graph: op i = x @ Wu (plain) and op
+  // i+1 = act(x @ Wg [+ bias]) * C_i on the same decode GEMV route become
+  // one launch that streams Wg and Wu together and writes both outputs.
+  static bool fusable_pair(const MatmulOp &up, const OpPlan &pu, const MatmulOp &gate,
+                           const OpPlan &pg) {
+    if (pu.kernel != pg.kernel || !KERNEL_SPECS[pu.kernel].weights_f16() ||
+        !KERNEL_SPECS[pu.kernel].is_gemv() || pu.splitk2 || pg.splitk2)
+      return false;
+    if (!up.epilogue.is_none() || up.call.accumulate || gate.call.accumulate)
+      return false;
+    if (gate.epilogue.binary.kind != EpilogueBinary::Kind::Mul ||
+        gate.epilogue.binary.d->buffer_id() != up.call.c->buffer_id())
+      return false;
+    if (gate.epilogue.bias && (gate.epilogue.bias->buffer_id() == up.call.c->buffer_id() ||
+                               gate.epilogue.bias->shape().size() != 1))
+      return false;
+    if (up.call.a->buffer_id() != gate.call.a->buffer_id() ||
+        up.call.a->shape() != gate.call.a->shape() || up.call.b->shape() != gate.call.b->shape() ||
+        up.call.c->shape() != gate.call.c->shape() || up.call.alpha != gate.call.alpha ||
+        up.packed_b != gate.packed_b || up.call.b->dtype() != gate.call.b->dtype())
+      return false;
+    return gate.call.c->buffer_id() != up.call.c->buffer_id();
+  }
+
+  void mark_fusions(const std::vector<MatmulOp> &ops, std::vector<OpPlan> &plans) const {
+    if (std::getenv("TA_NO_FUSE"))
+      return;
+    for (size_t i = 0; i + 1 < ops.size(); ++i) {
+      if (plans[i].role != 0 || plans[i + 1].role != 0)
+        continue;
+      if (fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1])) {
+        plans[i].role = 1;
+        plans[i + 1].role = 2;
+        ++i;
+      }
+    }
+  }
+
+  void check_supported(const KernelSpec &s, const ResolvedMatmul &d) const {
+    if (!kernel_supports(s, d)) {
+      std::ostringstream o;
+      o << "kernel '" << s.name << "' cannot run B=" << d.batch << " " << d.m << "x" << d.n
+        << "x" << d.k << (d.b_f16 ? " (f16 B)" : " (f32 B)") << (d.packed_b ? " packed" : "");
+      fail(o.str());
+    }
+  }
+
+  ScratchNeed total_need(const std::vector<ResolvedMatmul> &res,
+                         const std::vector<OpPlan> &plans) const {
+    ScratchNeed need;
+    for (size_t i = 0; i < res.size(); ++i)
+      if (plans[i].role != 1)
+        need.merge(scratch_need(res[i], plans[i]));
+    return need;
+  }
+
+  void record(const std::vector<MatmulOp> &ops, const std::vector<ResolvedMatmul> &res,
+              const std::vector<OpPlan> &plans, Scratch &scratch, hipStream_t stream) const {
+    for (size_t i = 0; i < ops.size(); ++i) {
+      const OpPlan &p = plans[i];
+      if (p.role == 1)
+        continue; // produced by the dual launch of op i+1
+      const KernelSpec &s = KERNEL_SPECS[p.kernel];
+      check_supported(s, res[i]);
+      if (s.is_gemv())
+        launch_gemv(s, res[i], ops[i], p.role == 2 ? &ops[i - 1] : nullptr, scratch, stream);
+      else
+        launch_gemm(s, res[i], ops[i], p.splitk2.value_or(1), scratch.splitk, stream);
+    }
+  }
+
+  // Submit `ops` on a slot and wait; returns GPU ns between the events.
+  uint64_t submit_and_wait(Slot *slot, const std::vector<MatmulOp> &ops,
+                           const std::vector<ResolvedMatmul> &res,
+                           const std::vector<OpPlan> &plans) const {
+    ScratchNeed need = total_need(res, plans);
+    slot->scratch.ensure(need.splitk, need.partial, need.counters);
+    hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
+    record(ops, res, plans, slot->scratch, slot->stream);
+    hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
+    hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
+    return (uint64_t)((double)ms * 1e6);
+  }
+
+  // ---- tuning (src/executor/tuning.rs) ----
+  void load_store() {
+    header = tune_header_line(*ctx);
+    const std::string path = tune_store_path(*ctx);
+    if (path.empty())
+      return;
+    std::ifstream in(path);
+    if (!in)
+      return;
+    std::stringstream ss;
+    ss << in.rdbuf();
+    tuned = parse_tune_store(ss.str(), header);
+  }
+
+  void record_tuned(const TuneKey &key, const TuneEntry &e) {
+    std::string text;
+    {
+      std::lock_guard<std::mutex> lock(tuned_mu);
+      tuned[key] = e;
+      text = format_tune_store(tuned, header);
+    }
+    const std::string path = tune_store_path(*ctx);
+    if (path.empty())
+      return;
+    // Atomic rewrite: temp file + rename (pipeline/tuning.rs:157-199).
+    const size_t slash = path.rfind('/');
+    std::string dir = path.substr(0, slash);
+    std::string parent = dir.substr(0, dir.rfind('/'));
+    mkdir(parent.c_str(), 0755);
+    mkdir(dir.c_str(), 0755);
+    static std::atomic<uint64_t> next{0};
+    const std::string tmp = path + ".tmp." + std::to_string(getpid()) + "." +
+                            std::to_string(next.fetch_add(1));
+    {
+      std::ofstream out(tmp, std::ios::trunc);
+      out << text;
+      if (!out)
+        return;
+    }
+    if (std::rename(tmp.c_str(), path.c_str()) != 0)
+      std::remove(tmp.c_str());
+  }
+
+  bool is_tuned(const TuneKey &key) const {
+    if (!selection.is_auto())
+      return true;
+    std::lock_guard<std::mutex> lock(tuned_mu);
+    return tuned.count(key) != 0;
+  }
+
+  std::optional<uint64_t> run_forced_once(const MatmulOp &op, const ResolvedMatmul &d,
+                                          size_t kernel, std::optional<uint32_t> splits) const {
+    ExecutorImpl *self = const_cast<ExecutorImpl *>(this);
+    Lease lease(self);
+    OpPlan p;
+    p.kernel = kernel;
+    p.splitk2 = splits;
+    return submit_and_wait(lease.s, {op}, {d}, {p});
+  }
+
+  void tune_op(const MatmulOp &op, const ResolvedMatmul &d) {
+    std::vector<size_t> cands = tune_candidate_indices(d);
+    if (cands.empty())
+      fail("no tunable kernel fits this shape");
+    const size_t heur =
+        heuristic_kernel_index(ctx->cu_count(), d.batch, d.m, d.n, d.k, d.b_f16, d.packed_b);
+    const double est_ms = (double)d.total_flops / 50e12 * 1e3;
+    const uint32_t rounds = est_ms > 8.0 ? 2 : 4;
+    (void)run_forced_once(op, d, std::count(cands.begin(), cands.end(), heur) ? heur : cands[0],
+                          std::nullopt);
+    std::vector<std::vector<uint64_t>> samples(cands.size());
+    for (uint32_t round = 0; round <= rounds; ++round)
+      for (size_t off = 0; off < cands.size(); ++off) {
+        const size_t ci = candidate_at(cands.size(), round, off);
+        auto ns = run_forced_once(op, d, cands[ci], std::nullopt);
+        if (round > 0 && ns)
+          samples[ci].push_back(*ns);
+      }
+    std::optional<uint64_t> heur_ns;
+    size_t win = cands[0];
+    std::optional<uint64_t> win_ns;
+    for (size_t i = 0; i < cands.size(); ++i) {
+      auto md = median(samples[i]);
+      if (!md)
+        continue;
+      if (cands[i] == heur)
+        heur_ns = md;
+      if (!win_ns || *md < *win_ns) {
+        win_ns = md;
+        win = cands[i];
+      }
+    }
+    if (!win_ns)
+      fail("no candidate produced a measurement");
+    if (heur_ns && (double)*win_ns >= (double)*heur_ns * 0.98) {
+      win = heur;
+      win_ns = heur_ns;
+    }
+    // Reduction pass: probe split-K against the DP winner on deep-K,
+    // few-tile shapes (executor/tuning.rs:203-250).
+    std::optional<uint32_t> best_splits;
+    const KernelSpec &s1 = splitk_stage1_spec(d.m, d.n);
+    const uint64_t tiles = (uint64_t)d.batch * div_ceil(d.m, s1.tile_m) * div_ceil(d.n, s1.tile_n);
+    if (!d.b_f16 && !d.packed_b && d.k >= 1024 && tiles < ctx->cu_count()) {
+      std::optional<uint64_t> best;
+      for (uint32_t splits : {4u, 8u, 16u, 32u, 64u, 128u}) {
+        if (d.k / splits < 128 || !auto_route_fits(d.batch, d.m, d.n, d.k, splits))
+          continue;
+        std::vector<uint64_t> ss;
+        for (uint32_t r = 0; r <= rounds; ++r) {
+          auto ns = run_forced_once(op, d, registry_index(s1.name), splits);
+          if (r > 0 && ns)
+            ss.push_back(*ns);
+        }
+        auto md = median(ss);
+        if (md && (!best || *md < *best)) {
+          best = md;
+          best_splits = splits;
+        }
+      }
+      if (!best || (double)*best >= (double)*win_ns * 0.98)
+        best_splits.reset();
+    }
+    record_tuned(TuneKey{d.batch, d.m, d.n, d.k, d.b_f16}, TuneEntry{win, best_splits});
+    if (std::getenv("TA_LOG"))
+      std::fprintf(stderr, "tensor-ash: tuned B=%u %ux%ux%u: %s%s\n", d.batch, d.m, d.n, d.k,
+                   KERNEL_SPECS[win].name,
+                   best_splits ? (" + splitk2=" + std::to_string(*best_splits)).c_str() : "");
+  }
+
+  // ---- run_ops (src/executor/dispatch.rs:87-188) ----
+  RunStats run_ops_impl(const std::vector<MatmulOp> &ops, bool graph) {
+    if (ops.empty())
+      return RunStats{std::nullopt, 0, 0};
+    if (ops.size() > config.max_calls_per_submit)
+      fail("run_ops: " + std::to_string(ops.size()) + " ops > max_calls_per_submit " +
+           std::to_string(config.max_calls_per_submit));
+    ctx->make_current();
+    for (const auto &op : ops)
+      validate_op(op);
+    std::vector<ResolvedMatmul> res;
+    res.reserve(ops.size());
+    for (const auto &op : ops)
+      res.push_back(ResolvedMatmul::from_op(op));
+    const uint64_t flops = total_flops(res);
+
+    if (config.tune && ops.size() == 1 && !ops[0].call.accumulate && ops[0].epilogue.is_none() &&
+        !res[0].a_f16 && !res[0].packed_b) {
+      const ResolvedMatmul &d = res[0];
+      const TuneKey key{d.batch, d.m, d.n, d.k, d.b_f16};
+      if (!is_tuned(key)) {
+        try {
+          tune_op(ops[0], d);
+        } catch (const Error &e) {
+          std::fprintf(stderr, "tensor-ash: tuning failed for B=%u %ux%ux%u: %s\n", d.batch,
+                       d.m, d.n, d.k, e.what());
+        }
+      }
+    }
+
+    std::vector<OpPlan> plans;
+    for (size_t i = 0; i < ops.size(); ++i) {
+      const bool eligible = !ops[i].call.accumulate && ops[i].epilogue.is_none() &&
+                            (graph || ops.size() == 1);
+      plans.push_back(plan_matmul(res[i], eligible));
+    }
+    if (graph)
+      mark_fusions(ops, plans);
+    if (!graph && plans.size() == 1 && plans[0].splitk2)
+      return run_split_k2(ops[0].call, *plans[0].splitk2);
+
+    Lease lease(this);
+    const uint64_t ns = submit_and_wait(lease.s, ops, res, plans);
+    return RunStats{ns, ops.size(), flops};
+  }
+
+  // ---- split-K (src/executor/reduction.rs:21-70) ----
+  RunStats run_split_k2(const MatmulCall &call, uint32_t num_k_splits) {
+    ctx->make_current();
+    validate_call(call);
+    if (call.accumulate)
+      fail("run_matmuls_split_k2: accumulate=true is not supported");
+    ResolvedMatmul d = ResolvedMatmul::from_call(call);
+    if (num_k_splits > 0xFFFF)
+      fail("run_matmuls_split_k2: num_k_splits=" + std::to_string(num_k_splits) +
+           " out of range [1, 65535]");
+    if (num_k_splits > d.k)
+      fail("run_matmuls_split_k2: num_k_splits=" + std::to_string(num_k_splits) +
+           " exceeds K=" + std::to_string(d.k));
+    if (d.a_f16 || d.b_f16)
+      fail("run_matmuls_split_k2: split-K stage 1 reads f32 A and B only");
+    const uint32_t splits =
+        num_k_splits == 0 ? default_num_k_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k)
+                          : num_k_splits;
+    if (splits <= 1)
+      return run_ops_impl({MatmulOp(call)}, false);
+    validate_scratch_geometry(d.batch, d.m, d.n, d.k, splits);
+    if ((uint64_t)d.batch * splits > 65535)
+      fail("split-K2 dispatch grid Z (" + std::to_string((uint64_t)d.batch * splits) +
+           ") exceeds 65535");
+    OpPlan p;
+    p.kernel = registry_index(splitk_stage1_spec(d.m, d.n).name);
+    p.splitk2 = splits;
+    Lease lease(this);
+    const uint64_t ns = submit_and_wait(lease.s, {MatmulOp(call)}, {d}, {p});
+    return RunStats{ns, 1, d.total_flops};
+  }
+
+  // ---- prepared (src/executor/prepared.rs:67-160) ----
+  std::unique_ptr<PreparedOps> prepare_impl(const Executor *owner,
+                                            const std::vector<MatmulOp> &ops, bool graph) {
+    if (ops.empty())
+      fail("prepare_ops: empty op batch");
+    if (ops.size() > config.max_calls_per_submit)
+      fail("prepare_ops: " + std::to_string(ops.size()) + " ops > max_calls_per_submit " +
+           std::to_string(config.max_calls_per_submit));
+    ctx->make_current();
+    for (const auto &op : ops)
+      validate_op(op);
+    std::vector<ResolvedMatmul> res;
+    for (const auto &op : ops)
+      res.push_back(ResolvedMatmul::from_op(op));
+    const uint64_t flops = total_flops(res);
+    // Data-parallel routes only, like the reference: split-K would need
+    // its scratch baked into the graph for the handle's lifetime.
+    std::vector<OpPlan> plans;
+    for (const auto &d : res)
+      plans.push_back(plan_matmul(d, false));
+    if (graph)
+      mark_fusions(ops, plans);
+    for (size_t i = 0; i < ops.size(); ++i)
+      if (plans[i].role != 1)
+        check_supported(KERNEL_SPECS[plans[i].kernel], res[i]);
+
+    std::unique_ptr<PreparedOps> p(new PreparedOps());
+    p->exec_ = owner;
+    p->n_calls_ = ops.size();
+    p->flops_ = flops;
+    hipStream_t stream = nullptr;
+    hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+    p->stream_ = stream;
+    hipEvent_t e0, e1;
+    hip_check(hipEventCreate(&e0), "hipEventCreate");
+    p->ev_start_ = e0;
+    hip_check(hipEventCreate(&e1), "hipEventCreate");
+    p->ev_end_ = e1;
+    // Graph-owned scratch, zeroed outside the capture (no memset nodes).
+    Scratch scratch;
+    ScratchNeed need = total_need(res, plans);
+    scratch.ensure(need.splitk, need.partial, need.counters);
+    p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters};
+
+    hipGraph_t g = nullptr;
+    hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal),
+              "hipStreamBeginCapture");
+    try {
+      record(ops, res, plans, scratch, stream);
+    } catch (...) {
+      (void)hipStreamEndCapture(stream, &g);
+      if (g)
+        (void)hipGraphDestroy(g);
+      throw;
+    }
+    hip_check(hipStreamEndCapture(stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t ge = nullptr;
+    hipError_t err = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    hip_check(err, "hipGraphInstantiate");
+    p->graph_exec_ = ge;
+    return p;
+  }
+
+  // ---- transfers (src/executor/transfer.rs) ----
+  void copy_to_device(const void *src, uint64_t bytes, const Tensor &dst, const char *op) {
+    if (bytes > dst.size_bytes())
+      fail(std::string(op) + ": " + std::to_string(bytes) + " bytes > tensor capacity " +
+           std::to_string(dst.size_bytes()));
+    Lease lease(this);
+    hip_check(hipMemcpyAsync(dst.device_ptr(), src, bytes, hipMemcpyHostToDevice, lease.s->stream),
+              "hipMemcpyAsync (upload)");
+    hip_check(hipStreamSynchronize(lease.s->stream), "hipStreamSynchronize");
+  }
+};
+
+// ---------------------------------------------------------------- Executor
+
+Executor::Executor(std::shared_ptr<Context> ctx, KernelSelection selection, ExecutorConfig config)
+    : impl_(new ExecutorImpl()) {
+  impl_->ctx = std::move(ctx);
+  impl_->selection = selection;
+  config.n_slots = std::max<size_t>(1, config.n_slots);
+  config.max_calls_per_submit = std::max<uint32_t>(1, config.max_calls_per_submit);
+  impl_->config = config;
+  impl_->ctx->make_current();
+  for (size_t i = 0; i < config.n_slots; ++i) {
+    Slot *s = new Slot();
+    hip_check(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+    hip_check(hipEventCreate(&s->start), "hipEventCreate");
+    hip_check(hipEventCreate(&s->end), "hipEventCreate");
+    impl_->all_slots.push_back(s);
+    impl_->free_slots.push_back(s);
+  }
+  impl_->load_store();
+}
+
+namespace {
+bool env_tune() {
+  const char *v = std::getenv("ML_TUNE");
+  if (!v)
+    return false;
+  std::string s = v;
+  for (auto &c : s)
+    c = (char)std::tolower((unsigned char)c);
+  return s == "1" || s == "on" || s == "true";
+}
+} // namespace
+
+Executor::Executor(std::shared_ptr<Context> ctx, KernelSelection selection, size_t n_slots,
+                   uint32_t max_calls_per_submit)
+    : Executor(std::move(ctx), selection, ExecutorConfig{n_slots, max_calls_per_submit, env_tune()}) {}
+
+Executor::~Executor() {
+  if (!impl_)
+    return;
+  (void)hipSetDevice(impl_->ctx->device());
+  for (Slot *s : impl_->all_slots) {
+    (void)hipStreamSynchronize(s->stream);
+    s->scratch.release();
+    (void)hipEventDestroy(s->start);
+    (void)hipEventDestroy(s->end);
+    (void)hipStreamDestroy(s->stream);
+    delete s;
+  }
+}
+
+const std::shared_ptr<Context> &Executor::context() const { return impl_->ctx; }
+
+RunStats Executor::run_matmuls(const std::vector<MatmulCall> &calls) const {
+  std::vector<MatmulOp> ops;
+  for (const auto &c : calls)
+    ops.emplace_back(c);
+  return impl_->run_ops_impl(ops, false);
+}
+RunStats Executor::run_matmul_graph(const std::vector<MatmulCall> &calls) const {
+  std::vector<MatmulOp> ops;
+  for (const auto &c : calls)
+    ops.emplace_back(c);
+  return impl_->run_ops_impl(ops, true);
+}
+RunStats Executor::run_ops(const std::vector<MatmulOp> &ops) const {
+  return impl_->run_ops_impl(ops, false);
+}
+RunStats Executor::run_op_graph(const std::vector<MatmulOp> &ops) const {
+  return impl_->run_ops_impl(ops, true);
+}
+RunStats Executor::run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const {
+  return impl_->run_split_k2(call, num_k_splits);
+}
+
+std::unique_ptr<PreparedOps> Executor::prepare_matmuls(const std::vector<MatmulCall> &calls) const {
+  std::vector<MatmulOp> ops;
+  for (const auto &c : calls)
+    ops.emplace_back(c);
+  return impl_->prepare_impl(this, ops, false);
+}
+std::unique_ptr<PreparedOps> Executor::prepare_ops(const std::vector<MatmulOp> &ops) const {
+  return impl_->prepare_impl(this, ops, false);
+}
+std::unique_ptr<PreparedOps> Executor::prepare_op_graph(const std::vector<MatmulOp> &ops) const {
+  return impl_->prepare_impl(this, ops, true);
+}
+
+// src/executor/tuning.rs:18-56: tune against 1.0-filled scratch tensors.
+void Executor::tune_shape(uint32_t batch, uint32_t m, uint32_t n, uint32_t k) const {
+  const TuneKey key{batch, m, n, k, false};
+  if (impl_->is_tuned(key))
+    return;
+  impl_->ctx->make_current();
+  auto shape = [&](uint32_t r, uint32_t c) {
+    return batch == 1 ? std::vector<uint32_t>{r, c} : std::vector<uint32_t>{batch, r, c};
+  };
+  Tensor a = Tensor::uninit_device(impl_->ctx, shape(m, k));
+  Tensor b = Tensor::uninit_device(impl_->ctx, shape(k, n));
+  Tensor c = Tensor::uninit_device(impl_->ctx, shape(m, n));
+  std::vector<float> ones(std::max(a.len(), b.len()), 1.0f);
+  upload(ones.data(), a.len(), a);
+  upload(ones.data(), b.len(), b);
+  MatmulOp op(MatmulCall{&a, &b, &c, 1.0f, false});
+  ResolvedMatmul d = ResolvedMatmul::from_op(op);
+  impl_->tune_op(op, d);
+}
+
+DispatchInfo Executor::dispatch_info(uint32_t batch, uint32_t m, uint32_t n, uint32_t k) const {
+  return dispatch_info_for(batch, m, n, k, false);
+}
+
+// src/executor/mod.rs:156-172.
+DispatchInfo Executor::dispatch_info_for(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                                         bool b_f16) const {
+  OpPlan p = impl_->plan_shape(batch, m, n, k, b_f16, true);
+  const KernelSpec &s = p.splitk2 ? splitk_stage1_spec(m, n) : KERNEL_SPECS[p.kernel];
+  DispatchInfo info;
+  info.kernel = s.name;
+  info.tile = {s.tile_m, s.tile_n, s.tile_k};
+  info.split_k2_splits = p.splitk2;
+  return info;
+}
+
+void Executor::upload(const float *src, size_t len, const Tensor &dst) const {
+  impl_->validate_tensor(&dst, "upload destination");
+  if (len == 0)
+    return;
+  impl_->ctx->make_current();
+  if (dst.dtype() == DType::F32) {
+    impl_->copy_to_device(src, (uint64_t)len * 4, dst, "upload");
+  } else {
+    std::vector<uint16_t> halves(len);
+    for (size_t i = 0; i < len; ++i)
+      halves[i] = f32_to_f16_bits(src[i]);
+    impl_->copy_to_device(halves.data(), (uint64_t)len * 2, dst, "upload");
+  }
+}
+
+void Executor::upload_f16(const uint16_t *src, size_t len, const Tensor &dst) const {
+  impl_->validate_tensor(&dst, "upload destination");
+  if (len == 0)
+    return;
+  if (dst.dtype() != DType::F16)
+    fail(std::string("upload_f16 requires an f16 destination tensor, got ") +
+         dtype_name(dst.dtype()));
+  impl_->ctx->make_current();
+  impl_->copy_to_device(src, (uint64_t)len * 2, dst, "upload");
+}
+
+void Executor::download(const Tensor &src, float *dst, size_t len) const {
+  impl_->validate_tensor(&src, "download source");
+  if (len == 0)
+    return;
+  impl_->ctx->make_current();
+  const uint64_t bytes = (uint64_t)len * dtype_size(src.dtype());
+  if (bytes > src.size_bytes())
+    fail("download: " + std::to_string(bytes) + " bytes > tensor capacity " +
+         std::to_string(src.size_bytes()));
+  ExecutorImpl::Lease lease(impl_.get());
+  if (src.dtype() == DType::F32) {
+    hip_check(hipMemcpyAsync(dst, src.device_ptr(), bytes, hipMemcpyDeviceToHost, lease.s->stream),
+              "hipMemcpyAsync (download)");
+    hip_check(hipStreamSynchronize(lease.s->stream), "hipStreamSynchronize");
+  } else {
+    std::vector<uint16_t> halves(len);
+    hip_check(hipMemcpyAsync(halves.data(), src.device_ptr(), bytes, hipMemcpyDeviceToHost,
+                             lease.s->stream),
+              "hipMemcpyAsync (download)");
+    hip_check(hipStreamSynchronize(lease.s->stream), "hipStreamSynchronize");
+    for (size_t i = 0; i < len; ++i)
+      dst[i] = f16_bits_to_f32(halves[i]);
+  }
+}
+
+// ------------------------------------------------------------ PreparedOps
+
+PreparedOps::~PreparedOps() {
+  if (!exec_)
+    return;
+  (void)hipSetDevice(exec_->context()->device());
+  hipStream_t s = static_cast<hipStream_t>(stream_);
+  if (s)
+    (void)hipStreamSynchronize(s); // Drop waits for in-flight work
+  if (graph_exec_)
+    (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec_));
+  for (void *p : scratch_)
+    if (p)
+      (void)hipFree(p);
+  if (ev_start_)
+    (void)hipEventDestroy(static_cast<hipEvent_t>(ev_start_));
+  if (ev_end_)
+    (void)hipEventDestroy(static_cast<hipEvent_t>(ev_end_));
+  if (s)
+    (void)hipStreamDestroy(s);
+}
+
+RunStats PreparedOps::run() {
+  submit();
+  return wait();
+}
+
+void PreparedOps::run_silent() {
+  submit();
+  hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "hipStreamSynchronize");
+  in_flight_ = false;
+}
+
+// src/executor/prepared.rs:293-307.
+void PreparedOps::submit() {
+  if (in_flight_)
+    fail("PreparedOps::submit: already in flight; call wait() first");
+  exec_->context()->make_current();
+  hipStream_t s = static_cast<hipStream_t>(stream_);
+  hip_check(hipEventRecord(static_cast<hipEvent_t>(ev_start_), s), "hipEventRecord");
+  hip_check(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec_), s), "hipGraphLaunch");
+  hip_check(hipEventRecord(static_cast<hipEvent_t>(ev_end_), s), "hipEventRecord");
+  in_flight_ = true;
+  submitted_once_ = true;
+}
+
+RunStats PreparedOps::wait() {
+  if (!in_flight_)
+    fail("PreparedOps::wait: nothing submitted");
+  exec_->context()->make_current();
+  hip_check(hipEventSynchronize(static_cast<hipEvent_t>(ev_end_)), "hipEventSynchronize");
+  in_flight_ = false;
+  float ms = 0.f;
+  hip_check(hipEventElapsedTime(&ms, static_cast<hipEvent_t>(ev_start_),
+                                static_cast<hipEvent_t>(ev_end_)),
+            "hipEventElapsedTime");
+  return RunStats{(uint64_t)((double)ms * 1e6), n_calls_, flops_};
+}
+
+} // namespace tensor_ash

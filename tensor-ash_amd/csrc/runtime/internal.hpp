@@ -1,0 +1,101 @@
+// Internal declarations of the host runtime (not part of the public API).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "../kernels/kernel_args.h"
+#include "tensor_ash.hpp"
+
+namespace tensor_ash {
+
+[[noreturn]] void fail(const std::string &msg);
+void hip_check(hipError_t err, const char *what);
+
+struct DeviceBuffer {
+  std::shared_ptr<Context> ctx;
+  void *ptr = nullptr;
+  uint64_t bytes = 0;
+  ~DeviceBuffer();
+};
+
+// src/matmul/resolution.rs:10-76.
+struct MatrixShape {
+  uint32_t batch, rows, cols;
+  static MatrixShape from_tensor_shape(const std::vector<uint32_t> &shape);
+  uint32_t batch_stride(const char *label) const;
+};
+
+// src/matmul/resolution.rs:80-442.
+struct ResolvedMatmul {
+  uint32_t m = 0, n = 0, k = 0, batch = 0;
+  uint32_t batch_stride_a = 0, batch_stride_b = 0, batch_stride_c = 0;
+  uint64_t total_flops = 0;
+  bool b_f16 = false;
+  bool a_f16 = false;
+  bool packed_b = false;
+
+  static ResolvedMatmul from_shapes(const std::vector<uint32_t> &a,
+                                    const std::vector<uint32_t> &b,
+                                    const std::vector<uint32_t> &c);
+  static ResolvedMatmul from_call(const MatmulCall &call);
+  static ResolvedMatmul from_op(const MatmulOp &op);
+  void validate_bias_shape(const std::vector<uint32_t> &shape) const;
+  void validate_epilogue(const MatmulOp &op) const;
+  bool operator==(const ResolvedMatmul &o) const;
+};
+uint64_t total_flops(const std::vector<ResolvedMatmul> &resolved);
+
+// Largest rows a decode GEMV launch handles (register-resident X rows).
+constexpr uint32_t kGemvMaxRows = 8;
+
+// ---- routing (src/pipeline/mod.rs:293-535, selection.rs:89-172) ----
+size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                              bool b_f16, bool packed_b);
+bool kernel_supports(const KernelSpec &spec, const ResolvedMatmul &dims);
+std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims);
+size_t registry_index(const char *name);
+
+// ---- split-K (src/executor/splitk2.rs) ----
+constexpr uint32_t kReduceThreads = 256;
+constexpr uint64_t kAutoScratchCapBytes = 256ull << 20;
+const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n);
+std::optional<uint32_t> heuristic_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
+                                         uint32_t k);
+uint32_t default_num_k_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k);
+bool auto_route_fits(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, uint32_t splits);
+void validate_scratch_geometry(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                               uint32_t splits);
+std::optional<uint64_t> checked_auto_scratch_end(uint64_t offset, uint64_t bytes);
+
+// ---- GEMV geometry ----
+struct GemvPlan {
+  uint32_t tw = 64, mr = 1, tiles = 0, kchunk = 0, kchunks = 1;
+  uint64_t partial_bytes = 0; // 0 when kchunks == 1
+};
+GemvPlan plan_gemv(uint32_t cus, uint32_t rows, uint32_t n, uint32_t k, uint32_t tw, bool dual);
+
+// ---- tuner (src/executor/tuning.rs:300-313, pipeline/tuning.rs) ----
+std::optional<uint64_t> median(std::vector<uint64_t> samples);
+size_t candidate_at(size_t len, uint32_t round, size_t offset);
+
+struct TuneKey {
+  uint32_t batch, m, n, k;
+  bool b_f16;
+  bool operator<(const TuneKey &o) const;
+};
+struct TuneEntry {
+  size_t kernel;
+  std::optional<uint32_t> splitk2_splits;
+};
+std::string tune_store_path(const Context &ctx);
+std::string tune_header_line(const Context &ctx);
+std::map<TuneKey, TuneEntry> parse_tune_store(const std::string &text, const std::string &header);
+std::string format_tune_store(const std::map<TuneKey, TuneEntry> &map, const std::string &header);
+
+} // namespace tensor_ash

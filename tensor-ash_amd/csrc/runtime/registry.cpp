@@ -1,0 +1,352 @@
+// KERNEL_SPECS registry, ML_KERNEL parsing, shape routing, split-K and
+// GEMV geometry, and the pure helpers of the measured tuner.
+#include <algorithm>
+#include <cctype>
+#include <cstdlib>
+#include <sstream>
+
+#include "internal.hpp"
+
+namespace tensor_ash {
+
+// Data-driven registry (role of src/pipeline/catalog.rs:129-376): one
+// declaration per gfx950 kernel; the ML_KERNEL names and the routing all
+// derive from it.  `symbol` is the code-object symbol stem: GEMM entries
+// add "_vec" / "_gen" (aligned / ragged loads), GEMV entries add "_m1",
+// "_m2", "_m4", "_m8" (rows per launch) and "_dual" (SwiGLU pair).
+const KernelSpec KERNEL_SPECS[] = {
+    {"f32_m256n256", 256, 256, 16, KernelKind::GemmF32, "ta_gemm_f32_m256n256", "large"},
+    {"f32_m256n128", 256, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m256n128", ""},
+    {"f32_m128n128", 128, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m128n128", "medium"},
+    {"f32_m128n64", 128, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m128n64", ""},
+    {"f32_m64n64", 64, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m64n64", "small"},
+    {"f16w_m256n256", 256, 256, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m256n256", ""},
+    {"f16w_m256n128", 256, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m256n128", ""},
+    {"f16w_m128n128", 128, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n128", ""},
+    {"f16w_m128n64", 128, 64, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n64", ""},
+    {"f16w_m64n64", 64, 64, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m64n64", ""},
+    {"f16w_gemv_packed_t64", 8, 64, 0, KernelKind::GemvF16Packed, "ta_gemv_f16_t64",
+     "f16w_row_packed"},
+    {"f16w_gemv_packed_t32", 8, 32, 0, KernelKind::GemvF16Packed, "ta_gemv_f16_t32", ""},
+    {"f16w_gemv_row", 8, 64, 0, KernelKind::GemvF16Row, "ta_gemv_f16_t64", "f16w_row"},
+    {"f32_gemv_row", 8, 64, 0, KernelKind::GemvF32Row, "ta_gemv_f32_t64", "row_bda,row"},
+};
+const size_t KERNEL_SPECS_LEN = sizeof(KERNEL_SPECS) / sizeof(KERNEL_SPECS[0]);
+
+size_t registry_index(const char *name) {
+  for (size_t i = 0; i < KERNEL_SPECS_LEN; ++i)
+    if (std::string(KERNEL_SPECS[i].name) == name)
+      return i;
+  fail(std::string("no kernel named ") + name);
+}
+
+namespace {
+std::string trim_lower(const std::string &v) {
+  size_t b = 0, e = v.size();
+  while (b < e && std::isspace((unsigned char)v[b]))
+    ++b;
+  while (e > b && std::isspace((unsigned char)v[e - 1]))
+    --e;
+  std::string s = v.substr(b, e - b);
+  for (auto &c : s)
+    c = (char)std::tolower((unsigned char)c);
+  return s;
+}
+} // namespace
+
+// src/pipeline/catalog.rs:162-180: case-insensitive, surrounding
+// whitespace ignored, "" and "auto" mean Auto.
+KernelSelection KernelSelection::parse(const std::string &value) {
+  const std::string v = trim_lower(value);
+  if (v.empty() || v == "auto")
+    return KernelSelection{};
+  for (size_t i = 0; i < KERNEL_SPECS_LEN; ++i) {
+    if (v == KERNEL_SPECS[i].name)
+      return KernelSelection{i};
+    std::stringstream aliases(KERNEL_SPECS[i].aliases);
+    std::string a;
+    while (std::getline(aliases, a, ','))
+      if (!a.empty() && v == a)
+        return KernelSelection{i};
+  }
+  std::string names;
+  for (size_t i = 0; i < KERNEL_SPECS_LEN; ++i)
+    names += std::string(", ") + KERNEL_SPECS[i].name;
+  fail("invalid ML_KERNEL '" + v + "', expected one of auto" + names);
+}
+
+KernelSelection KernelSelection::from_env() {
+  const char *v = std::getenv("ML_KERNEL");
+  return parse(v ? v : "auto");
+}
+
+namespace {
+uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+} // namespace
+
+bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
+  if (d.a_f16)
+    return s.kind == KernelKind::GemmF16Mfma && d.m % s.tile_m == 0 && d.n % s.tile_n == 0;
+  if (d.packed_b)
+    return s.kind == KernelKind::GemvF16Packed && d.m <= kGemvMaxRows && d.batch == 1 &&
+           d.n % s.tile_n == 0;
+  switch (s.kind) {
+  case KernelKind::GemmF32:
+    return !d.b_f16;
+  case KernelKind::GemmF16w:
+  case KernelKind::GemmF16Mfma:
+    return d.b_f16;
+  case KernelKind::GemvF16Row:
+    return d.b_f16 && d.batch == 1 && d.m <= kGemvMaxRows && d.n % 2 == 0;
+  case KernelKind::GemvF32Row:
+    return !d.b_f16 && d.batch == 1 && d.m <= kGemvMaxRows && d.n % 2 == 0;
+  case KernelKind::GemvF16Packed:
+    return false;
+  }
+  return false;
+}
+
+// Shape heuristic for 256-CU MI355X (role of src/pipeline/mod.rs:293-360
+// and selection.rs:89-172; the reference's NVIDIA-tuned tables are not a
+// target): decode shapes (M <= 8, one batch) stream the weights through
+// the GEMV; otherwise the largest MFMA tile whose grid still covers every
+// CU once, else the 64x64 tile.
+size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                              bool b_f16, bool packed_b) {
+  (void)k;
+  if (packed_b)
+    return registry_index(n % 64 == 0 ? "f16w_gemv_packed_t64" : "f16w_gemv_packed_t32");
+  if (batch == 1 && m <= kGemvMaxRows && n % 2 == 0)
+    return registry_index(b_f16 ? "f16w_gemv_row" : "f32_gemv_row");
+  static const char *f32_tiles[] = {"f32_m256n256", "f32_m256n128", "f32_m128n128",
+                                    "f32_m128n64", "f32_m64n64"};
+  static const char *f16_tiles[] = {"f16w_m256n256", "f16w_m256n128", "f16w_m128n128",
+                                    "f16w_m128n64", "f16w_m64n64"};
+  const char **names = b_f16 ? f16_tiles : f32_tiles;
+  for (int i = 0; i < 5; ++i) {
+    const KernelSpec &s = KERNEL_SPECS[registry_index(names[i])];
+    const uint64_t tiles = (uint64_t)batch * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
+    if (tiles >= cus)
+      return registry_index(names[i]);
+  }
+  return registry_index(names[4]);
+}
+
+// Every kernel that can run the shape (role of pipeline/mod.rs:491-535).
+std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims) {
+  std::vector<size_t> out;
+  for (size_t i = 0; i < KERNEL_SPECS_LEN; ++i)
+    if (kernel_supports(KERNEL_SPECS[i], dims))
+      out.push_back(i);
+  return out;
+}
+
+// ---- split-K (src/executor/splitk2.rs:36-271, retuned for 256 CUs) ----
+
+const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n) {
+  return KERNEL_SPECS[registry_index(m >= 128 && n >= 128 ? "f32_m128n128" : "f32_m64n64")];
+}
+
+// Deep-K shapes whose data-parallel grid covers less than half of the CUs
+// get enough K splits for ~2 workgroups per CU, keeping >= 256 K values
+// per split so the partial planes never outweigh the MFMA work.
+std::optional<uint32_t> heuristic_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
+                                         uint32_t k) {
+  if (batch == 0 || m <= 1 || n <= 1 || k < 1024)
+    return std::nullopt;
+  const KernelSpec &s = splitk_stage1_spec(m, n);
+  const uint64_t tiles = (uint64_t)batch * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
+  if (tiles * 2 >= cus)
+    return std::nullopt;
+  const uint64_t wanted = (2ull * cus + tiles - 1) / tiles;
+  const uint32_t max_splits = k / 256;
+  for (uint32_t splits : {128u, 64u, 32u, 16u, 8u, 4u, 2u})
+    if (splits <= wanted && splits <= max_splits)
+      return splits;
+  return std::nullopt;
+}
+
+// Split count for run_matmuls_split_k2(call, 0) (splitk2.rs:94-122): the
+// heuristic when it applies, else enough splits for ~2 workgroups per CU
+// with at least 32 K values each.
+uint32_t default_num_k_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k) {
+  if (auto h = heuristic_splits(cus, batch, m, n, k))
+    return *h;
+  const KernelSpec &s = splitk_stage1_spec(m, n);
+  const uint64_t tiles =
+      (uint64_t)std::max(batch, 1u) * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
+  if (tiles == 0)
+    return 1;
+  const uint64_t raw = std::max<uint64_t>(1, (2ull * cus + tiles - 1) / tiles);
+  const uint64_t max_splits = std::max<uint64_t>(1, k / 32);
+  return (uint32_t)std::min<uint64_t>({raw, max_splits, 0xFFFF});
+}
+
+// splitk2.rs:226-246.
+void validate_scratch_geometry(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                               uint32_t splits) {
+  if (splits > k)
+    fail("split-K2: splits=" + std::to_string(splits) + " exceeds K=" + std::to_string(k));
+  unsigned __int128 e = (unsigned __int128)batch * m * n * splits;
+  if (e > (unsigned __int128)UINT32_MAX + 1) {
+    std::ostringstream o;
+    o << "split-K2: batch*M*N*splits = " << (uint64_t)e << " exceeds u32 scratch addressing";
+    fail(o.str());
+  }
+}
+
+// splitk2.rs:155-188 (grid z limited to 65535 launches per batch*splits).
+bool auto_route_fits(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, uint32_t splits) {
+  if (batch == 0 || m == 0 || n == 0 || splits < 2 || splits > 0xFFFF || splits > k)
+    return false;
+  const unsigned __int128 total = (unsigned __int128)batch * m * n;
+  const unsigned __int128 elems = total * splits;
+  if (elems > (unsigned __int128)UINT32_MAX + 1)
+    return false;
+  if (elems * 4 > kAutoScratchCapBytes)
+    return false;
+  return (uint64_t)batch * splits <= 65535;
+}
+
+// splitk2.rs:189-193: 16-byte aligned reservation inside the cap.
+std::optional<uint64_t> checked_auto_scratch_end(uint64_t offset, uint64_t bytes) {
+  if (bytes > UINT64_MAX - 15)
+    return std::nullopt;
+  const uint64_t rounded = (bytes + 15) / 16 * 16;
+  if (offset > UINT64_MAX - rounded)
+    return std::nullopt;
+  const uint64_t end = offset + rounded;
+  if (end > kAutoScratchCapBytes)
+    return std::nullopt;
+  return end;
+}
+
+// ---- GEMV geometry ----
+// ~3 workgroups per CU: K windows of 64..512 rows (multiple of 64).
+GemvPlan plan_gemv(uint32_t cus, uint32_t rows, uint32_t n, uint32_t k, uint32_t tw, bool dual) {
+  GemvPlan p;
+  p.tw = tw;
+  p.mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+  p.tiles = div_ceil(n, tw);
+  const uint32_t wanted = std::max(1u, div_ceil(3 * cus, p.tiles));
+  uint32_t kchunk = div_ceil(k, wanted);
+  kchunk = div_ceil(kchunk, 64) * 64;
+  kchunk = std::clamp(kchunk, 64u, 512u);
+  p.kchunk = kchunk;
+  p.kchunks = div_ceil(k, kchunk);
+  p.partial_bytes =
+      p.kchunks > 1 ? (uint64_t)p.kchunks * p.tiles * (dual ? 2 : 1) * p.mr * tw * 4 : 0;
+  return p;
+}
+
+// ---- tuner helpers (src/executor/tuning.rs:283-313) ----
+
+std::optional<uint64_t> median(std::vector<uint64_t> s) {
+  if (s.empty())
+    return std::nullopt;
+  std::sort(s.begin(), s.end());
+  const size_t mid = s.size() / 2;
+  if (s.size() % 2 == 0)
+    return (uint64_t)(((unsigned __int128)s[mid - 1] + s[mid]) / 2);
+  return s[mid];
+}
+
+// Interleaved candidate order: round 0 in registry order, then pairs of
+// rounds walking forward and backward from a start that moves by half the
+// list per pair, so every candidate sees every position equally often.
+size_t candidate_at(size_t len, uint32_t round, size_t offset) {
+  if (round == 0)
+    return offset;
+  const size_t pair = (round - 1) / 2;
+  const size_t start = pair * ((len + 1) / 2) % len;
+  if (round % 2 == 1)
+    return (start + offset) % len;
+  return (start + len - 1 - offset) % len;
+}
+
+bool TuneKey::operator<(const TuneKey &o) const {
+  return std::tie(batch, m, n, k, b_f16) < std::tie(o.batch, o.m, o.n, o.k, o.b_f16);
+}
+
+// Persistent store (src/pipeline/tuning.rs:60-199): one header line that
+// binds the HIP runtime version, the gfx arch and a hash of every loaded
+// code object, then "B M N K kernel [splitk2=S] [bf16]" lines.
+std::string tune_store_path(const Context &ctx) {
+  std::string base;
+  if (const char *x = std::getenv("XDG_CACHE_HOME"); x && *x)
+    base = x;
+  else if (const char *h = std::getenv("HOME"); h && *h)
+    base = std::string(h) + "/.cache";
+  else
+    return "";
+  std::string arch = ctx.arch();
+  for (auto &c : arch)
+    if (c == ':' || c == '/')
+      c = '_';
+  return base + "/tensor-ash/tuned_kernels_" + arch + ".txt";
+}
+
+std::string tune_header_line(const Context &ctx) {
+  char hash[32];
+  std::snprintf(hash, sizeof hash, "%016llx", (unsigned long long)ctx.code_object_hash());
+  return "tensor-ash-tune-v3 hip=" + std::to_string(ctx.runtime_version()) +
+         " arch=" + ctx.arch() + " kernels=" + hash;
+}
+
+std::map<TuneKey, TuneEntry> parse_tune_store(const std::string &text,
+                                              const std::string &header) {
+  std::map<TuneKey, TuneEntry> map;
+  std::istringstream in(text);
+  std::string line;
+  if (!std::getline(in, line) || line != header)
+    return map;
+  while (std::getline(in, line)) {
+    std::istringstream ls(line);
+    long long b, m, n, k;
+    std::string name;
+    if (!(ls >> b >> m >> n >> k >> name))
+      continue;
+    if (b <= 0 || m <= 0 || n <= 0 || k <= 0 || b > UINT32_MAX || m > UINT32_MAX ||
+        n > UINT32_MAX || k > UINT32_MAX)
+      continue;
+    size_t idx = KERNEL_SPECS_LEN;
+    for (size_t i = 0; i < KERNEL_SPECS_LEN; ++i)
+      if (name == KERNEL_SPECS[i].name)
+        idx = i;
+    if (idx == KERNEL_SPECS_LEN)
+      continue;
+    TuneEntry e{idx, std::nullopt};
+    bool bf16 = false;
+    std::string tok;
+    while (ls >> tok) {
+      if (tok.rfind("splitk2=", 0) == 0) {
+        char *end = nullptr;
+        const unsigned long s = std::strtoul(tok.c_str() + 8, &end, 10);
+        if (end && *end == 0 && s >= 2 && s <= 0xFFFF)
+          e.splitk2_splits = (uint32_t)s;
+      } else if (tok == "bf16") {
+        bf16 = true;
+      }
+    }
+    map[TuneKey{(uint32_t)b, (uint32_t)m, (uint32_t)n, (uint32_t)k, bf16}] = e;
+  }
+  return map;
+}
+
+std::string format_tune_store(const std::map<TuneKey, TuneEntry> &map,
+                              const std::string &header) {
+  std::ostringstream o;
+  o << header << "\n";
+  for (const auto &[key, e] : map) {
+    o << key.batch << " " << key.m << " " << key.n << " " << key.k << " "
+      << KERNEL_SPECS[e.kernel].name;
+    if (e.splitk2_splits)
+      o << " splitk2=" << *e.splitk2_splits;
+    if (key.b_f16)
+      o << " bf16";
+    o << "\n";
+  }
+  return o.str();
+}
+
+} // namespace tensor_ash

@@ -1,0 +1,285 @@
+// C++ mirror of the reference's Rust API for the fused-epilogue GEMM path
+// (gusahlg/tensor-ash: src/lib.rs re-exports).  Same type and function
+// names, argument meaning and error behaviour (errors are thrown as
+// tensor_ash::Error with the reference's message text).  The C ABI in
+// include/tensor_ash.h is a thin layer over this header.
+#pragma once
+
+#include <array>
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace tensor_ash {
+
+struct Error : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+// src/dtype.rs:10-18.
+enum class DType { F32, F16 };
+uint64_t dtype_size(DType d);
+const char *dtype_name(DType d);
+
+// src/dtype.rs:42-112 (f16 decode is exact IEEE, see dtype.cpp).
+uint16_t f32_to_f16_bits(float value);
+float f16_bits_to_f32(uint16_t bits);
+float round_f32_via_f16(float value);
+
+class Context;
+struct DeviceBuffer;
+
+// src/tensor.rs:20-174: shape + dtype + shared device allocation.
+class Tensor {
+public:
+  static Tensor uninit_device(const std::shared_ptr<Context> &ctx,
+                              const std::vector<uint32_t> &shape);
+  static Tensor uninit_device_f16(const std::shared_ptr<Context> &ctx,
+                                  const std::vector<uint32_t> &shape);
+  static uint64_t numel_checked(const std::vector<uint32_t> &shape);
+
+  Tensor alias_with_shape(const std::vector<uint32_t> &shape) const;
+  const std::vector<uint32_t> &shape() const { return shape_; }
+  DType dtype() const { return dtype_; }
+  uint64_t len() const;
+  uint64_t size_bytes() const;
+  void *device_ptr() const;
+  const DeviceBuffer *buffer_id() const { return buffer_.get(); }
+  bool belongs_to(const Context *ctx) const;
+
+private:
+  Tensor(std::vector<uint32_t> shape, DType dtype, std::shared_ptr<DeviceBuffer> buf)
+      : shape_(std::move(shape)), dtype_(dtype), buffer_(std::move(buf)) {}
+  std::vector<uint32_t> shape_;
+  DType dtype_;
+  std::shared_ptr<DeviceBuffer> buffer_;
+};
+
+// src/matmul/api.rs:5-11.
+struct MatmulCall {
+  const Tensor *a = nullptr;
+  const Tensor *b = nullptr;
+  const Tensor *c = nullptr;
+  float alpha = 1.0f;
+  bool accumulate = false;
+};
+
+// src/matmul/api.rs:15-35 (codes 0-3).
+enum class Activation : uint32_t { None = 0, Relu = 1, Silu = 2, Gelu = 3 };
+
+// src/matmul/api.rs:41-48.
+struct EpilogueBinary {
+  enum class Kind : uint32_t { None = 0, AddScaled = 1, Mul = 2 };
+  Kind kind = Kind::None;
+  const Tensor *d = nullptr;
+  float beta = 0.0f;
+  static EpilogueBinary none() { return {}; }
+  static EpilogueBinary add_scaled(const Tensor &d, float beta) {
+    return {Kind::AddScaled, &d, beta};
+  }
+  static EpilogueBinary mul(const Tensor &d) { return {Kind::Mul, &d, 0.0f}; }
+};
+
+// src/matmul/api.rs:56-105.
+struct Epilogue {
+  const Tensor *bias = nullptr;
+  Activation activation = Activation::None;
+  EpilogueBinary binary;
+  bool is_none() const {
+    return bias == nullptr && activation == Activation::None &&
+           binary.kind == EpilogueBinary::Kind::None;
+  }
+  const Tensor *d_tensor() const {
+    return binary.kind == EpilogueBinary::Kind::None ? nullptr : binary.d;
+  }
+};
+
+// src/matmul/api.rs:213-299 (normed_a / store are not on this path).
+struct MatmulOp {
+  MatmulCall call;
+  Epilogue epilogue;
+  bool packed_b = false;
+  MatmulOp() = default;
+  explicit MatmulOp(const MatmulCall &c) : call(c) {}
+  MatmulOp(const MatmulCall &c, const Epilogue &e) : call(c), epilogue(e) {}
+  static MatmulOp with_epilogue(const MatmulCall &c, const Epilogue &e) {
+    return MatmulOp(c, e);
+  }
+  MatmulOp with_packed_b() const {
+    MatmulOp o = *this;
+    o.packed_b = true;
+    return o;
+  }
+};
+
+// src/matmul/api.rs:311-353.
+struct RunStats {
+  std::optional<uint64_t> gpu_time_ns;
+  size_t n_calls = 0;
+  uint64_t total_flops = 0;
+  std::optional<double> tflops() const {
+    if (!gpu_time_ns || *gpu_time_ns == 0)
+      return std::nullopt;
+    return (double)total_flops / (double)*gpu_time_ns * 1e-3;
+  }
+};
+
+// src/executor/mod.rs:64-81.
+struct DispatchInfo {
+  const char *kernel = "";
+  std::array<uint32_t, 3> tile{0, 0, 0};
+  std::optional<uint32_t> split_k2_splits;
+};
+
+// src/executor/mod.rs:86-100.
+struct ExecutorConfig {
+  size_t n_slots = 2;
+  uint32_t max_calls_per_submit = 64;
+  bool tune = false;
+};
+
+// src/matmul/api.rs:324-344 and src/pipeline/routing.rs:10-23.
+std::vector<float> pack_f16w_row_tiles(const float *src, size_t k, size_t n, size_t tile_n);
+uint32_t f16w_row_tile_n(uint32_t k, uint32_t n);
+
+// src/pipeline/catalog.rs:10-197: one registry entry per gfx950 kernel.
+enum class KernelKind : uint32_t {
+  GemmF32,       // f32 A, f32 B, FP32 MFMA
+  GemmF16w,      // f32 A, f16 B widened to f32, FP32 MFMA
+  GemmF16Mfma,   // f16-rounded A, f16 B, f16 MFMA with f32 accumulation
+  GemvF16Packed, // M <= 8 decode GEMV, f16 B packed [N/TW][K][TW]
+  GemvF16Row,    // M <= 8 decode GEMV, f16 B row-major
+  GemvF32Row,    // M <= 8 decode GEMV, f32 B row-major
+};
+struct KernelSpec {
+  const char *name;
+  uint32_t tile_m, tile_n, tile_k;
+  KernelKind kind;
+  const char *symbol; // code-object symbol stem
+  const char *aliases; // extra ML_KERNEL spellings, comma separated
+  bool weights_f16() const {
+    return kind == KernelKind::GemmF16w || kind == KernelKind::GemmF16Mfma ||
+           kind == KernelKind::GemvF16Packed || kind == KernelKind::GemvF16Row;
+  }
+  bool is_gemv() const {
+    return kind == KernelKind::GemvF16Packed || kind == KernelKind::GemvF16Row ||
+           kind == KernelKind::GemvF32Row;
+  }
+  bool packed() const { return kind == KernelKind::GemvF16Packed; }
+};
+extern const KernelSpec KERNEL_SPECS[];
+extern const size_t KERNEL_SPECS_LEN;
+
+// ML_KERNEL value: Auto or one registry index.
+struct KernelSelection {
+  std::optional<size_t> index; // nullopt = Auto
+  static KernelSelection parse(const std::string &value);
+  static KernelSelection from_env();
+  bool is_auto() const { return !index.has_value(); }
+};
+
+// src/context: one HIP device + the loaded gfx950 code objects.
+class Context {
+public:
+  // preference: "auto", "discrete", "index:N", "N", "name:<substr>",
+  // "<substr>" (src/context/device.rs:18-54).
+  static std::shared_ptr<Context> create(bool enable_validation,
+                                         const std::string &preference);
+  ~Context();
+  int device() const { return device_; }
+  uint32_t cu_count() const { return cu_count_; }
+  const std::string &device_name() const { return name_; }
+  const std::string &arch() const { return arch_; }
+  int runtime_version() const { return runtime_version_; }
+  uint64_t code_object_hash() const { return code_hash_; }
+  void *function(const std::string &symbol) const; // hipFunction_t
+  void make_current() const;
+
+private:
+  Context() = default;
+  int device_ = 0;
+  uint32_t cu_count_ = 0;
+  std::string name_, arch_;
+  int runtime_version_ = 0;
+  uint64_t code_hash_ = 0;
+  std::vector<void *> modules_;
+  std::vector<std::pair<std::string, void *>> functions_;
+};
+
+class Executor;
+struct ExecutorImpl;
+
+// src/executor/prepared.rs:46-353: validated + routed op batch recorded
+// once as a hipGraph and replayed with one launch per call.
+class PreparedOps {
+public:
+  ~PreparedOps();
+  PreparedOps(const PreparedOps &) = delete;
+  PreparedOps &operator=(const PreparedOps &) = delete;
+  RunStats run();
+  void run_silent();
+  void submit();
+  RunStats wait();
+  size_t n_calls() const { return n_calls_; }
+
+private:
+  friend class Executor;
+  friend struct ExecutorImpl;
+  PreparedOps() = default;
+  const Executor *exec_ = nullptr;
+  void *stream_ = nullptr; // hipStream_t
+  void *graph_exec_ = nullptr;
+  void *ev_start_ = nullptr, *ev_end_ = nullptr;
+  std::vector<void *> scratch_;
+  bool in_flight_ = false;
+  bool submitted_once_ = false;
+  size_t n_calls_ = 0;
+  uint64_t flops_ = 0;
+};
+
+struct ExecutorImpl;
+
+// src/executor/mod.rs:102-391: thread-safe dispatcher over a pool of
+// slots (a slot = one HIP stream + its events and scratch).
+class Executor {
+public:
+  Executor(std::shared_ptr<Context> ctx, KernelSelection selection, ExecutorConfig config);
+  // ML_TUNE read from the environment (src/executor/mod.rs:325-339).
+  Executor(std::shared_ptr<Context> ctx, KernelSelection selection, size_t n_slots,
+           uint32_t max_calls_per_submit);
+  ~Executor();
+  Executor(const Executor &) = delete;
+  Executor &operator=(const Executor &) = delete;
+
+  const std::shared_ptr<Context> &context() const;
+
+  RunStats run_matmuls(const std::vector<MatmulCall> &calls) const;
+  RunStats run_matmul_graph(const std::vector<MatmulCall> &calls) const;
+  RunStats run_ops(const std::vector<MatmulOp> &ops) const;
+  RunStats run_op_graph(const std::vector<MatmulOp> &ops) const;
+  RunStats run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const;
+
+  std::unique_ptr<PreparedOps> prepare_matmuls(const std::vector<MatmulCall> &calls) const;
+  std::unique_ptr<PreparedOps> prepare_ops(const std::vector<MatmulOp> &ops) const;
+  std::unique_ptr<PreparedOps> prepare_op_graph(const std::vector<MatmulOp> &ops) const;
+
+  void tune_shape(uint32_t batch, uint32_t m, uint32_t n, uint32_t k) const;
+  DispatchInfo dispatch_info(uint32_t batch, uint32_t m, uint32_t n, uint32_t k) const;
+  DispatchInfo dispatch_info_for(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                                 bool b_f16) const;
+
+  void upload(const float *src, size_t len, const Tensor &dst) const;
+  void upload_f16(const uint16_t *src, size_t len, const Tensor &dst) const;
+  void download(const Tensor &src, float *dst, size_t len) const;
+
+  ExecutorImpl *impl() const { return impl_.get(); }
+
+private:
+  std::unique_ptr<ExecutorImpl> impl_;
+};
+
+} // namespace tensor_ash

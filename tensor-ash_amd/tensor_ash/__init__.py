@@ -1,0 +1,370 @@
+"""ctypes binding of the tensor-ash C ABI (include/tensor_ash.h).
+
+Loads ``tensor-ash_amd/lib/libtensor_ash.so`` (built by
+``tensor-ash_amd/build.py``) and wraps its handles in small Python classes
+that follow the reference's Rust API names (``Context``, ``Executor``,
+``Tensor``, ``MatmulOp``, ``Epilogue``, ``run_ops``, ``run_op_graph``,
+``run_matmuls_split_k2``, ``prepare_ops`` ...).  There is no CPU fallback:
+every compute call goes through the HIP library, and a missing library is
+an ImportError.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("TA_LIBRARY", _PKG / "lib" / "libtensor_ash.so"))
+
+if not LIB_PATH.exists():
+    raise ImportError(f"{LIB_PATH} is missing: build it with `python tensor-ash_amd/build.py`")
+
+_lib = C.CDLL(str(LIB_PATH))
+
+ACTIVATION_NONE, ACTIVATION_RELU, ACTIVATION_SILU, ACTIVATION_GELU = 0, 1, 2, 3
+BINARY_NONE, BINARY_ADD_SCALED, BINARY_MUL = 0, 1, 2
+
+
+class TensorAshError(RuntimeError):
+    """A tensor-ash call returned -1 / NULL; the message is ta_last_error()."""
+
+
+class RunStats(C.Structure):
+    _fields_ = [("has_gpu_time", C.c_uint32), ("gpu_time_ns", C.c_uint64), ("n_calls", C.c_size_t),
+                ("total_flops", C.c_uint64), ("tflops", C.c_double)]
+
+
+class _Call(C.Structure):
+    _fields_ = [("a", C.c_void_p), ("b", C.c_void_p), ("c", C.c_void_p), ("alpha", C.c_float),
+                ("accumulate", C.c_uint32)]
+
+
+class _Epilogue(C.Structure):
+    _fields_ = [("bias", C.c_void_p), ("activation", C.c_uint32), ("binary_kind", C.c_uint32),
+                ("d", C.c_void_p), ("beta", C.c_float)]
+
+
+class _Op(C.Structure):
+    _fields_ = [("call", _Call), ("epilogue", _Epilogue)]
+
+
+class _OpV2(C.Structure):
+    _fields_ = [("base", _Op), ("packed_b", C.c_uint32), ("reserved", C.c_uint32 * 3)]
+
+
+class _DispatchInfo(C.Structure):
+    _fields_ = [("kernel", C.c_char_p), ("tile", C.c_uint32 * 3), ("has_split_k2", C.c_uint32),
+                ("split_k2_splits", C.c_uint32)]
+
+
+def _sig(name, restype, *argtypes):
+    fn = getattr(_lib, name)
+    fn.restype = restype
+    fn.argtypes = list(argtypes)
+    return fn
+
+
+P = C.c_void_p
+u32, u64, sz, f32 = C.c_uint32, C.c_uint64, C.c_size_t, C.c_float
+_sig("ta_version", C.c_char_p)
+_sig("ta_last_error", C.c_char_p)
+_sig("ta_context_create", P, u32, C.c_char_p)
+_sig("ta_context_destroy", None, P)
+_sig("ta_context_supports_f16", u32, P)
+_sig("ta_context_supports_bda", u32, P)
+_sig("ta_context_cu_count", u32, P)
+_sig("ta_executor_create", P, P, sz, u32, C.c_char_p)
+_sig("ta_executor_create_v2", P, P, sz, u32, C.c_char_p, u32)
+_sig("ta_executor_destroy", None, P)
+for _n in ("ta_tensor_create", "ta_tensor_create_on_executor", "ta_tensor_create_f16",
+           "ta_tensor_create_f16_on_executor"):
+    _sig(_n, P, P, C.POINTER(u32), sz)
+_sig("ta_tensor_destroy", None, P)
+_sig("ta_tensor_len", u64, P)
+_sig("ta_tensor_size_bytes", u64, P)
+_sig("ta_tensor_is_f16", u32, P)
+_sig("ta_upload", C.c_int, P, P, C.POINTER(f32), sz)
+_sig("ta_upload_f16", C.c_int, P, P, C.POINTER(C.c_uint16), sz)
+_sig("ta_download", C.c_int, P, P, C.POINTER(f32), sz)
+_sig("ta_matmul", C.c_int, P, P, P, P, f32, u32, C.POINTER(RunStats))
+_sig("ta_matmul_batch", C.c_int, P, C.POINTER(_Call), sz, C.POINTER(RunStats))
+_sig("ta_run_ops", C.c_int, P, C.POINTER(_Op), sz, C.POINTER(RunStats))
+_sig("ta_run_op_graph", C.c_int, P, C.POINTER(_Op), sz, C.POINTER(RunStats))
+_sig("ta_run_ops_v2", C.c_int, P, C.POINTER(_OpV2), sz, C.POINTER(RunStats))
+_sig("ta_run_op_graph_v2", C.c_int, P, C.POINTER(_OpV2), sz, C.POINTER(RunStats))
+_sig("ta_matmul_split_k2", C.c_int, P, P, P, P, f32, u32, C.POINTER(RunStats))
+_sig("ta_prepared_create", P, P, C.POINTER(_Op), sz, u32)
+_sig("ta_prepared_create_v2", P, P, C.POINTER(_OpV2), sz, u32)
+_sig("ta_prepared_run", C.c_int, P, C.POINTER(RunStats))
+_sig("ta_prepared_submit", C.c_int, P)
+_sig("ta_prepared_wait", C.c_int, P, C.POINTER(RunStats))
+_sig("ta_prepared_destroy", None, P)
+_sig("ta_dispatch_info_for", C.c_int, P, u32, u32, u32, u32, u32, C.POINTER(_DispatchInfo))
+_sig("ta_tune_shape", C.c_int, P, u32, u32, u32, u32)
+_sig("ta_pack_f16w_row_tiles", C.c_int, C.POINTER(f32), sz, sz, sz, C.POINTER(f32))
+_sig("ta_f16w_row_tile_n", u32, u32, u32)
+_sig("ta_kernel_count", sz)
+_sig("ta_kernel_name", C.c_char_p, sz)
+_sig("ta_kernel_tile", C.c_int, sz, C.POINTER(u32))
+
+lib = _lib
+
+
+def last_error() -> str:
+    return (_lib.ta_last_error() or b"").decode()
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise TensorAshError(last_error())
+
+
+def _checkp(ptr):
+    if not ptr:
+        raise TensorAshError(last_error())
+    return ptr
+
+
+def version() -> str:
+    return _lib.ta_version().decode()
+
+
+def kernel_names() -> list[str]:
+    return [_lib.ta_kernel_name(i).decode() for i in range(_lib.ta_kernel_count())]
+
+
+def f16w_row_tile_n(k: int, n: int) -> int:
+    return int(_lib.ta_f16w_row_tile_n(k, n))
+
+
+def pack_f16w_row_tiles(src: np.ndarray, k: int, n: int, tile_n: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32).reshape(-1)
+    out = np.empty_like(src)
+    _check(_lib.ta_pack_f16w_row_tiles(src.ctypes.data_as(C.POINTER(f32)), k, n, tile_n,
+                                       out.ctypes.data_as(C.POINTER(f32))))
+    return out
+
+
+class Context:
+    def __init__(self, device_preference: Optional[str] = None, enable_validation: bool = False):
+        pref = None if device_preference is None else device_preference.encode()
+        self._h = _checkp(_lib.ta_context_create(int(enable_validation), pref))
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def cu_count(self) -> int:
+        return int(_lib.ta_context_cu_count(self._h))
+
+    def close(self):
+        if self._h:
+            _lib.ta_context_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Tensor:
+    def __init__(self, ctx: Context, shape: Sequence[int], f16: bool = False):
+        arr = (u32 * len(shape))(*shape)
+        fn = _lib.ta_tensor_create_f16 if f16 else _lib.ta_tensor_create
+        self._h = _checkp(fn(ctx.handle, arr, len(shape)))
+        self._ctx = ctx  # keep the context alive
+        self.shape = tuple(int(s) for s in shape)
+        self.f16 = f16
+
+    @property
+    def handle(self):
+        return self._h
+
+    def __len__(self):
+        return int(_lib.ta_tensor_len(self._h))
+
+    @property
+    def size_bytes(self) -> int:
+        return int(_lib.ta_tensor_size_bytes(self._h))
+
+    def close(self):
+        if self._h:
+            _lib.ta_tensor_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class Epilogue:
+    """src/matmul/api.rs:56-105: +bias -> activation -> binary with D."""
+    bias: Optional[Tensor] = None
+    activation: int = ACTIVATION_NONE
+    binary: int = BINARY_NONE
+    d: Optional[Tensor] = None
+    beta: float = 0.0
+
+
+@dataclass
+class MatmulOp:
+    """src/matmul/api.rs:213-299 (with_packed_b -> packed_b=True)."""
+    a: Tensor
+    b: Tensor
+    c: Tensor
+    alpha: float = 1.0
+    accumulate: bool = False
+    epilogue: Epilogue = field(default_factory=Epilogue)
+    packed_b: bool = False
+
+    def _raw(self) -> _Op:
+        e = self.epilogue
+        return _Op(_Call(self.a.handle, self.b.handle, self.c.handle, self.alpha, int(self.accumulate)),
+                   _Epilogue(e.bias.handle if e.bias else None, e.activation, e.binary,
+                             e.d.handle if e.d else None, e.beta))
+
+
+def _ops_array(ops: Sequence[MatmulOp]):
+    if any(o.packed_b for o in ops):
+        arr = (_OpV2 * len(ops))(*[_OpV2(o._raw(), int(o.packed_b)) for o in ops])
+        return arr, True
+    return (_Op * len(ops))(*[o._raw() for o in ops]), False
+
+
+class Prepared:
+    def __init__(self, exec_: "Executor", ops: Sequence[MatmulOp], as_graph: bool):
+        arr, v2 = _ops_array(ops)
+        fn = _lib.ta_prepared_create_v2 if v2 else _lib.ta_prepared_create
+        self._h = _checkp(fn(exec_.handle, arr, len(ops), int(as_graph)))
+        self._keep = (exec_, list(ops))
+
+    def run(self) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_prepared_run(self._h, C.byref(st)))
+        return st
+
+    def submit(self) -> None:
+        _check(_lib.ta_prepared_submit(self._h))
+
+    def wait(self) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_prepared_wait(self._h, C.byref(st)))
+        return st
+
+    def close(self):
+        if self._h:
+            _lib.ta_prepared_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Executor:
+    def __init__(self, ctx: Context, n_slots: int = 2, max_calls_per_submit: int = 64,
+                 kernel_selection: Optional[str] = None, tune: Optional[bool] = None):
+        sel = None if kernel_selection is None else kernel_selection.encode()
+        if tune is None:
+            h = _lib.ta_executor_create(ctx.handle, n_slots, max_calls_per_submit, sel)
+        else:
+            h = _lib.ta_executor_create_v2(ctx.handle, n_slots, max_calls_per_submit, sel, int(tune))
+        self._h = _checkp(h)
+        self.ctx = ctx
+
+    @property
+    def handle(self):
+        return self._h
+
+    def tensor(self, shape: Sequence[int], f16: bool = False) -> Tensor:
+        return Tensor(self.ctx, shape, f16)
+
+    def upload(self, t: Tensor, data: np.ndarray) -> None:
+        a = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+        _check(_lib.ta_upload(self._h, t.handle, a.ctypes.data_as(C.POINTER(f32)), a.size))
+
+    def upload_f16(self, t: Tensor, bits: np.ndarray) -> None:
+        a = np.ascontiguousarray(bits, dtype=np.uint16).reshape(-1)
+        _check(_lib.ta_upload_f16(self._h, t.handle, a.ctypes.data_as(C.POINTER(C.c_uint16)), a.size))
+
+    def download(self, t: Tensor, n: Optional[int] = None) -> np.ndarray:
+        n = len(t) if n is None else n
+        out = np.empty(n, dtype=np.float32)
+        _check(_lib.ta_download(self._h, t.handle, out.ctypes.data_as(C.POINTER(f32)), n))
+        return out.reshape(t.shape) if n == len(t) else out
+
+    def tensor_from(self, data: np.ndarray, f16: bool = False, shape=None) -> Tensor:
+        t = self.tensor(shape or data.shape, f16)
+        self.upload(t, data)
+        return t
+
+    def matmul(self, a: Tensor, b: Tensor, c: Tensor, alpha: float = 1.0, accumulate: bool = False) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_matmul(self._h, a.handle, b.handle, c.handle, alpha, int(accumulate), C.byref(st)))
+        return st
+
+    def matmul_batch(self, calls: Sequence[tuple]) -> RunStats:
+        arr = (_Call * len(calls))(*[_Call(a.handle, b.handle, c.handle, al, int(acc))
+                                     for (a, b, c, al, acc) in calls])
+        st = RunStats()
+        _check(_lib.ta_matmul_batch(self._h, arr, len(calls), C.byref(st)))
+        return st
+
+    def run_ops(self, ops: Sequence[MatmulOp]) -> RunStats:
+        arr, v2 = _ops_array(ops)
+        st = RunStats()
+        fn = _lib.ta_run_ops_v2 if v2 else _lib.ta_run_ops
+        _check(fn(self._h, arr, len(ops), C.byref(st)))
+        return st
+
+    def run_op_graph(self, ops: Sequence[MatmulOp]) -> RunStats:
+        arr, v2 = _ops_array(ops)
+        st = RunStats()
+        fn = _lib.ta_run_op_graph_v2 if v2 else _lib.ta_run_op_graph
+        _check(fn(self._h, arr, len(ops), C.byref(st)))
+        return st
+
+    def run_matmuls_split_k2(self, a: Tensor, b: Tensor, c: Tensor, splits: int, alpha: float = 1.0) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_matmul_split_k2(self._h, a.handle, b.handle, c.handle, alpha, splits, C.byref(st)))
+        return st
+
+    def prepare_ops(self, ops: Sequence[MatmulOp]) -> Prepared:
+        return Prepared(self, ops, False)
+
+    def prepare_op_graph(self, ops: Sequence[MatmulOp]) -> Prepared:
+        return Prepared(self, ops, True)
+
+    def dispatch_info_for(self, batch: int, m: int, n: int, k: int, b_f16: bool = False) -> dict:
+        info = _DispatchInfo()
+        _check(_lib.ta_dispatch_info_for(self._h, batch, m, n, k, int(b_f16), C.byref(info)))
+        return {"kernel": info.kernel.decode(), "tile": tuple(info.tile),
+                "split_k2": info.split_k2_splits if info.has_split_k2 else None}
+
+    def tune_shape(self, batch: int, m: int, n: int, k: int) -> None:
+        _check(_lib.ta_tune_shape(self._h, batch, m, n, k))
+
+    def close(self):
+        if self._h:
+            _lib.ta_executor_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,189 @@
+"""GPU parity of the FP32-MFMA fused-epilogue GEMM against the CPU oracle.
+
+Mirrors the reference's tests/correctness/{epilogue,shapes,batch,property,
+kernels,f16}.rs: same seeds style (fill_det), same tolerance family.
+
+Tolerances (written here, checked on every case):
+  * abs:  max |gpu - ref| <= 2 * tolerance(K) + 1e-4, tolerance(K) = 8*K*eps
+          (tests/correctness/epilogue.rs:49-54; plain GEMMs use tolerance(K))
+  * rel:  max |gpu - ref| / max |ref| <= 1e-5 * sqrt(K)   (BASELINE north star)
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def check_f32(got, ref, k, oracle, epi=True):
+    got = np.asarray(got, dtype=np.float32).reshape(-1)
+    ref = np.asarray(ref, dtype=np.float32).reshape(-1)
+    err, idx = oracle.max_abs_err(got, ref)
+    tol = 2 * oracle.tolerance(k) + 1e-4 if epi else oracle.tolerance(k)
+    assert err <= tol, f"abs err {err} at {idx} (gpu {got[idx]} ref {ref[idx]}) > {tol}"
+    r = rel_err(got, ref)
+    assert r <= 1e-5 * math.sqrt(k), f"rel err {r} > {1e-5 * math.sqrt(k)}"
+
+
+def run_case(ta, ex, oracle, m, n, k, batch_a=1, batch_b=1, batch_c=1, alpha=1.0, accumulate=False,
+             bias=None, act=0, binary=0, beta=0.0, seed=71, kernel_ex=None):
+    e = kernel_ex or ex
+    sa = [m, k] if batch_a == 1 and batch_c == 1 else [batch_a, m, k]
+    sb = [k, n] if batch_b == 1 and batch_c == 1 else [batch_b, k, n]
+    sc = [m, n] if batch_c == 1 else [batch_c, m, n]
+    ha = oracle.fill_det(int(np.prod(sa)), seed)
+    hb = oracle.fill_det(int(np.prod(sb)), seed + 1)
+    a, b = e.tensor_from(ha, shape=sa), e.tensor_from(hb, shape=sb)
+    c = e.tensor(sc)
+    hc0 = None
+    if accumulate:
+        hc0 = oracle.fill_det(int(np.prod(sc)), seed + 2)
+        e.upload(c, hc0)
+    epi = ta.Epilogue(activation=act, binary=binary, beta=beta)
+    hbias = None
+    bias_stride = 0
+    if bias is not None:
+        hbias = oracle.fill_det(int(np.prod(bias)), seed + 3)
+        epi.bias = e.tensor_from(hbias, shape=bias)
+        bias_stride = n if len(bias) == 2 else 0
+    hd = None
+    if binary:
+        hd = oracle.fill_det(int(np.prod(sc)), seed + 4)
+        epi.d = e.tensor_from(hd, shape=sc)
+    st = e.run_ops([ta.MatmulOp(a, b, c, alpha, accumulate, epi)])
+    assert st.n_calls == 1 and st.total_flops == 2 * batch_c * m * n * k
+    got = e.download(c)
+    ref = oracle.reference_gemm(ha, hb, batch_c, m, n, k, alpha, hc0, accumulate, hbias,
+                                bias_stride, act, binary, hd, beta)
+    check_f32(got, ref, k, oracle)
+    return st
+
+
+def test_c_smoke_values(ta, ex):
+    """examples/c_smoke.c:60-104: [58,64,139,154], then bias -58.5 + SiLU."""
+    a = ex.tensor_from(np.array([1, 2, 3, 4, 5, 6], np.float32), shape=[2, 3])
+    b = ex.tensor_from(np.array([7, 8, 9, 10, 11, 12], np.float32), shape=[3, 2])
+    c = ex.tensor([2, 2])
+    st = ex.matmul(a, b, c)
+    np.testing.assert_allclose(ex.download(c).reshape(-1), [58, 64, 139, 154], atol=1e-4)
+    assert st.has_gpu_time == 1 and st.total_flops == 24
+    bias = ex.tensor_from(np.array([-58.5, 0.0], np.float32), shape=[2])
+    ex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_SILU))])
+    out = ex.download(c).reshape(-1)
+    x = -0.5
+    assert abs(out[0] - x / (1 + math.exp(-x))) < 1e-3
+    assert abs(out[1] - 64 * (1 / (1 + math.exp(-64)))) < 1e-2
+
+
+def test_config1_512_bias_relu(ta, ex, oracle):
+    """512^3, bias[N] + ReLU, fill_det seeds 1, 2, 3."""
+    m = n = k = 512
+    ha, hb, hbias = oracle.fill_det(m * k, 1), oracle.fill_det(k * n, 2), oracle.fill_det(n, 3)
+    a, b = ex.tensor_from(ha, shape=[m, k]), ex.tensor_from(hb, shape=[k, n])
+    bias, c = ex.tensor_from(hbias, shape=[n]), ex.tensor([m, n])
+    ex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_RELU))])
+    ref = oracle.reference_gemm(ha, hb, 1, m, n, k, bias=hbias, act=1)
+    check_f32(ex.download(c), ref, k, oracle)
+
+
+@pytest.mark.parametrize("shape", [(512, 512, 512), (67, 45, 33), (130, 257, 129), (300, 520, 1000)])
+@pytest.mark.parametrize("epi", [
+    dict(bias=True), dict(act=1), dict(act=2, bias=True), dict(act=3, binary=1, beta=0.5),
+    dict(binary=2), dict(alpha=0.25, accumulate=True, act=3), dict(bias=True, act=2, binary=2),
+])
+def test_epilogues(ta, ex, oracle, shape, epi):
+    m, n, k = shape
+    epi = dict(epi)
+    bias = [n] if epi.pop("bias", False) else None
+    run_case(ta, ex, oracle, m, n, k, bias=bias, **epi)
+
+
+@pytest.mark.parametrize("ba,bb,bc", [(3, 1, 3), (1, 3, 3), (1, 1, 3), (3, 3, 3)])
+def test_batch_broadcast(ta, ex, oracle, ba, bb, bc):
+    run_case(ta, ex, oracle, 70, 90, 50, batch_a=ba, batch_b=bb, batch_c=bc, bias=[bc, 90], act=1)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (1, 7, 3), (5, 1, 9), (3, 4, 1), (17, 19, 23),
+                                   (64, 64, 64), (65, 63, 17), (255, 257, 31), (256, 256, 16)])
+def test_ragged_shapes(ta, ex, oracle, shape):
+    run_case(ta, ex, oracle, *shape)
+
+
+def test_property_random_shapes(ta, ex, oracle):
+    """tests/correctness/property.rs:5-63: 32 random shapes from LcgRng(0xC0FFEE)."""
+    dims = oracle.lcg_range(0xC0FFEE, 1, 300, 32 * 3).reshape(32, 3)
+    for m, n, k in dims:
+        run_case(ta, ex, oracle, int(m), int(n), int(k), seed=int(m) + 7)
+
+
+def gemm_kernels(ta):
+    return [n for n in ta.kernel_names() if n.startswith("f32_m")]
+
+
+@pytest.mark.parametrize("shape", [(300, 200, 77), (512, 256, 128), (37, 41, 1088)])
+def test_every_f32_kernel(ta, ctx, oracle, shape):
+    """tests/correctness/kernels.rs:7-76: every registry GEMM agrees with the oracle."""
+    for name in gemm_kernels(ta):
+        kex = ta.Executor(ctx, kernel_selection=name, tune=False)
+        run_case(ta, kex, oracle, *shape, bias=[shape[1]], act=3, kernel_ex=kex)
+        kex.close()
+
+
+@pytest.mark.parametrize("shape", [(256, 384, 256), (100, 130, 70)])
+def test_f16w_gemm(ta, ctx, ex, oracle, shape):
+    """f16 B widened exactly: parity against cpu_bmm on the f16-rounded B (f16.rs:65-122)."""
+    m, n, k = shape
+    ha, hb = oracle.fill_det(m * k, 81), oracle.fill_det(k * n, 82)
+    hbr = oracle.round_via_f16(hb)
+    for name in [None] + [n_ for n_ in ta.kernel_names() if n_.startswith("f16w_m")]:
+        kex = ex if name is None else ta.Executor(ctx, kernel_selection=name, tune=False)
+        a = kex.tensor_from(ha, shape=[m, k])
+        b = kex.tensor_from(hb, shape=[k, n], f16=True)
+        c = kex.tensor([m, n])
+        kex.matmul(a, b, c)
+        check_f32(kex.download(c), oracle.cpu_bmm(ha, hbr, None, 1, m, n, k), k, oracle)
+
+
+def sampled_rows(ex, oracle, ha, hb, batch, m, n, k, rows):
+    """Oracle on a subset of output rows (ml-bench validate_samples style)."""
+    out = np.zeros(batch * m * n, np.float32)
+    for r in rows:
+        oracle.cpu_bmm_rows(ha, hb, batch, m, n, k, 1.0, out, r, r + 1, 0)
+    return out
+
+
+def test_config2_batched_gelu_sampled(ta, ex, oracle):
+    """BASELINE config 2a at full size: B=8, 2048^3, B broadcast, bias[8,N], GELU.
+    A ~ N(0,1), B ~ N(0, 1/sqrt(K)).  Checked on 48 sampled rows."""
+    bt, m, n, k = 8, 2048, 2048, 2048
+    ha = oracle.fill_normal(bt * m * k, 21, 1.0)
+    hb = oracle.fill_normal(k * n, 22, 1.0 / math.sqrt(k))
+    hbias = oracle.fill_det(bt * n, 23)
+    a, b = ex.tensor_from(ha, shape=[bt, m, k]), ex.tensor_from(hb, shape=[k, n])
+    bias, c = ex.tensor_from(hbias, shape=[bt, n]), ex.tensor([bt, m, n])
+    ex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_GELU))])
+    got = ex.download(c).reshape(-1)
+    rows = [int(r) for r in oracle.lcg_range(2, 0, bt * m - 1, 48)]
+    ref = sampled_rows(ex, oracle, ha, hb, bt, m, n, k, rows)
+    ref = oracle.epilogue(ref, n, m * n, hbias, n, 3)
+    idx = np.concatenate([np.arange(r * n, (r + 1) * n) for r in rows])
+    check_f32(got[idx], ref[idx], k, oracle)
+
+
+def test_4096_cube_sampled(ta, ex, oracle):
+    """Headline 4096^3 shape, bias + ReLU, uniform inputs seeds 31, 32; 24 sampled rows."""
+    m = n = k = 4096
+    ha, hb, hbias = oracle.fill_det(m * k, 31), oracle.fill_det(k * n, 32), oracle.fill_det(n, 33)
+    a, b = ex.tensor_from(ha, shape=[m, k]), ex.tensor_from(hb, shape=[k, n])
+    bias, c = ex.tensor_from(hbias, shape=[n]), ex.tensor([m, n])
+    ex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_RELU))])
+    got = ex.download(c).reshape(-1)
+    rows = [int(r) for r in oracle.lcg_range(3, 0, m - 1, 24)]
+    ref = sampled_rows(ex, oracle, ha, hb, 1, m, n, k, rows)
+    ref = oracle.epilogue(ref, n, m * n, hbias, 0, 1)
+    idx = np.concatenate([np.arange(r * n, (r + 1) * n) for r in rows])
+    check_f32(got[idx], ref[idx], k, oracle)
