@@ -1,0 +1,302 @@
+"""Benchmark of the fused-epilogue GEMM path on one MI355X.
+
+Headline (`value`): FP32 fused GEMM 4096^3 with bias[N] + ReLU (BASELINE
+config 2b), TFLOP/s over the timed steps (wall clock, inputs resident in
+HBM).  One step = one `ta_run_ops` call of that fused op.  The same JSON
+line carries, under "secondary", the decode SwiGLU MLP GEMVs (config 3,
+HBM GB/s with weight copies rotated past the 256 MB last-level cache),
+the batched GELU GEMM (config 2a), the deterministic split-K shapes
+(config 4) and the TinyLlama-shaped prefill GEMMs (config 5).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+
+Synthetic inputs from numpy's PCG64 (seeded); no dataset or checkpoint.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "tensor-ash_amd"))
+
+PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense FP32 matrix
+PEAK_FP16_MFMA = 2516.6  # TFLOP/s, dense
+PEAK_HBM = 8000.0  # GB/s
+METRIC = "fused-GEMM TFLOP/s at 4096^3 f32 + decode-GEMV HBM GB/s (f16 W), 1 MI355X"
+LLC_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def median_ns(stats_list):
+    return statistics.median([s.gpu_time_ns for s in stats_list])
+
+
+def headline(ta, ex, steps: int, warmup: int):
+    m = n = k = 4096
+    rng = np.random.default_rng(31)
+    ha = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    hb = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    hbias = rng.uniform(-1, 1, n).astype(np.float32)
+    a, b = ex.tensor_from(ha), ex.tensor_from(hb)
+    bias, c = ex.tensor_from(hbias), ex.tensor([m, n])
+    op = ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_RELU))
+    for _ in range(warmup):
+        ex.run_ops([op])
+    stats = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        stats.append(ex.run_ops([op]))
+    wall = time.perf_counter() - t0
+    flops = 2.0 * m * n * k
+    kernel_ns = statistics.mean(s.gpu_time_ns for s in stats)
+    # post-timing validation on 8 rows against float64 numpy
+    got = ex.download(c)
+    rows = rng.integers(0, m, 8)
+    ref = np.maximum(ha[rows].astype(np.float64) @ hb.astype(np.float64) + hbias, 0.0)
+    rel = float(np.max(np.abs(got[rows] - ref)) / np.max(np.abs(ref)))
+    info = ex.dispatch_info_for(1, m, n, k)
+    return dict(
+        wall_s=wall, ms_per_step=wall / steps * 1e3, value=flops / (wall / steps) / 1e12,
+        kernel_ms=kernel_ns / 1e6, achieved=flops / kernel_ns / 1e3, kernel=info["kernel"],
+        rel_err=rel, inputs=(ha, hb),
+    )
+
+
+def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=60):
+    """Config 3: h = silu(x@Wg) * (x@Wu); y = h@Wd + res, packed f16 weights.
+    The op graph is prepared once per weight copy (hipGraph: one dual
+    gate/up GEMV launch + one down GEMV launch) and copies are rotated so
+    the working set (5 x 69 MB) exceeds the 256 MB last-level cache."""
+    hdim, ffn = 2048, 5632
+    w_bytes = 2 * (2 * hdim * ffn) + 2 * ffn * hdim
+    copies = max(5, math.ceil(LLC_BYTES / w_bytes) + 1)
+    rng = np.random.default_rng(41)
+    weights = []
+    for i in range(copies):
+        ws = []
+        for (kk, nn) in ((hdim, ffn), (hdim, ffn), (ffn, hdim)):
+            w = (rng.standard_normal(kk * nn, dtype=np.float32) * 0.02).astype(np.float32)
+            ws.append(ex.tensor_from(ta.pack_f16w_row_tiles(w, kk, nn, ta.f16w_row_tile_n(kk, nn)),
+                                     shape=[kk, nn], f16=True))
+        weights.append(ws)
+    out = {}
+    for m in rows_list:
+        x = ex.tensor_from(rng.uniform(-1, 1, (m, hdim)).astype(np.float32))
+        res = ex.tensor_from(rng.uniform(-1, 1, (m, hdim)).astype(np.float32))
+        up, h, y = ex.tensor([m, ffn]), ex.tensor([m, ffn]), ex.tensor([m, hdim])
+        preps = []
+        for (wg, wu, wd) in weights:
+            ops = [ta.MatmulOp(x, wu, up, packed_b=True),
+                   ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=ta.ACTIVATION_SILU,
+                                                              binary=ta.BINARY_MUL, d=up), packed_b=True),
+                   ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=res, beta=1.0),
+                               packed_b=True)]
+            preps.append(ex.prepare_op_graph(ops))
+        for i in range(2 * copies):
+            preps[i % copies].run()
+        stats = []
+        t0 = time.perf_counter()
+        for i in range(iters):
+            stats.append(preps[i % copies].run())
+        wall = time.perf_counter() - t0
+        bytes_step = w_bytes + 4 * m * (hdim + 2 * ffn + 2 * hdim)
+        step_ns = median_ns(stats)
+        out[f"M{m}"] = dict(step_us=step_ns / 1e3, gbps=bytes_step / step_ns,
+                            frac_hbm=bytes_step / step_ns / PEAK_HBM, bytes_per_step=bytes_step,
+                            wall_us_per_step=wall / iters * 1e6)
+        for p in preps:
+            p.close()
+    return out
+
+
+def batched_gelu(ta, ex, iters=10):
+    bt, m, n, k = 8, 2048, 2048, 2048
+    rng = np.random.default_rng(21)
+    a = ex.tensor_from(rng.standard_normal((bt, m, k), dtype=np.float32))
+    b = ex.tensor_from((rng.standard_normal((k, n), dtype=np.float32) / math.sqrt(k)).astype(np.float32))
+    bias = ex.tensor_from(rng.uniform(-1, 1, (bt, n)).astype(np.float32))
+    c = ex.tensor([bt, m, n])
+    op = ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_GELU))
+    for _ in range(3):
+        ex.run_ops([op])
+    ns = median_ns([ex.run_ops([op]) for _ in range(iters)])
+    flops = 2.0 * bt * m * n * k
+    return dict(kernel_ms=ns / 1e6, tflops=flops / ns / 1e3, frac=flops / ns / 1e3 / PEAK_FP32_MFMA,
+                kernel=ex.dispatch_info_for(bt, m, n, k)["kernel"])
+
+
+def splitk(ta, ex, iters=10):
+    out = {}
+    rng = np.random.default_rng(51)
+    for (m, n, k) in ((64, 256, 65536), (32, 128, 131072)):
+        copies = 4
+        As = [ex.tensor_from(rng.uniform(-1, 1, (m, k)).astype(np.float32)) for _ in range(copies)]
+        Bs = [ex.tensor_from(rng.uniform(-1, 1, (k, n)).astype(np.float32)) for _ in range(copies)]
+        c = ex.tensor([m, n])
+        flops = 2.0 * m * n * k
+        bytes_ = 4.0 * (m * k + k * n + m * n)
+        for s in (8, 16, 32, 0):
+            for i in range(copies):
+                ex.run_matmuls_split_k2(As[i], Bs[i], c, s)
+            ns = median_ns([ex.run_matmuls_split_k2(As[i % copies], Bs[i % copies], c, s)
+                            for i in range(iters)])
+            key = f"{m}x{n}x{k}_S{s if s else 'auto'}"
+            out[key] = dict(us=ns / 1e3, tflops=flops / ns / 1e3, gbps=bytes_ / ns,
+                            frac_mfma=flops / ns / 1e3 / PEAK_FP32_MFMA, frac_hbm=bytes_ / ns / PEAK_HBM)
+    return out
+
+
+def prefill_layer(ta, ex, iters=10):
+    """Config 5 GEMMs (TinyLlama-1.1B-shaped, seq 512, f16 weights, f32 acts)."""
+    s, hid, ffn, qkv = 512, 2048, 5632, 2560
+    rng = np.random.default_rng(61)
+    wt = lambda k, n: ex.tensor_from((rng.standard_normal((k, n), dtype=np.float32) * 0.02), f16=True)
+    x = ex.tensor_from(rng.uniform(-1, 1, (s, hid)).astype(np.float32))
+    attn = ex.tensor_from(rng.uniform(-1, 1, (s, hid)).astype(np.float32))
+    wq, wo, wg, wu, wd = wt(hid, qkv), wt(hid, hid), wt(hid, ffn), wt(hid, ffn), wt(ffn, hid)
+    q, o, up, h, y = ex.tensor([s, qkv]), ex.tensor([s, hid]), ex.tensor([s, ffn]), ex.tensor([s, ffn]), ex.tensor([s, hid])
+    cases = {
+        "qkv_512x2560x2048": [ta.MatmulOp(x, wq, q)],
+        "o_512x2048x2048": [ta.MatmulOp(attn, wo, o, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0))],
+        "up_512x5632x2048": [ta.MatmulOp(x, wu, up)],
+        "gate_silu_mul_512x5632x2048": [ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=2, binary=2, d=up))],
+        "down_512x2048x5632": [ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=1, d=x, beta=1.0))],
+    }
+    out = {}
+    total_ns = 0.0
+    total_flops = 0.0
+    for name, ops in cases.items():
+        for _ in range(3):
+            ex.run_ops(ops)
+        ns = median_ns([ex.run_ops(ops) for _ in range(iters)])
+        dims = [int(v) for v in name.split("_")[-1].split("x")]
+        flops = 2.0 * dims[0] * dims[1] * dims[2]
+        out[name] = dict(us=ns / 1e3, tflops=flops / ns / 1e3)
+        total_ns += ns
+        total_flops += flops
+    out["layer_gemms"] = dict(us=total_ns / 1e3, tflops=total_flops / total_ns / 1e3)
+    return out
+
+
+def cpu_baseline(inputs, target_s: float = 12.0):
+    """The oracle's cpu_bmm (restatement of tools/test-support cpu_bmm:
+    naive i-j-k, f64 accumulate) on host cores, over a bounded sample of
+    output rows of the same 4096^3 problem."""
+    import oracle
+    ha, hb = inputs
+    m, k = ha.shape
+    n = hb.shape[1]
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    a = np.ascontiguousarray(ha).reshape(-1)
+    b = np.ascontiguousarray(hb).reshape(-1)
+    out = np.zeros(m * n, np.float32)
+    rows = threads
+    t0 = time.perf_counter()
+    oracle.cpu_bmm_rows(a, b, 1, m, n, k, 1.0, out, 0, rows, threads)
+    dt = time.perf_counter() - t0
+    if dt < target_s / 4:
+        more = int(rows * (target_s - dt) / max(dt, 1e-3))
+        more = max(threads, min(more - more % threads, m - rows))
+        t1 = time.perf_counter()
+        oracle.cpu_bmm_rows(a, b, 1, m, n, k, 1.0, out, rows, rows + more, threads)
+        dt += time.perf_counter() - t1
+        rows += more
+    flops = 2.0 * rows * n * k
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"cpu_bmm (f64-accumulate i-j-k oracle) on {rows} of 4096 output rows of the "
+                       f"4096^3 GEMM, {dt:.1f} s on {threads} threads, extrapolation-free rate")
+
+
+def load_traffic():
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled), or None."""
+    p = ROOT / "profiles" / "gemm_f32_4096_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("traffic_bytes")
+        except Exception:
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--sections", default="decode,gelu,splitk,prefill",
+                    help="comma list of secondary sections to run")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is described in DESIGN.md but not built", file=sys.stderr)
+        return 2
+    import tensor_ash as ta
+
+    ctx = ta.Context()
+    ex = ta.Executor(ctx, tune=False)
+    log("headline 4096^3 f32 fused GEMM ...")
+    hl = headline(ta, ex, args.steps, args.warmup)
+    secondary = {}
+    sections = set() if args.only_headline else set(args.sections.split(","))
+    if "decode" in sections:
+        log("decode SwiGLU MLP ...")
+        secondary["decode_swiglu_mlp_f16w"] = decode_mlp(ta, ex)
+    if "gelu" in sections:
+        log("batched GELU GEMM ...")
+        secondary["batched_gelu_8x2048^3"] = batched_gelu(ta, ex)
+    if "splitk" in sections:
+        log("split-K ...")
+        secondary["splitk_f32"] = splitk(ta, ex)
+    if "prefill" in sections:
+        log("prefill layer GEMMs ...")
+        secondary["prefill_tinyllama_m512_f16w"] = prefill_layer(ta, ex)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(hl["inputs"])
+    flops = 2.0 * 4096 ** 3
+    line = {
+        "metric": METRIC,
+        "value": round(hl["value"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(hl["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (numpy PCG64 uniform[-1,1]; inputs resident in HBM)",
+        "config": {"workload": "gemm_f32_4096x4096x4096_bias_relu (BASELINE config 2b)",
+                   "kernel": hl["kernel"], "m": 4096, "n": 4096, "k": 4096,
+                   "epilogue": "bias[N]+relu", "validation_rel_err": hl["rel_err"]},
+        "roofline": {"bound": "mfma", "achieved": round(hl["achieved"], 3), "peak": PEAK_FP32_MFMA,
+                     "unit": "TFLOP/s", "frac": round(hl["achieved"] / PEAK_FP32_MFMA, 4),
+                     "traffic": load_traffic(), "kernel_ms": round(hl["kernel_ms"], 4),
+                     "flops_per_launch": flops},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -11,15 +11,16 @@
 // stride TW, row stride N).
 //
 // Work decomposition: workgroup (256 threads = 4 waves) = one TW-column
-// tile x one window of `kchunk` K rows.  A lane owns two adjacent columns
-// (one 32-bit f16 pair, or one 64-bit f32 pair), TW/2 lanes span a row,
-// so a wave instruction reads 64*4 = 256 contiguous bytes of the packed
-// tile.  Each lane issues UNROLL independent loads before its FMAs, giving
-// ~32-64 KiB in flight per workgroup.  X for the window sits in LDS as
-// [k][MR] so one k costs MR/4 128-bit broadcast reads.
+// tile x one window of `kchunk` K rows.  A lane owns CPL adjacent columns
+// read with one 64-bit load (four f16 or two f32), TW/CPL lanes span a
+// row, so one wave instruction reads 512 contiguous bytes of the packed
+// tile.  Each lane issues all kUnroll loads of a group unconditionally
+// (rows past the window re-read a valid row and are zeroed afterwards) so
+// they are in flight together.  X for the window sits in LDS as [k][MR]
+// so one k costs MR/4 128-bit broadcast reads.
 //
 // Reduction, fixed order throughout (bit-reproducible):
-//   rows of a wave   -> xor shuffles across the 64/(TW/2) row groups;
+//   rows of a wave   -> xor shuffles across the 64/(TW/CPL) row groups;
 //   waves            -> LDS, summed wave 0..3;
 //   K windows        -> every workgroup stores its partial, the last one
 //                       of a tile to arrive (integer counter) sums windows
@@ -34,24 +35,26 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxChunk = 512;
-constexpr int kUnroll = 16;
 
 template <int MR, bool DUAL, int TW, bool WF32>
 struct Gemv {
   static constexpr int WAYS = DUAL ? 2 : 1;
-  static constexpr int LPR = TW / 2;   // lanes per weight row
-  static constexpr int RPI = 64 / LPR; // rows per wave instruction
-  static constexpr int RPW = RPI * kWaves; // rows per workgroup step
-  typedef typename std::conditional<WF32, uint64_t, uint32_t>::type Raw;
+  static constexpr int kMaxChunk = 4096 / MR; // X-window rows held in LDS (16 KiB)
+  static constexpr int CPL = WF32 ? 2 : 4;   // columns per lane (8-byte load)
+  static constexpr int LPR = TW / CPL;       // lanes per weight row
+  static constexpr int RPI = 64 / LPR;       // rows per wave instruction
+  static constexpr int RPW = RPI * kWaves;   // rows per workgroup step
+  static constexpr int EB = WF32 ? 4 : 2;    // bytes per weight element
+  static constexpr int kUnroll = 16; // loads per weight matrix per group
 
-  static TA_DEVICE void unpack(Raw raw, float &lo, float &hi) {
+  static TA_DEVICE void unpack(uint64_t raw, float (&v)[CPL]) {
     if constexpr (WF32) {
-      lo = __builtin_bit_cast(float, (uint32_t)raw);
-      hi = __builtin_bit_cast(float, (uint32_t)(raw >> 32));
+      v[0] = __builtin_bit_cast(float, (uint32_t)raw);
+      v[1] = __builtin_bit_cast(float, (uint32_t)(raw >> 32));
     } else {
-      lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw & 0xffffu));
-      hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> 16));
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        v[c] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> (16 * c)));
     }
   }
 
@@ -68,53 +71,69 @@ struct Gemv {
     const uint32_t kend = min(p.k, k0 + p.kchunk);
     const bool packed = p.flags & TA_GEMV_PACKED;
 
-    // X window -> LDS as [k][MR], zero rows past `rows` and k past kend.
-    for (uint32_t i = tid; i < p.kchunk * MR; i += kThreads) {
+    const uint32_t cp = lane % LPR, r0 = lane / LPR;
+    // Lanes past N (row-major, ragged last tile) read column 0 of the tile
+    // and have their values discarded: every load below is unconditional,
+    // so the compiler keeps all of a group's loads in flight.
+    const uint32_t col = tile * TW + CPL * cp;
+    const bool col_ok = col + CPL <= p.n; // host requires N % CPL == 0
+    const uint64_t tile_base = packed ? (uint64_t)tile * p.k * TW : (uint64_t)tile * TW;
+    const uint64_t row_stride = (packed ? TW : p.n) * (uint64_t)EB;
+    const uint64_t lane_off = (tile_base + (col_ok ? CPL * cp : 0)) * EB;
+    const char *wp[WAYS];
+    wp[0] = reinterpret_cast<const char *>(p.w) + lane_off;
+    if constexpr (DUAL)
+      wp[1] = reinterpret_cast<const char *>(p.w2) + lane_off;
+    const uint32_t my_first = wave * RPI + r0;
+    constexpr uint32_t G = RPW * kUnroll; // rows per unrolled group
+
+    // One group of loads; rows at or past kend re-read row k0 (valid, and
+    // zeroed before use), so the loads carry no branches.
+    auto issue = [&](uint32_t kb, uint64_t (&raw)[WAYS][kUnroll]) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t k = k0 + kb + u * RPW + my_first;
+        const uint32_t kc = k < kend ? k : k0;
+#pragma unroll
+        for (int w = 0; w < WAYS; ++w)
+          raw[w][u] = __builtin_nontemporal_load(
+              reinterpret_cast<const uint64_t *>(wp[w] + (uint64_t)kc * row_stride));
+      }
+    };
+
+    // X loads go out first, then the first weight group: vmcnt retires in
+    // issue order, so staging X into LDS then waits only for X.
+    constexpr int XPT = kMaxChunk * MR / kThreads;
+    float xr[XPT];
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+      const uint32_t i = tid + j * kThreads;
       const uint32_t kk = i / MR, m = i % MR;
-      xs[i] = (m < p.rows && k0 + kk < kend) ? p.x[(uint64_t)m * p.k + k0 + kk] : 0.0f;
+      const bool ok = i < p.kchunk * MR && m < p.rows && k0 + kk < kend;
+      xr[j] = p.x[ok ? (uint64_t)m * p.k + k0 + kk : 0];
+      xr[j] = ok ? xr[j] : 0.0f;
     }
+    uint64_t cur[WAYS][kUnroll];
+    issue(0, cur);
+#pragma unroll
+    for (int j = 0; j < XPT; ++j)
+      xs[tid + j * kThreads] = xr[j];
     __syncthreads();
 
-    const uint32_t cp = lane % LPR, r0 = lane / LPR;
-    const uint32_t col = tile * TW + 2 * cp;
-    const bool col_ok = col < p.n; // N % 2 == 0 is required by the host
-    const uint64_t tile_base = packed ? (uint64_t)tile * p.k * TW : (uint64_t)tile * TW;
-    const uint64_t row_stride = packed ? TW : p.n;
-    const Raw *wp[WAYS];
-    wp[0] = reinterpret_cast<const Raw *>(
-        reinterpret_cast<const char *>(p.w) + (tile_base + 2 * cp) * (WF32 ? 4 : 2));
-    if constexpr (DUAL)
-      wp[1] = reinterpret_cast<const Raw *>(
-          reinterpret_cast<const char *>(p.w2) + (tile_base + 2 * cp) * (WF32 ? 4 : 2));
-
-    float acc[WAYS][MR][2];
+    float acc[WAYS][MR][CPL];
 #pragma unroll
     for (int w = 0; w < WAYS; ++w)
 #pragma unroll
       for (int m = 0; m < MR; ++m)
-        acc[w][m][0] = acc[w][m][1] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+          acc[w][m][c] = 0.0f;
 
-    const uint32_t my_first = wave * RPI + r0; // row offset inside a step
-    const uint32_t steps = (p.kchunk + RPW - 1) / RPW;
-    for (uint32_t s0 = 0; s0 < steps; s0 += kUnroll) {
-      Raw raw[WAYS][kUnroll];
+    auto consume = [&](uint32_t kb, const uint64_t (&raw)[WAYS][kUnroll]) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t kk = (s0 + u) * RPW + my_first;
-        const uint32_t k = k0 + kk;
-        const bool ok = col_ok && kk < p.kchunk && k < kend;
-#pragma unroll
-        for (int w = 0; w < WAYS; ++w)
-          raw[w][u] = ok ? *reinterpret_cast<const Raw *>(
-                               reinterpret_cast<const char *>(wp[w]) +
-                               (uint64_t)k * row_stride * (WF32 ? 4 : 2))
-                         : (Raw)0;
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t kk = (s0 + u) * RPW + my_first;
-        if (kk >= p.kchunk)
-          break;
+        const uint32_t kk = kb + u * RPW + my_first;
+        const bool ok = k0 + kk < kend && col_ok;
         float xv[MR];
         if constexpr (MR >= 4) {
 #pragma unroll
@@ -132,15 +151,24 @@ struct Gemv {
         }
 #pragma unroll
         for (int w = 0; w < WAYS; ++w) {
-          float lo, hi;
-          unpack(raw[w][u], lo, hi);
+          float wv[CPL];
+          unpack(ok ? raw[w][u] : 0ull, wv);
 #pragma unroll
-          for (int m = 0; m < MR; ++m) {
-            acc[w][m][0] = fmaf(xv[m], lo, acc[w][m][0]);
-            acc[w][m][1] = fmaf(xv[m], hi, acc[w][m][1]);
-          }
+          for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+              acc[w][m][c] = fmaf(xv[m], wv[c], acc[w][m][c]);
         }
       }
+    };
+
+    // kchunk is a multiple of G (host contract): whole groups only.  The
+    // resident grid (every workgroup of a decode launch fits at once)
+    // keeps HBM busy while each wave waits on its own group.
+    consume(0, cur);
+    for (uint32_t kb = G; kb < p.kchunk; kb += G) {
+      issue(kb, cur);
+      consume(kb, cur);
     }
 
     // Rows of one wave: lanes cp, cp + LPR, ... hold the same columns.
@@ -149,18 +177,19 @@ struct Gemv {
 #pragma unroll
       for (int w = 0; w < WAYS; ++w)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-          acc[w][m][0] += __shfl_xor(acc[w][m][0], off);
-          acc[w][m][1] += __shfl_xor(acc[w][m][1], off);
-        }
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+          for (int c = 0; c < CPL; ++c)
+            acc[w][m][c] += __shfl_xor(acc[w][m][c], off);
     if (r0 == 0) {
 #pragma unroll
       for (int w = 0; w < WAYS; ++w)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          float *dst = &red[((wave * WAYS + w) * MR + m) * TW + 2 * cp];
-          dst[0] = acc[w][m][0];
-          dst[1] = acc[w][m][1];
+          float *dst = &red[((wave * WAYS + w) * MR + m) * TW + CPL * cp];
+#pragma unroll
+          for (int c = 0; c < CPL; ++c)
+            dst[c] = acc[w][m][c];
         }
     }
     __syncthreads();
@@ -181,38 +210,62 @@ struct Gemv {
     }
 
     if (p.kchunks > 1) {
+      // Cross-XCD hand-off without an L2 write-back: partials are written
+      // and read only with agent-scope relaxed atomics (sc1 loads/stores,
+      // coherent per location across the XCDs' L2s).  Waiting for this
+      // thread's stores to complete before the barrier makes them visible
+      // before thread 0 bumps the tile counter (release); the last
+      // workgroup reads them after observing the count (acquire by control
+      // dependency).  __threadfence() would instead write back and
+      // invalidate the whole L2 in every workgroup.
       float *mine = p.partial + ((uint64_t)chunk * tiles + tile) * OUTS;
 #pragma unroll
       for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
         const uint32_t o = tid + i * kThreads;
         if (o < OUTS)
-          mine[o] = part[i];
+          __hip_atomic_store(mine + o, part[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __threadfence();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (tid == 0) {
-        const uint32_t seen = atomicAdd(&p.counters[tile], 1u);
+        const uint32_t seen =
+            __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last_flag = (seen == p.kchunks - 1) ? 1u : 0u;
       }
       __syncthreads();
       if (!last_flag)
         return;
-      __threadfence();
+      // Sum the windows in order 0..kchunks-1.  All partial loads of a
+      // batch go out at once (one memory round trip) into the X window's
+      // LDS, which is free now; then each output is summed sequentially.
+      const uint64_t step = (uint64_t)tiles * OUTS;
+      const float *tsrc = p.partial + (uint64_t)tile * OUTS;
+      constexpr uint32_t NB = (kMaxChunk * MR) / OUTS; // windows per batch
+      float sum[(OUTS + kThreads - 1) / kThreads];
 #pragma unroll
-      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
-        const uint32_t o = tid + i * kThreads;
-        float s = 0.0f;
-        if (o < OUTS) {
-          const float *src = p.partial + (uint64_t)tile * OUTS + o;
-          const uint64_t step = (uint64_t)tiles * OUTS;
-          s = __builtin_nontemporal_load(src);
-          for (uint32_t c = 1; c < p.kchunks; ++c)
-            s += __builtin_nontemporal_load(src + c * step);
+      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i)
+        sum[i] = 0.0f;
+      for (uint32_t c0 = 0; c0 < p.kchunks; c0 += NB) {
+        const uint32_t nb = min(NB, p.kchunks - c0);
+        __syncthreads(); // previous batch fully consumed
+        for (uint32_t e = tid; e < nb * OUTS; e += kThreads) {
+          const uint32_t c = c0 + e / OUTS, o = e % OUTS;
+          xs[e] = __hip_atomic_load(tsrc + c * step + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        part[i] = s;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
+          const uint32_t o = tid + i * kThreads;
+          if (o < OUTS)
+            for (uint32_t c = 0; c < nb; ++c)
+              sum[i] = (c0 + c == 0) ? xs[o] : sum[i] + xs[c * OUTS + o];
+        }
       }
+#pragma unroll
+      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i)
+        part[i] = sum[i];
       if (tid == 0)
-        atomicExch(&p.counters[tile], 0u);
+        __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // Epilogue (shaders/matmul_epilogue_common.glsl:14-21 order).

@@ -218,7 +218,8 @@ struct ExecutorImpl {
     if (p.splitk2) {
       need.splitk = (uint64_t)d.batch * d.m * d.n * *p.splitk2 * 4;
     } else if (s.is_gemv()) {
-      GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, p.role == 2);
+      GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, p.role == 2,
+                            gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, p.role == 2));
       need.partial = g.partial_bytes;
       need.counters = g.tiles;
     }
@@ -282,7 +283,8 @@ struct ExecutorImpl {
   void launch_gemv(const KernelSpec &s, const ResolvedMatmul &d, const MatmulOp &op,
                    const MatmulOp *up, Scratch &scratch, hipStream_t stream) const {
     const bool dual = up != nullptr;
-    GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, dual);
+    GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, dual,
+                          gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, dual));
     GemvArgs a{};
     a.x = static_cast<const float *>(op.call.a->device_ptr());
     a.w = static_cast<const uint16_t *>(op.call.b->device_ptr());

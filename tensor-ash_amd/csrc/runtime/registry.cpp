@@ -97,7 +97,7 @@ bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
   case KernelKind::GemmF16Mfma:
     return d.b_f16;
   case KernelKind::GemvF16Row:
-    return d.b_f16 && d.batch == 1 && d.m <= kGemvMaxRows && d.n % 2 == 0;
+    return d.b_f16 && d.batch == 1 && d.m <= kGemvMaxRows && d.n % 4 == 0;
   case KernelKind::GemvF32Row:
     return !d.b_f16 && d.batch == 1 && d.m <= kGemvMaxRows && d.n % 2 == 0;
   case KernelKind::GemvF16Packed:
@@ -116,7 +116,7 @@ size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t
   (void)k;
   if (packed_b)
     return registry_index(n % 64 == 0 ? "f16w_gemv_packed_t64" : "f16w_gemv_packed_t32");
-  if (batch == 1 && m <= kGemvMaxRows && n % 2 == 0)
+  if (batch == 1 && m <= kGemvMaxRows && n % (b_f16 ? 4 : 2) == 0)
     return registry_index(b_f16 ? "f16w_gemv_row" : "f32_gemv_row");
   static const char *f32_tiles[] = {"f32_m256n256", "f32_m256n128", "f32_m128n128",
                                     "f32_m128n64", "f32_m64n64"};
@@ -222,16 +222,28 @@ std::optional<uint64_t> checked_auto_scratch_end(uint64_t offset, uint64_t bytes
 }
 
 // ---- GEMV geometry ----
-// ~3 workgroups per CU: K windows of 64..512 rows (multiple of 64).
-GemvPlan plan_gemv(uint32_t cus, uint32_t rows, uint32_t n, uint32_t k, uint32_t tw, bool dual) {
+// K granularity of a GEMV window: one unrolled load group of the kernel
+// (4 waves x 64/(TW/CPL) rows x 16 loads; CPL = 4 for f16, 2 for f32).
+uint32_t gemv_unit(uint32_t tw, bool f32_weights, bool /*dual*/) {
+  const uint32_t cpl = f32_weights ? 2 : 4;
+  return 4 * (64 / (tw / cpl)) * 16;
+}
+
+// ~3 workgroups per CU: K windows of at most 512 rows, a multiple of the
+// kernel's unrolled group (host contract of the GEMV kernels).
+GemvPlan plan_gemv(uint32_t cus, uint32_t rows, uint32_t n, uint32_t k, uint32_t tw, bool dual,
+                   uint32_t unit) {
   GemvPlan p;
   p.tw = tw;
   p.mr = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
   p.tiles = div_ceil(n, tw);
   const uint32_t wanted = std::max(1u, div_ceil(3 * cus, p.tiles));
   uint32_t kchunk = div_ceil(k, wanted);
-  kchunk = div_ceil(kchunk, 64) * 64;
-  kchunk = std::clamp(kchunk, 64u, 512u);
+  if (const char *env = std::getenv("TA_GEMV_KCHUNK"))
+    kchunk = (uint32_t)std::strtoul(env, nullptr, 10);
+  kchunk = div_ceil(kchunk, unit) * unit;
+  const uint32_t cap = 4096 / p.mr; // X-window rows the kernel stages in LDS
+  kchunk = std::clamp(kchunk, unit, std::max(unit, cap / unit * unit));
   p.kchunk = kchunk;
   p.kchunks = div_ceil(k, kchunk);
   p.partial_bytes =
