@@ -205,13 +205,13 @@ def cpu_baseline(inputs, target_s: float = 12.0):
     out = np.zeros(m * n, np.float32)
     rows = threads
     t0 = time.perf_counter()
-    oracle.cpu_bmm_rows(a, b, 1, m, n, k, 1.0, out, 0, rows, threads)
+    oracle.cpu_bmm_rows(a, b, 1, m, n, k, 1.0, out, 0, rows, threads, reference_order=True)
     dt = time.perf_counter() - t0
     if dt < target_s / 4:
         more = int(rows * (target_s - dt) / max(dt, 1e-3))
         more = max(threads, min(more - more % threads, m - rows))
         t1 = time.perf_counter()
-        oracle.cpu_bmm_rows(a, b, 1, m, n, k, 1.0, out, rows, rows + more, threads)
+        oracle.cpu_bmm_rows(a, b, 1, m, n, k, 1.0, out, rows, rows + more, threads, reference_order=True)
         dt += time.perf_counter() - t1
         rows += more
     flops = 2.0 * rows * n * k

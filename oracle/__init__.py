@@ -35,7 +35,7 @@ _sig("ta_oracle_lcg_range", C.c_int, C.c_uint64, C.c_uint32, C.c_uint32, _U32, C
 _sig("ta_oracle_cpu_bmm", C.c_int, _F, C.c_size_t, _F, C.c_size_t, _F, C.c_uint32, C.c_uint32,
      C.c_uint32, C.c_uint32, C.c_float, C.c_int, _F)
 _sig("ta_oracle_cpu_bmm_rows", C.c_int, _F, C.c_size_t, _F, C.c_size_t, C.c_uint32, C.c_uint32,
-     C.c_uint32, C.c_uint32, C.c_float, _F, C.c_uint64, C.c_uint64, C.c_int)
+     C.c_uint32, C.c_uint32, C.c_float, _F, C.c_uint64, C.c_uint64, C.c_int, C.c_int)
 _sig("ta_oracle_max_threads", C.c_int)
 _sig("ta_oracle_max_abs_err", C.c_float, _F, _F, C.c_size_t, C.POINTER(C.c_size_t))
 _sig("ta_oracle_tolerance", C.c_float, C.c_uint32)
@@ -95,9 +95,13 @@ def cpu_bmm(a, b, c_init, batch: int, m: int, n: int, k: int, alpha: float = 1.0
     return out
 
 
-def cpu_bmm_rows(a, b, batch, m, n, k, alpha, out, row_begin, row_end, threads=0) -> None:
+def cpu_bmm_rows(a, b, batch, m, n, k, alpha, out, row_begin, row_end, threads=0,
+                 reference_order=False) -> None:
+    """Rows [row_begin, row_end) of cpu_bmm (parallel, bit-identical to it).
+    reference_order=True uses the reference's j-outer/k-inner loop (slow;
+    for timing the CPU baseline)."""
     rc = _lib.ta_oracle_cpu_bmm_rows(_f(a), a.size, _f(b), b.size, batch, m, n, k, alpha, _f(out),
-                                     row_begin, row_end, threads)
+                                     row_begin, row_end, threads, int(reference_order))
     if rc != 0:
         raise ValueError("cpu_bmm_rows: bad shapes")
 

@@ -31,6 +31,7 @@
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -92,16 +93,36 @@ void ta_oracle_fill_normal(float *out, size_t len, uint64_t seed,
 }
 
 /* One output row of tools/test-support/src/lib.rs:66-135 (cpu_bmm): f64
- * accumulation over k in order, cast to f32, times alpha in f32, plus the
- * old C value in f32 when accumulating. */
+ * accumulation over k in ascending order, cast to f32, times alpha in f32,
+ * plus the old C value in f32 when accumulating.  The loops run k-outer /
+ * j-inner over a row of f64 accumulators so B is read contiguously; every
+ * output still adds its K products in the same (ascending k) order as the
+ * reference's j-outer / k-inner loop, so the result is bit-identical. */
 static void bmm_row(const float *a, const float *b, float *c, uint32_t n,
-                    uint32_t k, float alpha, int accumulate) {
+                    uint32_t k, float alpha, int accumulate, double *acc) {
+  for (uint32_t j = 0; j < n; ++j)
+    acc[j] = 0.0;
+  for (uint32_t kk = 0; kk < k; ++kk) {
+    const double av = (double)a[kk];
+    const float *brow = b + (size_t)kk * n;
+    for (uint32_t j = 0; j < n; ++j)
+      acc[j] += av * (double)brow[j];
+  }
+  for (uint32_t j = 0; j < n; ++j) {
+    float scaled = alpha * (float)acc[j];
+    c[j] = accumulate ? c[j] + scaled : scaled;
+  }
+}
+
+/* The reference's own loop order (j outer, k inner; lib.rs:113-127), kept
+ * for timing the CPU baseline; same sums in the same order as bmm_row. */
+static void bmm_row_ijk(const float *a, const float *b, float *c, uint32_t n,
+                        uint32_t k, float alpha) {
   for (uint32_t j = 0; j < n; ++j) {
     double acc = 0.0;
     for (uint32_t kk = 0; kk < k; ++kk)
       acc += (double)a[kk] * (double)b[(size_t)kk * n + j];
-    float scaled = alpha * (float)acc;
-    c[j] = accumulate ? c[j] + scaled : scaled;
+    c[j] = alpha * (float)acc;
   }
 }
 
@@ -135,10 +156,14 @@ int ta_oracle_cpu_bmm(const float *a, size_t a_len, const float *b,
     memmove(out, c_init, (size_t)batch * mn * sizeof(float));
   else
     memset(out, 0, (size_t)batch * mn * sizeof(float));
+  double *acc = (double *)malloc((size_t)n * sizeof(double));
+  if (!acc)
+    return -3;
   for (uint32_t bi = 0; bi < batch; ++bi)
     for (uint32_t i = 0; i < m; ++i)
       bmm_row(a + (ab ? bi * mk : 0) + (size_t)i * k, b + (bb ? bi * kn : 0),
-              out + bi * mn + (size_t)i * n, n, k, alpha, accumulate);
+              out + bi * mn + (size_t)i * n, n, k, alpha, accumulate, acc);
+  free(acc);
   return 0;
 }
 
@@ -147,12 +172,14 @@ int ta_oracle_cpu_bmm(const float *a, size_t a_len, const float *b,
  * is bit-identical to ta_oracle_cpu_bmm.  Used as the multi-core CPU
  * baseline.  `row_begin`/`row_end` bound the flattened (batch*m) row range
  * that is computed (the rest of `out` is left untouched), so a bounded
- * sample of a large GEMM can be timed. */
+ * sample of a large GEMM can be timed.  ijk != 0 runs the reference's own
+ * j-outer / k-inner loop order (the timed CPU baseline); 0 runs the
+ * cache-friendly order with identical results. */
 int ta_oracle_cpu_bmm_rows(const float *a, size_t a_len, const float *b,
                            size_t b_len, uint32_t batch, uint32_t m,
                            uint32_t n, uint32_t k, float alpha, float *out,
                            uint64_t row_begin, uint64_t row_end,
-                           int threads) {
+                           int threads, int ijk) {
   int ab, bb;
   int rc = bmm_check(a_len, b_len, batch, m, n, k, &ab, &bb);
   if (rc)
@@ -164,15 +191,33 @@ int ta_oracle_cpu_bmm_rows(const float *a, size_t a_len, const float *b,
 #ifdef _OPENMP
   if (threads > 0)
     omp_set_num_threads(threads);
-#pragma omp parallel for schedule(dynamic, 1)
 #endif
-  for (int64_t r = (int64_t)row_begin; r < (int64_t)row_end; ++r) {
-    uint64_t bi = (uint64_t)r / m, i = (uint64_t)r % m;
-    bmm_row(a + (ab ? bi * mk : 0) + i * k, b + (bb ? bi * kn : 0),
-            out + bi * mn + i * n, n, k, alpha, 0);
+  int failed = 0;
+#ifdef _OPENMP
+#pragma omp parallel reduction(| : failed)
+#endif
+  {
+    double *acc = (double *)malloc((size_t)n * sizeof(double));
+    if (!acc) {
+      failed = 1;
+    } else {
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+      for (int64_t r = (int64_t)row_begin; r < (int64_t)row_end; ++r) {
+        uint64_t bi = (uint64_t)r / m, i = (uint64_t)r % m;
+        if (ijk)
+          bmm_row_ijk(a + (ab ? bi * mk : 0) + i * k, b + (bb ? bi * kn : 0),
+                      out + bi * mn + i * n, n, k, alpha);
+        else
+          bmm_row(a + (ab ? bi * mk : 0) + i * k, b + (bb ? bi * kn : 0),
+                  out + bi * mn + i * n, n, k, alpha, 0, acc);
+      }
+      free(acc);
+    }
   }
   (void)threads;
-  return 0;
+  return failed ? -3 : 0;
 }
 
 int ta_oracle_max_threads(void) {

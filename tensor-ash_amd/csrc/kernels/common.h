@@ -66,3 +66,78 @@ TA_DEVICE void ta_tile_coords(uint32_t lin, uint32_t tiles_m, uint32_t tiles_n,
   tm = first_m + r % rows;
   tn = r / rows;
 }
+
+// Output stage shared by the MFMA GEMMs.  One 32-row block of each wave's
+// WTM x WTN sub-tile at a time goes through LDS (the K loop's buffers are
+// free after its last barrier); the wave reads its block back row-major,
+// applies the epilogue and stores 128-bit (f32) or 64-bit (f16) vectors.
+// This keeps the accumulators in registers (no dynamic indexing) and makes
+// the C/D traffic coalesced.  Accumulator layout of the 32x32 MFMAs: lane
+// l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// Split mode (num_splits > 1): alpha * partial to plane (batch*S + split).
+// C_F16: C is f16 storage (RNE), only alpha / accumulate apply.
+template <int WTM, int WTN, int FM, int FN, int T, bool C_F16>
+TA_DEVICE void ta_store_tile(float *smem, int smem_floats, const f32x16 (&acc)[FM][FN],
+                             const GemmArgs &p, uint32_t lane, uint32_t wave, uint32_t wm,
+                             uint32_t wn, uint32_t m0, uint32_t n0, uint32_t batch,
+                             uint32_t split) {
+  constexpr int LDC = WTN + 4;
+  (void)smem_floats;
+  float *Cs = smem + wave * (32 * LDC);
+  const uint32_t lr = lane & 31u, lg = lane >> 5;
+  const uint32_t S = p.num_splits;
+  const uint64_t mn = (uint64_t)p.m * p.n;
+  const bool vec_out = (p.n & 3u) == 0u;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        Cs[(8 * (r / 4) + 4 * lg + (r % 4)) * LDC + fn * 32 + lr] = acc[fm][fn][r];
+    __syncthreads();
+    const uint32_t row0 = m0 + wm * WTM + fm * 32;
+    const uint32_t col0 = n0 + wn * WTN;
+#pragma unroll 2
+    for (int i = 0; i < 32 * WTN / 4 / 64; ++i) {
+      const uint32_t e = lane + 64u * i;
+      const uint32_t lrow = e / (WTN / 4), c4 = (e % (WTN / 4)) * 4;
+      const uint32_t row = row0 + lrow, col = col0 + c4;
+      if (row >= p.m || col >= p.n)
+        continue;
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(&Cs[lrow * LDC + c4]);
+      const uint64_t base = S > 1 ? ((uint64_t)batch * S + split) * mn + (uint64_t)row * p.n + col
+                                  : (uint64_t)batch * p.stride_c + (uint64_t)row * p.n + col;
+      if constexpr (C_F16) {
+        _Float16 *c16 = reinterpret_cast<_Float16 *>(p.c);
+        const bool acc_old = p.flags & TA_FLAG_ACCUMULATE;
+        if (vec_out && col + 4 <= p.n) {
+          f16x4 old = acc_old ? *reinterpret_cast<const f16x4 *>(c16 + base) : f16x4{0, 0, 0, 0};
+          f16x4 o;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            o[c] = (_Float16)(p.alpha * v[c] + (acc_old ? (float)old[c] : 0.0f));
+          *reinterpret_cast<f16x4 *>(c16 + base) = o;
+        } else {
+          for (int c = 0; c < 4 && col + c < p.n; ++c)
+            c16[base + c] =
+                (_Float16)(p.alpha * v[c] + (acc_old ? (float)c16[base + c] : 0.0f));
+        }
+      } else if (vec_out && col + 4 <= p.n) {
+        f32x4 o;
+        if (S > 1) {
+          o = p.alpha * v;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            o[c] = ta_epilogue(v[c], p, base + c, col + c, batch);
+        }
+        *reinterpret_cast<f32x4 *>(&p.c[base]) = o;
+      } else {
+        for (int c = 0; c < 4 && col + c < p.n; ++c)
+          p.c[base + c] = S > 1 ? p.alpha * v[c] : ta_epilogue(v[c], p, base + c, col + c, batch);
+      }
+    }
+    __syncthreads();
+  }
+}

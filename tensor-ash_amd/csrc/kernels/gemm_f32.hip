@@ -45,6 +45,7 @@ struct GemmF32 {
   static_assert(A_PER * T * 4 == BM * BK, "A slab must split evenly");
   static_assert(B_PER * T * 4 == BK * BN, "B slab must split evenly");
   static_assert(FM >= 1 && FN >= 1, "wave tile must be a multiple of 32");
+  static_assert(T / 64 * 32 * (WTN + 4) <= 2 * (A_STAGE + B_STAGE), "C staging fits in LDS");
 
   typedef typename std::conditional<HALF_B, const _Float16, const float>::type BT;
 
@@ -223,56 +224,8 @@ struct GemmF32 {
       }
     }
 
-    // Output: one 32-row block of each wave's sub-tile at a time goes
-    // through LDS (the K loop's buffers are free after its last barrier),
-    // then the wave reads its block back row-major, applies the epilogue
-    // and stores 128-bit vectors.  This keeps the accumulators in
-    // registers (no dynamic indexing) and makes the C/D traffic coalesced.
-    // Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r
-    // holds row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 block.
-    constexpr int LDC = WTN + 4;
-    static_assert(T / 64 * 32 * LDC <= 2 * (A_STAGE + B_STAGE), "C staging fits");
-    float *Cs = smem + wave * (32 * LDC);
-    const uint32_t lr = lane & 31u, lg = lane >> 5;
-    const uint64_t mn = (uint64_t)p.m * p.n;
-    const bool vec_out = (p.n & 3u) == 0u;
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Cs[(8 * (r / 4) + 4 * lg + (r % 4)) * LDC + fn * 32 + lr] = acc[fm][fn][r];
-      __syncthreads();
-      const uint32_t row0 = m0 + wm * WTM + fm * 32;
-      const uint32_t col0 = n0 + wn * WTN;
-#pragma unroll 2
-      for (int i = 0; i < 32 * WTN / 4 / 64; ++i) {
-        const uint32_t e = lane + 64u * i;
-        const uint32_t lrow = e / (WTN / 4), c4 = (e % (WTN / 4)) * 4;
-        const uint32_t row = row0 + lrow, col = col0 + c4;
-        if (row >= p.m || col >= p.n)
-          continue;
-        const f32x4 v = *reinterpret_cast<const f32x4 *>(&Cs[lrow * LDC + c4]);
-        const uint64_t base = S > 1 ? ((uint64_t)batch * S + split) * mn + (uint64_t)row * p.n + col
-                                    : (uint64_t)batch * p.stride_c + (uint64_t)row * p.n + col;
-        if (vec_out && col + 4 <= p.n) {
-          f32x4 o;
-          if (S > 1) {
-            o = p.alpha * v;
-          } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              o[c] = ta_epilogue(v[c], p, base + c, col + c, batch);
-          }
-          *reinterpret_cast<f32x4 *>(&p.c[base]) = o;
-        } else {
-          for (int c = 0; c < 4 && col + c < p.n; ++c)
-            p.c[base + c] = S > 1 ? p.alpha * v[c] : ta_epilogue(v[c], p, base + c, col + c, batch);
-        }
-      }
-      __syncthreads();
-    }
+    ta_store_tile<WTM, WTN, FM, FN, T, false>(smem, 2 * (A_STAGE + B_STAGE), acc, p, lane, wave,
+                                              wm, wn, m0, n0, batch, split);
   }
 };
 

@@ -198,8 +198,15 @@ struct ExecutorImpl {
       p.kernel = heuristic_kernel_index(ctx->cu_count(), d.batch, d.m, d.n, d.k, true, true);
       return p;
     }
-    if (d.a_f16)
-      fail("matmul with f16 A storage is not supported by this build's kernels yet");
+    if (d.a_f16) {
+      // The a16 kernels are the only f16-activation route: a fixed pick,
+      // outside tuning and split-K (src/executor/mod.rs:218-257).
+      OpPlan p;
+      p.kernel = heuristic_kernel_index(ctx->cu_count(), d.batch, d.m, d.n, d.k, true, false, true);
+      if (selection.index && kernel_supports(KERNEL_SPECS[*selection.index], d))
+        p.kernel = *selection.index;
+      return p;
+    }
     return plan_shape(d.batch, d.m, d.n, d.k, d.b_f16, splitk_eligible);
   }
 

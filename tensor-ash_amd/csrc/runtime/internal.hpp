@@ -56,7 +56,7 @@ constexpr uint32_t kGemvMaxRows = 8;
 
 // ---- routing (src/pipeline/mod.rs:293-535, selection.rs:89-172) ----
 size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
-                              bool b_f16, bool packed_b);
+                              bool b_f16, bool packed_b, bool a_f16 = false);
 bool kernel_supports(const KernelSpec &spec, const ResolvedMatmul &dims);
 std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims);
 size_t registry_index(const char *name);

@@ -25,6 +25,22 @@ const KernelSpec KERNEL_SPECS[] = {
     {"f16w_m128n128", 128, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n128", ""},
     {"f16w_m128n64", 128, 64, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n64", ""},
     {"f16w_m64n64", 64, 64, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m64n64", ""},
+    {"f16w_mfma_m128n128", 128, 128, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m128n128",
+     "f16w_coopmat_aligned"},
+    {"f16w_mfma_m128n64", 128, 64, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m128n64",
+     "f16w_coopmat_m128n64"},
+    {"f16w_mfma_m64n128", 64, 128, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m64n128",
+     "f16w_coopmat_m64n128"},
+    {"f16w_mfma_m64n64", 64, 64, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m64n64",
+     "f16w_coopmat_m64n64"},
+    {"f16w_a16_m128n128", 128, 128, 64, KernelKind::GemmA16, "ta_gemm_a16_m128n128",
+     "f16w_a16_coopmat_aligned"},
+    {"f16w_a16_m128n64", 128, 64, 64, KernelKind::GemmA16, "ta_gemm_a16_m128n64",
+     "f16w_a16_coopmat_m128n64"},
+    {"f16w_a16_m64n128", 64, 128, 64, KernelKind::GemmA16, "ta_gemm_a16_m64n128",
+     "f16w_a16_coopmat_m64n128"},
+    {"f16w_a16_m64n64", 64, 64, 64, KernelKind::GemmA16, "ta_gemm_a16_m64n64",
+     "f16w_a16_coopmat_m64n64"},
     {"f16w_gemv_packed_t64", 8, 64, 0, KernelKind::GemvF16Packed, "ta_gemv_f16_t64",
      "f16w_row_packed"},
     {"f16w_gemv_packed_t32", 8, 32, 0, KernelKind::GemvF16Packed, "ta_gemv_f16_t32", ""},
@@ -86,7 +102,7 @@ uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
 bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
   if (d.a_f16)
-    return s.kind == KernelKind::GemmF16Mfma && d.m % s.tile_m == 0 && d.n % s.tile_n == 0;
+    return s.kind == KernelKind::GemmA16;
   if (d.packed_b)
     return s.kind == KernelKind::GemvF16Packed && d.m <= kGemvMaxRows && d.batch == 1 &&
            d.n % s.tile_n == 0;
@@ -96,6 +112,8 @@ bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
   case KernelKind::GemmF16w:
   case KernelKind::GemmF16Mfma:
     return d.b_f16;
+  case KernelKind::GemmA16:
+    return false;
   case KernelKind::GemvF16Row:
     return d.b_f16 && d.batch == 1 && d.m <= kGemvMaxRows && d.n % 4 == 0;
   case KernelKind::GemvF32Row:
@@ -106,30 +124,45 @@ bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
   return false;
 }
 
-// Shape heuristic for 256-CU MI355X (role of src/pipeline/mod.rs:293-360
-// and selection.rs:89-172; the reference's NVIDIA-tuned tables are not a
-// target): decode shapes (M <= 8, one batch) stream the weights through
-// the GEMV; otherwise the largest MFMA tile whose grid still covers every
-// CU once, else the 64x64 tile.
-size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
-                              bool b_f16, bool packed_b) {
-  (void)k;
-  if (packed_b)
-    return registry_index(n % 64 == 0 ? "f16w_gemv_packed_t64" : "f16w_gemv_packed_t32");
-  if (batch == 1 && m <= kGemvMaxRows && n % (b_f16 ? 4 : 2) == 0)
-    return registry_index(b_f16 ? "f16w_gemv_row" : "f32_gemv_row");
-  static const char *f32_tiles[] = {"f32_m256n256", "f32_m256n128", "f32_m128n128",
-                                    "f32_m128n64", "f32_m64n64"};
-  static const char *f16_tiles[] = {"f16w_m256n256", "f16w_m256n128", "f16w_m128n128",
-                                    "f16w_m128n64", "f16w_m64n64"};
-  const char **names = b_f16 ? f16_tiles : f32_tiles;
-  for (int i = 0; i < 5; ++i) {
+// Largest tile of `names` whose grid covers every CU once, else the last.
+static size_t pick_tile(const char *const *names, int count, uint32_t cus, uint32_t batch,
+                        uint32_t m, uint32_t n) {
+  for (int i = 0; i < count; ++i) {
     const KernelSpec &s = KERNEL_SPECS[registry_index(names[i])];
     const uint64_t tiles = (uint64_t)batch * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
     if (tiles >= cus)
       return registry_index(names[i]);
   }
-  return registry_index(names[4]);
+  return registry_index(names[count - 1]);
+}
+
+// Shape heuristic for 256-CU MI355X (role of src/pipeline/mod.rs:293-360
+// and selection.rs:89-172; the reference's NVIDIA-tuned tables are not a
+// target): decode shapes (M <= 8, one batch) stream the weights through
+// the GEMV; f16 weights with M, N >= 64 run on the f16 MFMA (A rounded to
+// f16 at staging, like the reference's coopmat route), smaller f16-weight
+// shapes widen B exactly on the FP32 MFMA; f16 activations take the a16
+// kernels.  Tiles: the largest whose grid still covers every CU once.
+size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                              bool b_f16, bool packed_b, bool a_f16) {
+  (void)k;
+  static const char *f32_tiles[] = {"f32_m256n256", "f32_m256n128", "f32_m128n128",
+                                    "f32_m128n64", "f32_m64n64"};
+  static const char *f16w_tiles[] = {"f16w_m256n256", "f16w_m256n128", "f16w_m128n128",
+                                     "f16w_m128n64", "f16w_m64n64"};
+  static const char *mfma16_tiles[] = {"f16w_mfma_m128n128", "f16w_mfma_m128n64",
+                                       "f16w_mfma_m64n128", "f16w_mfma_m64n64"};
+  static const char *a16_tiles[] = {"f16w_a16_m128n128", "f16w_a16_m128n64",
+                                    "f16w_a16_m64n128", "f16w_a16_m64n64"};
+  if (a_f16)
+    return pick_tile(a16_tiles, 4, cus, batch, m, n);
+  if (packed_b)
+    return registry_index(n % 64 == 0 ? "f16w_gemv_packed_t64" : "f16w_gemv_packed_t32");
+  if (batch == 1 && m <= kGemvMaxRows && n % (b_f16 ? 4 : 2) == 0)
+    return registry_index(b_f16 ? "f16w_gemv_row" : "f32_gemv_row");
+  if (b_f16 && m >= 64 && n >= 64)
+    return pick_tile(mfma16_tiles, 4, cus, batch, m, n);
+  return pick_tile(b_f16 ? f16w_tiles : f32_tiles, 5, cus, batch, m, n);
 }
 
 // Every kernel that can run the shape (role of pipeline/mod.rs:491-535).

@@ -150,7 +150,8 @@ uint32_t f16w_row_tile_n(uint32_t k, uint32_t n);
 enum class KernelKind : uint32_t {
   GemmF32,       // f32 A, f32 B, FP32 MFMA
   GemmF16w,      // f32 A, f16 B widened to f32, FP32 MFMA
-  GemmF16Mfma,   // f16-rounded A, f16 B, f16 MFMA with f32 accumulation
+  GemmF16Mfma,   // f32 A rounded to f16, f16 B, f16 MFMA, f32 accumulation
+  GemmA16,       // f16 A, f16 B, f16 C (RNE store), f16 MFMA
   GemvF16Packed, // M <= 8 decode GEMV, f16 B packed [N/TW][K][TW]
   GemvF16Row,    // M <= 8 decode GEMV, f16 B row-major
   GemvF32Row,    // M <= 8 decode GEMV, f32 B row-major
@@ -163,7 +164,8 @@ struct KernelSpec {
   const char *aliases; // extra ML_KERNEL spellings, comma separated
   bool weights_f16() const {
     return kind == KernelKind::GemmF16w || kind == KernelKind::GemmF16Mfma ||
-           kind == KernelKind::GemvF16Packed || kind == KernelKind::GemvF16Row;
+           kind == KernelKind::GemmA16 || kind == KernelKind::GemvF16Packed ||
+           kind == KernelKind::GemvF16Row;
   }
   bool is_gemv() const {
     return kind == KernelKind::GemvF16Packed || kind == KernelKind::GemvF16Row ||

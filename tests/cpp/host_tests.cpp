@@ -131,7 +131,12 @@ static void test_routing() {
   CHECK(name(1, 4096, 4096, 4096, false, false) == "f32_m256n256");
   CHECK(name(8, 2048, 2048, 2048, false, false) == "f32_m256n256");
   CHECK(name(1, 512, 512, 512, false, false) == "f32_m64n64");
-  CHECK(name(1, 512, 2560, 2048, true, false) == "f16w_m64n64");
+  CHECK(name(1, 512, 2560, 2048, true, false) == "f16w_mfma_m64n64");
+  CHECK(name(1, 512, 5632, 2048, true, false) == "f16w_mfma_m128n64");
+  CHECK(name(1, 4096, 4096, 4096, true, false) == "f16w_mfma_m128n128");
+  CHECK(name(1, 32, 4096, 4096, true, false) == "f16w_m64n64"); // M < 64: exact widening path
+  CHECK(std::string(KERNEL_SPECS[heuristic_kernel_index(cus, 1, 512, 256, 2048, true, false, true)]
+                        .name) == "f16w_a16_m64n64");
   CHECK(name(1, 1, 5632, 2048, true, true) == "f16w_gemv_packed_t64");
   CHECK(name(1, 8, 96, 2048, true, true) == "f16w_gemv_packed_t32");
   CHECK(name(1, 1, 4096, 4096, false, false) == "f32_gemv_row");

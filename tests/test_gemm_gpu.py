@@ -133,13 +133,14 @@ def test_every_f32_kernel(ta, ctx, oracle, shape):
         kex.close()
 
 
-@pytest.mark.parametrize("shape", [(256, 384, 256), (100, 130, 70)])
+@pytest.mark.parametrize("shape", [(32, 384, 256), (40, 130, 70)])
 def test_f16w_gemm(ta, ctx, ex, oracle, shape):
     """f16 B widened exactly: parity against cpu_bmm on the f16-rounded B (f16.rs:65-122)."""
     m, n, k = shape
     ha, hb = oracle.fill_det(m * k, 81), oracle.fill_det(k * n, 82)
     hbr = oracle.round_via_f16(hb)
-    for name in [None] + [n_ for n_ in ta.kernel_names() if n_.startswith("f16w_m")]:
+    import re
+    for name in [None] + [n_ for n_ in ta.kernel_names() if re.match(r"f16w_m\d", n_)]:
         kex = ex if name is None else ta.Executor(ctx, kernel_selection=name, tune=False)
         a = kex.tensor_from(ha, shape=[m, k])
         b = kex.tensor_from(hb, shape=[k, n], f16=True)
@@ -187,3 +188,72 @@ def test_4096_cube_sampled(ta, ex, oracle):
     ref = oracle.epilogue(ref, n, m * n, hbias, 0, 1)
     idx = np.concatenate([np.arange(r * n, (r + 1) * n) for r in rows])
     check_f32(got[idx], ref[idx], k, oracle)
+
+
+def f16_mfma_refs(ha, hb, batch, m, n, k, oracle, alpha=1.0, c0=None, acc=False, **epi):
+    """f16-MFMA route: A is rounded to f16 at staging (like the reference's
+    coopmat route, tests/correctness/f16.rs:776-817), so the oracle on the
+    dual-rounded inputs is exact up to accumulation order (f32 tolerance),
+    and the oracle on the unrounded A is within 2e-3."""
+    har, hbr = oracle.round_via_f16(ha), oracle.round_via_f16(hb)
+    return (oracle.reference_gemm(har, hbr, batch, m, n, k, alpha, c0, acc, **epi),
+            oracle.reference_gemm(ha, hbr, batch, m, n, k, alpha, c0, acc, **epi))
+
+
+def check_f16_mfma(got, refs, k, oracle):
+    check_f32(got, refs[0], k, oracle)
+    assert rel_err(got, refs[1]) <= 2e-3
+
+
+@pytest.mark.parametrize("shape", [(512, 2560, 2048), (512, 2048, 5632), (128, 128, 64), (200, 300, 100),
+                                   (65, 70, 33)])
+def test_f16_mfma_gemm(ta, ctx, ex, oracle, shape):
+    m, n, k = shape
+    ha, hb = oracle.fill_det(m * k, 91), oracle.fill_normal(k * n, 92, 0.02)
+    hbias = oracle.fill_det(n, 93)
+    refs = f16_mfma_refs(ha, hb, 1, m, n, k, oracle, bias=hbias, act=2)
+    names = [n_ for n_ in ta.kernel_names() if n_.startswith("f16w_mfma")] if m * n * k <= 1 << 24 else []
+    for name in [None] + names:
+        kex = ex if name is None else ta.Executor(ctx, kernel_selection=name, tune=False)
+        if name is None:
+            assert "mfma" in kex.dispatch_info_for(1, m, n, k, True)["kernel"]
+        a = kex.tensor_from(ha, shape=[m, k])
+        b = kex.tensor_from(hb, shape=[k, n], f16=True)
+        bias, c = kex.tensor_from(hbias, shape=[n]), kex.tensor([m, n])
+        kex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_SILU))])
+        check_f16_mfma(kex.download(c), refs, k, oracle)
+
+
+def test_f16_mfma_batched_alpha_accumulate(ta, ex, oracle):
+    """f16.rs:791-817: batched + alpha + accumulate."""
+    bt, m, n, k = 2, 256, 384, 256
+    ha, hb, hc = oracle.fill_det(bt * m * k, 9700), oracle.fill_det(bt * k * n, 9701), oracle.fill_det(bt * m * n, 9702)
+    a = ex.tensor_from(ha, shape=[bt, m, k])
+    b = ex.tensor_from(hb, shape=[bt, k, n], f16=True)
+    c = ex.tensor_from(hc, shape=[bt, m, n])
+    ex.run_ops([ta.MatmulOp(a, b, c, alpha=0.75, accumulate=True)])
+    refs = f16_mfma_refs(ha, hb, bt, m, n, k, oracle, alpha=0.75, c0=hc, acc=True)
+    check_f16_mfma(ex.download(c), refs, k, oracle)
+
+
+@pytest.mark.parametrize("bt,m,n,k", [(1, 256, 384, 256), (1, 128, 128, 64), (1, 512, 256, 2048), (3, 64, 128, 96)])
+def test_a16_activations(ta, ex, oracle, bt, m, n, k):
+    """f16.rs:316-360: f16 A/B/C; tolerance(K) + half an f16 ulp of max|ref|
+    (a16_tolerance, f16.rs:311-314)."""
+    sa, sb, sc = ([m, k], [k, n], [m, n]) if bt == 1 else ([bt, m, k], [bt, k, n], [bt, m, n])
+    ha = oracle.round_via_f16(oracle.fill_det(bt * m * k, 31))
+    hb = oracle.round_via_f16(oracle.fill_det(bt * k * n, 32))
+    a, b, c = ex.tensor_from(ha, f16=True, shape=sa), ex.tensor_from(hb, f16=True, shape=sb), ex.tensor(sc, f16=True)
+    ex.matmul(a, b, c)
+    ref = oracle.cpu_bmm(ha, hb, None, bt, m, n, k)
+    got = ex.download(c).reshape(-1)
+    tol = oracle.tolerance(k) + float(np.max(np.abs(ref))) * (0.5 / 1024.0)
+    err, idx = oracle.max_abs_err(got, ref)
+    assert err <= tol, f"a16 abs err {err} > {tol} at {idx}"
+
+
+def test_a16_rejects_epilogue(ta, ex):
+    a, b, c = ex.tensor([64, 64], f16=True), ex.tensor([64, 64], f16=True), ex.tensor([64, 64], f16=True)
+    bias = ex.tensor([64])
+    with pytest.raises(ta.TensorAshError, match="cannot fuse"):
+        ex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias))])

@@ -116,6 +116,9 @@ def test_cpu_bmm_rows_bit_identical(oracle):
     out = np.zeros(3 * 20 * 11, np.float32)
     oracle.cpu_bmm_rows(a, b, 3, 20, 11, 30, 1.0, out, 0, 60, 4)
     assert np.array_equal(out, full)
+    out2 = np.zeros_like(out)
+    oracle.cpu_bmm_rows(a, b, 3, 20, 11, 30, 1.0, out2, 0, 60, 3, reference_order=True)
+    assert np.array_equal(out2, full)
 
 
 # ---------------------------------------------------------------- errors
