@@ -222,13 +222,15 @@ def cpu_baseline(inputs, target_s: float = 12.0):
 
 def load_traffic():
     """HBM bytes per launch of the headline kernel from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled), or None."""
-    p = ROOT / "profiles" / "gemm_f32_4096_traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get("traffic_bytes")
-        except Exception:
-            return None
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, each scaled by the
+    same counter on a plain copy of known size), or None."""
+    p = ROOT / "profiles" / "gemm_f32_m256n256_4096cube_pmc.txt"
+    try:
+        for line in p.read_text().splitlines():
+            if line.startswith("traffic_bytes="):
+                return int(line.split("=", 1)[1])
+    except OSError:
+        pass
     return None
 
 
@@ -239,6 +241,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy (rocprof counter calibration)")
     ap.add_argument("--sections", default="decode,gelu,splitk,prefill",
                     help="comma list of secondary sections to run")
     args = ap.parse_args()
@@ -246,6 +250,17 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is described in DESIGN.md but not built", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        # A plain copy kernel of known size: FETCH_SIZE / WRITE_SIZE of this
+        # dispatch calibrate the counters used for the headline's traffic.
+        import torch
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes_each_way": src.numel() * 4}), flush=True)
+        return 0
     import tensor_ash as ta
 
     ctx = ta.Context()
