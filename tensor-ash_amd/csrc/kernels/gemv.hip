@@ -1,51 +1,87 @@
-// Decode GEMV (M = 1..8 rows) for gfx950, HBM-bound, no MFMA.
+// Decode GEMV (M = 1..8 rows) for gfx950, HBM-bound, no MFMA, and the
+// persistent decode SwiGLU MLP built from it.
 //
 // Replaces the reference's row GEMV family
 // (shaders/matmul_row_bda_kernel.glsl:186-403 and the
-// matmul_f16w_row_bda_k16{,_v2}{,_packed}.comp wrappers).  Semantics:
-// Y[m, :] = epilogue(alpha * X[m, :] @ W (+Y_old)) with f32 accumulation.
-// W is f16 (or f32) in either the packed row-tile layout [N/TW][K][TW]
-// (src/matmul/api.rs:324-344) or plain row-major [K, N]; both are "tiles
-// of TW columns whose rows sit `row_stride` elements apart", so one kernel
-// covers both (packed: tile stride K*TW, row stride TW; row-major: tile
-// stride TW, row stride N).
+// matmul_f16w_row_bda_k16{,_v2}{,_packed}.comp wrappers) and plays the
+// role of its persistent GEMV chain (shaders/matmul_gemv_chain_kernel.glsl)
+// for the decode MLP.  Semantics: Y[m, :] = epilogue(alpha * X[m, :] @ W
+// (+Y_old)) with f32 accumulation.  W is f16 (or f32) in either the packed
+// row-tile layout [N/TW][K][TW] (src/matmul/api.rs:324-344) or plain
+// row-major [K, N]; both are "tiles of TW columns whose rows sit
+// `row_stride` elements apart", so one kernel covers both (packed: tile
+// stride K*TW, row stride TW; row-major: tile stride TW, row stride N).
 //
-// Work decomposition: workgroup (256 threads = 4 waves) = one TW-column
-// tile x one window of `kchunk` K rows.  A lane owns CPL adjacent columns
-// read with one 64-bit load (four f16 or two f32), TW/CPL lanes span a
-// row, so one wave instruction reads 512 contiguous bytes of the packed
-// tile.  Each lane issues all kUnroll loads of a group unconditionally
-// (rows past the window re-read a valid row and are zeroed afterwards) so
-// they are in flight together.  X for the window sits in LDS as [k][MR]
-// so one k costs MR/4 128-bit broadcast reads.
+// Work unit: 256 threads (4 waves) = one TW-column tile x one window of
+// `kchunk` K rows.  A lane owns CPL adjacent columns read with one 64-bit
+// load (four f16 or two f32), TW/CPL lanes span a row, so one wave
+// instruction reads 512 contiguous bytes of the packed tile.  Each lane
+// issues all kUnroll loads of a group unconditionally (rows past the window
+// re-read a valid row and are zeroed afterwards) so they are in flight
+// together.  X for the window sits in LDS as [k][MR] so one k costs MR/4
+// 128-bit broadcast reads.
 //
 // Reduction, fixed order throughout (bit-reproducible):
 //   rows of a wave   -> xor shuffles across the 64/(TW/CPL) row groups;
 //   waves            -> LDS, summed wave 0..3;
-//   K windows        -> every workgroup stores its partial, the last one
-//                       of a tile to arrive (integer counter) sums windows
+//   K windows        -> every unit stores its partial, the last one of a
+//                       tile to arrive (integer counter) sums windows
 //                       0..kchunks-1 in order and applies the epilogue.
+// The cross-workgroup hand-off uses agent-scope relaxed atomics only
+// (sc1 loads/stores, coherent per location across the XCDs' L2s); a
+// vmcnt(0) wait before the barrier orders the partial stores before the
+// counter increment.  __threadfence() would write back and invalidate the
+// whole L2 in every workgroup.
 //
 // Dual mode (w2 != null): the same pass reads the two weight matrices of
 // a SwiGLU gate/up pair and writes U = alpha * X @ W2 to y2 and
 // Y = act(alpha * X @ W + bias) * U to y.
 #include "common.h"
 
+// Compile-time phase-timing hook for offline analysis; expands to nothing
+// in the library build.
+#ifndef TA_GEMV_TRACE
+#define TA_GEMV_TRACE(point)
+#define TA_GEMV_TRACE_ROLE(role)
+#endif
+
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
-template <int MR, bool DUAL, int TW, bool WF32>
+// Standalone launch, decode-MLP producer (signals per-tile readiness of its
+// outputs), decode-MLP consumer (waits for the producer tiles its X reads).
+enum { kStandalone = 0, kProducer = 1, kConsumer = 2 };
+
+TA_DEVICE float coherent_load(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+TA_DEVICE void coherent_store(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int MR, bool DUAL, int TW, bool WF32, int MODE, int XROWS, int UNROLL = 16>
 struct Gemv {
   static constexpr int WAYS = DUAL ? 2 : 1;
-  static constexpr int kMaxChunk = 4096 / MR; // X-window rows held in LDS (16 KiB)
-  static constexpr int CPL = WF32 ? 2 : 4;   // columns per lane (8-byte load)
-  static constexpr int LPR = TW / CPL;       // lanes per weight row
-  static constexpr int RPI = 64 / LPR;       // rows per wave instruction
-  static constexpr int RPW = RPI * kWaves;   // rows per workgroup step
-  static constexpr int EB = WF32 ? 4 : 2;    // bytes per weight element
-  static constexpr int kUnroll = 16; // loads per weight matrix per group
+  static constexpr int CPL = WF32 ? 2 : 4;  // columns per lane (8-byte load)
+  static constexpr int LPR = TW / CPL;      // lanes per weight row
+  static constexpr int RPI = 64 / LPR;      // rows per wave instruction
+  static constexpr int RPW = RPI * kWaves;  // rows per workgroup step
+  static constexpr int EB = WF32 ? 4 : 2;   // bytes per weight element
+  static constexpr int kUnroll = UNROLL;    // loads per weight matrix per group
+  static constexpr int OUTS = WAYS * MR * TW; // outputs of one tile, all ways
+  static constexpr int OPT = (OUTS + kThreads - 1) / kThreads;
+  // The X window's LDS is reused to stage the partials of all K windows
+  // for the last unit of a tile: PSTAGE floats, 16 loads per thread.
+  static constexpr int PSTAGE = 16 * kThreads;
+  static constexpr int XS = XROWS * MR > PSTAGE ? XROWS * MR : PSTAGE;
+
+  struct Smem {
+    float xs[XS]; // X window, later the partials of the last unit
+    float red[kWaves * OUTS];
+    uint32_t last_flag;
+  };
 
   static TA_DEVICE void unpack(uint64_t raw, float (&v)[CPL]) {
     if constexpr (WF32) {
@@ -58,18 +94,60 @@ struct Gemv {
     }
   }
 
-  static TA_DEVICE void run(const GemvArgs &p) {
-    __shared__ __attribute__((aligned(16))) float xs[kMaxChunk * MR];
-    __shared__ __attribute__((aligned(16))) float red[kWaves * WAYS * MR * TW];
-    __shared__ uint32_t last_flag;
+  // Consumer: wait until every producer tile covering X columns
+  // [k0, kend) has published its outputs.  Polling starts only once this
+  // workgroup's own weight loads have landed (vmcnt(0)) and sleeps ~0.2 us
+  // between polls, so waiting units do not flood the memory system.
+  // Bounded: after spin_limit polls the wait gives up and raises the
+  // host-visible status word (the launch's results are then invalid).
+  static TA_DEVICE void wait_ready(const GemvArgs &p, uint32_t k0, uint32_t kend) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // One lane per producer tile polls its flag (all polls in parallel).
+    const uint32_t t_lo = k0 / p.x_tile, t_hi = (kend - 1) / p.x_tile;
+    if (threadIdx.x <= t_hi - t_lo) {
+      {
+        const uint32_t t = t_lo + threadIdx.x;
+        uint32_t polls = 0;
+        while (__hip_atomic_load(&p.ready[t * TA_GEMV_COUNTER_STRIDE], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+          __builtin_amdgcn_s_sleep(8);
+          if (++polls >= p.spin_limit) {
+            __hip_atomic_store(p.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            break;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    TA_GEMV_TRACE(6);
+  }
 
+  // Consumer, after X is read: count this unit as a reader of each
+  // producer tile; the last reader clears the tile's flag (and its count)
+  // for the next launch.
+  static TA_DEVICE void ack_ready(const GemvArgs &p, uint32_t k0, uint32_t kend) {
+    const uint32_t t_lo = k0 / p.x_tile, t_hi = (kend - 1) / p.x_tile;
+    if (threadIdx.x <= t_hi - t_lo) {
+      {
+        const uint32_t t = t_lo + threadIdx.x;
+        uint32_t *ack = &p.acks[t * TA_GEMV_COUNTER_STRIDE];
+        if (__hip_atomic_fetch_add(ack, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            p.x_readers - 1) {
+          __hip_atomic_store(ack, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(&p.ready[t * TA_GEMV_COUNTER_STRIDE], 0u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  }
+
+  static TA_DEVICE void unit(const GemvArgs &p, uint32_t tile, uint32_t chunk, Smem &sm) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t tiles = (p.n + TW - 1) / TW;
-    const uint32_t tile = blockIdx.x % tiles;
-    const uint32_t chunk = blockIdx.x / tiles;
     const uint32_t k0 = chunk * p.kchunk;
     const uint32_t kend = min(p.k, k0 + p.kchunk);
     const bool packed = p.flags & TA_GEMV_PACKED;
+    TA_GEMV_TRACE(0);
 
     const uint32_t cp = lane % LPR, r0 = lane / LPR;
     // Lanes past N (row-major, ragged last tile) read column 0 of the tile
@@ -101,24 +179,43 @@ struct Gemv {
       }
     };
 
-    // X loads go out first, then the first weight group: vmcnt retires in
-    // issue order, so staging X into LDS then waits only for X.
-    constexpr int XPT = kMaxChunk * MR / kThreads;
+    // X window: XPT values per thread, clamped index + select (no branch).
+    constexpr int XPT = XROWS * MR / kThreads;
     float xr[XPT];
+    auto load_x = [&]() {
 #pragma unroll
-    for (int j = 0; j < XPT; ++j) {
-      const uint32_t i = tid + j * kThreads;
-      const uint32_t kk = i / MR, m = i % MR;
-      const bool ok = i < p.kchunk * MR && m < p.rows && k0 + kk < kend;
-      xr[j] = p.x[ok ? (uint64_t)m * p.k + k0 + kk : 0];
-      xr[j] = ok ? xr[j] : 0.0f;
-    }
+      for (int j = 0; j < XPT; ++j) {
+        const uint32_t i = tid + j * kThreads;
+        const uint32_t kk = i / MR, m = i % MR;
+        const bool ok = i < p.kchunk * MR && m < p.rows && k0 + kk < kend;
+        const float *src = p.x + (ok ? (uint64_t)m * p.k + k0 + kk : 0);
+        if constexpr (MODE == kConsumer)
+          xr[j] = coherent_load(src); // written by producer units of this launch
+        else
+          xr[j] = *src;
+        xr[j] = ok ? xr[j] : 0.0f;
+      }
+    };
+
     uint64_t cur[WAYS][kUnroll];
-    issue(0, cur);
+    if constexpr (MODE == kConsumer) {
+      // Weights first (they do not depend on X), then wait for X.
+      issue(0, cur);
+      wait_ready(p, k0, kend);
+      load_x();
+    } else {
+      // X loads go out first, then the first weight group: vmcnt retires
+      // in issue order, so staging X into LDS then waits only for X.
+      load_x();
+      issue(0, cur);
+    }
 #pragma unroll
     for (int j = 0; j < XPT; ++j)
-      xs[tid + j * kThreads] = xr[j];
-    __syncthreads();
+      sm.xs[tid + j * kThreads] = xr[j];
+    __syncthreads(); // all of X is in registers/LDS: the unit's reads are done
+    if constexpr (MODE == kConsumer)
+      ack_ready(p, k0, kend);
+    TA_GEMV_TRACE(1);
 
     float acc[WAYS][MR][CPL];
 #pragma unroll
@@ -138,7 +235,7 @@ struct Gemv {
         if constexpr (MR >= 4) {
 #pragma unroll
           for (int q = 0; q < MR / 4; ++q) {
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(&xs[kk * MR + 4 * q]);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&sm.xs[kk * MR + 4 * q]);
             xv[4 * q] = v[0];
             xv[4 * q + 1] = v[1];
             xv[4 * q + 2] = v[2];
@@ -147,7 +244,7 @@ struct Gemv {
         } else {
 #pragma unroll
           for (int m = 0; m < MR; ++m)
-            xv[m] = xs[kk * MR + m];
+            xv[m] = sm.xs[kk * MR + m];
         }
 #pragma unroll
         for (int w = 0; w < WAYS; ++w) {
@@ -163,13 +260,13 @@ struct Gemv {
     };
 
     // kchunk is a multiple of G (host contract): whole groups only.  The
-    // resident grid (every workgroup of a decode launch fits at once)
-    // keeps HBM busy while each wave waits on its own group.
+    // resident grid keeps HBM busy while each wave waits on its group.
     consume(0, cur);
     for (uint32_t kb = G; kb < p.kchunk; kb += G) {
       issue(kb, cur);
       consume(kb, cur);
     }
+    TA_GEMV_TRACE(2);
 
     // Rows of one wave: lanes cp, cp + LPR, ... hold the same columns.
 #pragma unroll
@@ -186,7 +283,7 @@ struct Gemv {
       for (int w = 0; w < WAYS; ++w)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          float *dst = &red[((wave * WAYS + w) * MR + m) * TW + CPL * cp];
+          float *dst = &sm.red[((wave * WAYS + w) * MR + m) * TW + CPL * cp];
 #pragma unroll
           for (int c = 0; c < CPL; ++c)
             dst[c] = acc[w][m][c];
@@ -194,88 +291,99 @@ struct Gemv {
     }
     __syncthreads();
 
-    constexpr int OUTS = WAYS * MR * TW; // this tile's outputs, all ways
-    float part[(OUTS + kThreads - 1) / kThreads];
+    float part[OPT];
 #pragma unroll
-    for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
+    for (int i = 0; i < OPT; ++i) {
       const uint32_t o = tid + i * kThreads;
       float s = 0.0f;
       if (o < OUTS) {
-        s = red[o];
+        s = sm.red[o];
 #pragma unroll
         for (int wv = 1; wv < kWaves; ++wv)
-          s += red[wv * OUTS + o];
+          s += sm.red[wv * OUTS + o];
       }
       part[i] = s;
     }
 
     if (p.kchunks > 1) {
-      // Cross-XCD hand-off without an L2 write-back: partials are written
-      // and read only with agent-scope relaxed atomics (sc1 loads/stores,
-      // coherent per location across the XCDs' L2s).  Waiting for this
-      // thread's stores to complete before the barrier makes them visible
-      // before thread 0 bumps the tile counter (release); the last
-      // workgroup reads them after observing the count (acquire by control
-      // dependency).  __threadfence() would instead write back and
-      // invalidate the whole L2 in every workgroup.
+      uint32_t *counter = &p.counters[tile * TA_GEMV_COUNTER_STRIDE];
       float *mine = p.partial + ((uint64_t)chunk * tiles + tile) * OUTS;
 #pragma unroll
-      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
+      for (int i = 0; i < OPT; ++i) {
         const uint32_t o = tid + i * kThreads;
         if (o < OUTS)
-          __hip_atomic_store(mine + o, part[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          coherent_store(mine + o, part[i]);
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      TA_GEMV_TRACE(3);
       if (tid == 0) {
         const uint32_t seen =
-            __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = (seen == p.kchunks - 1) ? 1u : 0u;
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm.last_flag = (seen == p.kchunks - 1) ? 1u : 0u;
       }
       __syncthreads();
-      if (!last_flag)
+      TA_GEMV_TRACE(4);
+      if (!sm.last_flag)
         return;
-      // Sum the windows in order 0..kchunks-1.  All partial loads of a
-      // batch go out at once (one memory round trip) into the X window's
-      // LDS, which is free now; then each output is summed sequentially.
+      // Sum the windows in order 0..kchunks-1.  A batch of NB windows is
+      // loaded at once (16 loads per thread, one memory round trip) into the
+      // X window's LDS, which is free now; then each output adds its
+      // windows sequentially.
       const uint64_t step = (uint64_t)tiles * OUTS;
       const float *tsrc = p.partial + (uint64_t)tile * OUTS;
-      constexpr uint32_t NB = (kMaxChunk * MR) / OUTS; // windows per batch
-      float sum[(OUTS + kThreads - 1) / kThreads];
+      constexpr uint32_t NB = PSTAGE / OUTS; // windows per batch
+      static_assert(NB >= 1, "staging holds at least one partial");
+      float sum[OPT];
 #pragma unroll
-      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i)
+      for (int i = 0; i < OPT; ++i)
         sum[i] = 0.0f;
       for (uint32_t c0 = 0; c0 < p.kchunks; c0 += NB) {
         const uint32_t nb = min(NB, p.kchunks - c0);
         __syncthreads(); // previous batch fully consumed
-        for (uint32_t e = tid; e < nb * OUTS; e += kThreads) {
-          const uint32_t c = c0 + e / OUTS, o = e % OUTS;
-          xs[e] = __hip_atomic_load(tsrc + c * step + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float v[PSTAGE / kThreads];
+#pragma unroll
+        for (int j = 0; j < PSTAGE / kThreads; ++j) {
+          const uint32_t e = tid + j * kThreads;
+          const bool ok = e < nb * OUTS;
+          const uint32_t c = c0 + (ok ? e / OUTS : 0), o = ok ? e % OUTS : 0;
+          v[j] = coherent_load(tsrc + c * step + o);
         }
+#pragma unroll
+        for (int j = 0; j < PSTAGE / kThreads; ++j)
+          sm.xs[tid + j * kThreads] = v[j];
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
+        for (int i = 0; i < OPT; ++i) {
           const uint32_t o = tid + i * kThreads;
           if (o < OUTS)
             for (uint32_t c = 0; c < nb; ++c)
-              sum[i] = (c0 + c == 0) ? xs[o] : sum[i] + xs[c * OUTS + o];
+              sum[i] = (c0 + c == 0) ? sm.xs[o] : sum[i] + sm.xs[c * OUTS + o];
         }
       }
 #pragma unroll
-      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i)
+      for (int i = 0; i < OPT; ++i)
         part[i] = sum[i];
       if (tid == 0)
-        __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // Epilogue (shaders/matmul_epilogue_common.glsl:14-21 order).
+    TA_GEMV_TRACE(5);
+    // Epilogue (shaders/matmul_epilogue_common.glsl:14-21 order).  A
+    // producer publishes its outputs with coherent stores, then its flag.
+    auto put = [&](float *dst, float v) {
+      if constexpr (MODE == kProducer)
+        coherent_store(dst, v);
+      else
+        *dst = v;
+    };
     if constexpr (DUAL) {
       __syncthreads();
 #pragma unroll
-      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
+      for (int i = 0; i < OPT; ++i) {
         const uint32_t o = tid + i * kThreads;
         if (o < OUTS)
-          red[o] = part[i];
+          sm.red[o] = part[i];
       }
       __syncthreads();
       for (uint32_t o = tid; o < MR * TW; o += kThreads) {
@@ -283,16 +391,16 @@ struct Gemv {
         if (m >= p.rows || c >= p.n)
           continue;
         const uint64_t yi = (uint64_t)m * p.n + c;
-        const float u = p.alpha * red[MR * TW + o];
-        float g = p.alpha * red[o];
+        const float u = p.alpha * sm.red[MR * TW + o];
+        float g = p.alpha * sm.red[o];
         if (p.flags & TA_FLAG_BIAS)
           g += p.bias[c];
-        p.y2[yi] = u;
-        p.y[yi] = ta_activate(g, p.act) * u;
+        put(p.y2 + yi, u);
+        put(p.y + yi, ta_activate(g, p.act) * u);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < (OUTS + kThreads - 1) / kThreads; ++i) {
+      for (int i = 0; i < OPT; ++i) {
         const uint32_t o = tid + i * kThreads;
         const uint32_t m = o / TW, c = tile * TW + o % TW;
         if (o >= OUTS || m >= p.rows || c >= p.n)
@@ -308,9 +416,57 @@ struct Gemv {
           v = fmaf(p.beta, p.d[yi], v);
         else if (p.binary == TA_BIN_MUL)
           v *= p.d[yi];
-        p.y[yi] = v;
+        put(p.y + yi, v);
       }
     }
+    if constexpr (MODE == kProducer) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_store(&p.ready[tile * TA_GEMV_COUNTER_STRIDE], 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  static TA_DEVICE void run(const GemvArgs &p) {
+    __shared__ __attribute__((aligned(16))) Smem sm;
+    const uint32_t tiles = (p.n + TW - 1) / TW;
+    unit(p, blockIdx.x % tiles, blockIdx.x / tiles, sm);
+  }
+};
+
+// Rows of X staged per standalone unit: 16 KiB of LDS.
+template <int MR> constexpr int standalone_rows() { return 4096 / MR; }
+
+// Persistent decode MLP.  Workgroup ids below units_a run gate/up
+// (producer) units, the rest run down-proj (consumer) units.  Producers
+// never wait, and each XCD dispatches its workgroups in id order, so every
+// producer a consumer waits for has been dispatched before that consumer
+// and runs to completion; the bounded wait is a safety net only.  No
+// launch-wide counter exists (one hot atomic would serialise the starts).
+// K windows: gate/up units take 256 rows (one group of 16 loads per
+// matrix); down units take 512 rows (one group of 32 loads) so they are
+// fewer, every workgroup of the launch is resident at once, and a down
+// unit's whole weight window is in flight before it starts waiting.
+constexpr int kMlpRowsA = 256;
+constexpr int kMlpRowsB = 512;
+
+template <int MR> struct DecodeMlp {
+  typedef Gemv<MR, true, 64, false, kProducer, kMlpRowsA, 16> A;
+  typedef Gemv<MR, false, 64, false, kConsumer, kMlpRowsB, 32> B;
+  union Smem {
+    typename A::Smem a;
+    typename B::Smem b;
+  };
+
+  static TA_DEVICE void run(const MlpArgs &p) {
+    __shared__ __attribute__((aligned(16))) Smem sm;
+    const uint32_t r = blockIdx.x;
+    TA_GEMV_TRACE_ROLE(r);
+    if (r < p.units_a)
+      A::unit(p.a, r % p.tiles_a, r / p.tiles_a, sm.a);
+    else
+      B::unit(p.b, (r - p.units_a) % p.tiles_b, (r - p.units_a) / p.tiles_b, sm.b);
   }
 };
 
@@ -318,7 +474,7 @@ struct Gemv {
 
 #define TA_GEMV(NAME, MR, DUAL, TW, WF32)                                          \
   extern "C" __global__ __launch_bounds__(kThreads) void NAME(GemvArgs p) {        \
-    Gemv<MR, DUAL, TW, WF32>::run(p);                                              \
+    Gemv<MR, DUAL, TW, WF32, kStandalone, standalone_rows<MR>()>::run(p);         \
   }
 
 #define TA_GEMV_ROWS(PREFIX, DUAL, TW, WF32)                                       \
@@ -332,3 +488,13 @@ TA_GEMV_ROWS(ta_gemv_f16_t64_dual, true, 64, false)
 TA_GEMV_ROWS(ta_gemv_f16_t32, false, 32, false)
 TA_GEMV_ROWS(ta_gemv_f16_t32_dual, true, 32, false)
 TA_GEMV_ROWS(ta_gemv_f32_t64, false, 64, true)
+
+#define TA_MLP(MR)                                                                 \
+  extern "C" __global__ __launch_bounds__(kThreads) void ta_decode_mlp_f16_t64_m##MR( \
+      MlpArgs p) {                                                                 \
+    DecodeMlp<MR>::run(p);                                                         \
+  }
+TA_MLP(1)
+TA_MLP(2)
+TA_MLP(4)
+TA_MLP(8)

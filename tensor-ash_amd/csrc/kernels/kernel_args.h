@@ -63,16 +63,21 @@ typedef struct SplitReduceArgs {
   uint32_t pad;
 } SplitReduceArgs;
 
-// Decode GEMV over packed f16 weights W[N/64][K][64]:
+// Decode GEMV over packed f16 weights W[N/TW][K][TW] (or row-major):
 // Y[m, :] = epilogue(alpha * X[m, :] @ W) for m < rows (rows <= 8).
 // With `w2` set (dual mode) the same launch also computes
-// U = X @ W2 and stores U to `y2` and Y = act(X @ W) * U to `y`
-// (SwiGLU gating); then `binary` must be TA_BIN_NONE.
-// K is cut into `kchunks` windows of `kchunk` rows; every (tile, chunk)
-// workgroup writes its partial to `partial`, and the last workgroup of a
-// tile to finish (counted in `counters[tile]`) sums the chunks in chunk
-// order and applies the epilogue.  The counter is reset by that
-// workgroup, so the buffer stays zero between launches.
+// U = alpha * X @ W2, stores U to `y2` and Y = act(alpha * X @ W + bias) * U
+// to `y` (SwiGLU gating); then `binary` must be TA_BIN_NONE.
+// K is cut into `kchunks` windows of `kchunk` rows; every (tile, window)
+// workgroup stores its partial to `partial`, and the last workgroup of a
+// tile to arrive (counted in `counters[tile * stride]`) sums the windows in
+// window order and applies the epilogue.  That workgroup resets the
+// counter, so the buffer stays zero between launches.
+
+// One counter or flag per 128-byte line (atomics on a shared line
+// serialise across tiles).
+#define TA_GEMV_COUNTER_STRIDE 32u
+
 typedef struct GemvArgs {
   const float *x; // [rows, K] f32
   const uint16_t *w;
@@ -81,8 +86,11 @@ typedef struct GemvArgs {
   float *y2; // dual mode only
   const float *d;
   const float *bias;
-  float *partial;     // [kchunks][tiles][ways][rows][64]
-  uint32_t *counters; // [tiles]
+  float *partial;     // [kchunks][tiles][ways][MR][TW]
+  uint32_t *counters; // [tiles * TA_GEMV_COUNTER_STRIDE]
+  uint32_t *ready;    // decode MLP: per producer tile "outputs written" flags
+  uint32_t *acks;     // decode MLP consumer: per producer tile reader count
+  uint32_t *status;   // decode MLP consumer: host-mapped, 1 if a wait gave up
   uint32_t rows, n, k;
   uint32_t kchunk;
   uint32_t kchunks;
@@ -91,8 +99,22 @@ typedef struct GemvArgs {
   uint32_t binary;
   float alpha;
   float beta;
-  uint32_t pad0, pad1;
+  uint32_t x_tile;     // decode MLP consumer: column tile width of X's producer
+  uint32_t spin_limit; // decode MLP consumer: polls before giving up
+  uint32_t x_readers;  // decode MLP consumer: units reading each producer tile
+  uint32_t pad;
 } GemvArgs;
+
+// Persistent decode SwiGLU MLP in one launch: `a` is the dual gate/up GEMV
+// (producer of h = act(x Wg) * (x Wu)), `b` the down-proj GEMV reading h.
+// Workgroups 0..units_a-1 run `a` units, the rest run `b` units, which wait
+// on the `a` tiles they read (flags in a.ready, reset by their last reader).
+typedef struct MlpArgs {
+  GemvArgs a;
+  GemvArgs b;
+  uint32_t units_a, units_b;
+  uint32_t tiles_a, tiles_b;
+} MlpArgs;
 
 #ifdef __cplusplus
 }

@@ -81,14 +81,32 @@ struct Slot {
   hipStream_t stream = nullptr;
   hipEvent_t start = nullptr, end = nullptr;
   Scratch scratch;
+  uint32_t *host_status = nullptr; // mapped pinned word (decode-MLP status)
 };
+
+// Mapped pinned word the decode-MLP kernel reports its wait status into.
+uint32_t *alloc_host_status() {
+  void *p = nullptr;
+  hip_check(hipHostMalloc(&p, 64, hipHostMallocMapped), "hipHostMalloc");
+  *static_cast<volatile uint32_t *>(p) = 0;
+  return static_cast<uint32_t *>(p);
+}
+
+void check_host_status(uint32_t *word) {
+  volatile uint32_t *w = word;
+  if (*w != 0) {
+    *w = 0;
+    fail("decode MLP: a down-proj unit gave up waiting for the gate/up outputs");
+  }
+}
 
 // Complete route for one op (src/executor/mod.rs:125-139).
 struct OpPlan {
   size_t kernel = 0;
   std::optional<uint32_t> splitk2;
   // Launch role: 0 = normal, 1 = fused into the next op's dual GEMV,
-  // 2 = dual GEMV that also produces the previous op's output.
+  // 2 = dual GEMV that also produces the previous op's output,
+  // 3 = decode-MLP launch covering this op and the next two, 4 = covered.
   int role = 0;
 };
 
@@ -228,7 +246,7 @@ struct ExecutorImpl {
       GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, p.role == 2,
                             gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, p.role == 2));
       need.partial = g.partial_bytes;
-      need.counters = g.tiles;
+      need.counters = (uint64_t)g.tiles * TA_GEMV_COUNTER_STRIDE;
     }
     return need;
   }
@@ -321,7 +339,7 @@ struct ExecutorImpl {
       a.beta = op.epilogue.binary.beta;
     }
     if (g.kchunks > 1) {
-      if (scratch.partial_bytes < g.partial_bytes || scratch.counters_len < g.tiles)
+      if (scratch.partial_bytes < g.partial_bytes || scratch.counters_len < (uint64_t)g.tiles * TA_GEMV_COUNTER_STRIDE)
         fail("internal: GEMV scratch not reserved");
       a.partial = static_cast<float *>(scratch.partial);
       a.counters = scratch.counters;
@@ -360,6 +378,15 @@ struct ExecutorImpl {
     for (size_t i = 0; i + 1 < ops.size(); ++i) {
       if (plans[i].role != 0 || plans[i + 1].role != 0)
         continue;
+      if (!std::getenv("TA_NO_MLP") && i + 2 < ops.size() && plans[i + 2].role == 0 &&
+          fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1]) &&
+          mlp_tail_ok(ops[i], ops[i + 1], plans[i + 1], ops[i + 2], plans[i + 2])) {
+        plans[i].role = 3;
+        plans[i + 1].role = 4;
+        plans[i + 2].role = 4;
+        i += 2;
+        continue;
+      }
       if (fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1])) {
         plans[i].role = 1;
         plans[i + 1].role = 2;
@@ -380,18 +407,156 @@ struct ExecutorImpl {
   ScratchNeed total_need(const std::vector<ResolvedMatmul> &res,
                          const std::vector<OpPlan> &plans) const {
     ScratchNeed need;
-    for (size_t i = 0; i < res.size(); ++i)
-      if (plans[i].role != 1)
+    for (size_t i = 0; i < res.size(); ++i) {
+      if (plans[i].role == 3) {
+        MlpGeom g = mlp_geom(res[i], res[i + 2]);
+        ScratchNeed m;
+        m.partial = g.partial_bytes;
+        m.counters = g.counters_len;
+        need.merge(m);
+      } else if (plans[i].role != 1 && plans[i].role != 4) {
         need.merge(scratch_need(res[i], plans[i]));
+      }
+    }
     return need;
   }
 
+  // ---- persistent decode MLP: [up, gate*act*up, down] in one launch ----
+  struct MlpGeom {
+    uint32_t mr, tiles_a, kch_a, tiles_b, kch_b;
+    uint64_t part_a_bytes, partial_bytes;
+    // u32 offsets into the counters buffer
+    uint64_t cnt_a, cnt_b, ready, acks, counters_len;
+  };
+  // K windows of the two phases (kernel constants kMlpRowsA / kMlpRowsB).
+  static constexpr uint32_t kMlpRowsA = 256, kMlpRowsB = 512;
+
+  static MlpGeom mlp_geom(const ResolvedMatmul &up, const ResolvedMatmul &down) {
+    MlpGeom g{};
+    g.mr = up.m <= 1 ? 1 : up.m <= 2 ? 2 : up.m <= 4 ? 4 : 8;
+    g.tiles_a = up.n / 64;
+    g.kch_a = (up.k + kMlpRowsA - 1) / kMlpRowsA;
+    g.tiles_b = down.n / 64;
+    g.kch_b = (down.k + kMlpRowsB - 1) / kMlpRowsB;
+    g.part_a_bytes = ((uint64_t)g.kch_a * g.tiles_a * 2 * g.mr * 64 * 4 + 255) / 256 * 256;
+    g.partial_bytes = g.part_a_bytes + (uint64_t)g.kch_b * g.tiles_b * g.mr * 64 * 4;
+    const uint64_t S = TA_GEMV_COUNTER_STRIDE;
+    g.cnt_a = 0;
+    g.cnt_b = g.cnt_a + g.tiles_a * S;
+    g.ready = g.cnt_b + g.tiles_b * S;
+    g.acks = g.ready + g.tiles_a * S;
+    g.counters_len = g.acks + g.tiles_a * S;
+    return g;
+  }
+
+  // ops[i] = x@Wu, ops[i+1] = act(x@Wg) * up (a fusable pair), ops[i+2] =
+  // h@Wd reading the pair's output h, all on the packed 64-column decode
+  // GEMV.  The down op keeps its full epilogue.
+  static bool mlp_tail_ok(const MatmulOp &up, const MatmulOp &gate, const OpPlan &pg,
+                          const MatmulOp &down, const OpPlan &pd) {
+    const KernelSpec &sg = KERNEL_SPECS[pg.kernel], &sd = KERNEL_SPECS[pd.kernel];
+    if (!sg.packed() || !sd.packed() || sg.tile_n != 64 || sd.tile_n != 64 || pd.splitk2)
+      return false;
+    if (!down.packed_b || down.call.a->buffer_id() != gate.call.c->buffer_id() ||
+        down.call.a->shape() != gate.call.c->shape())
+      return false;
+    auto aliases = [&](const Tensor *t) {
+      return t && (t->buffer_id() == up.call.c->buffer_id() ||
+                   t->buffer_id() == gate.call.c->buffer_id() ||
+                   t->buffer_id() == up.call.a->buffer_id());
+    };
+    return !aliases(down.call.c) && !aliases(down.epilogue.bias) &&
+           !aliases(down.epilogue.d_tensor());
+  }
+
+  void launch_mlp(const std::vector<MatmulOp> &ops, const std::vector<ResolvedMatmul> &res,
+                  size_t i, Scratch &scratch, uint32_t *host_status, hipStream_t stream) const {
+    const MatmulOp &up = ops[i], &gate = ops[i + 1], &down = ops[i + 2];
+    MlpGeom g = mlp_geom(res[i], res[i + 2]);
+    if (scratch.partial_bytes < g.partial_bytes || scratch.counters_len < g.counters_len)
+      fail("internal: decode-MLP scratch not reserved");
+    if (!host_status)
+      fail("internal: decode-MLP status word missing");
+    MlpArgs m{};
+    GemvArgs &a = m.a;
+    a.x = static_cast<const float *>(gate.call.a->device_ptr());
+    a.w = static_cast<const uint16_t *>(gate.call.b->device_ptr());
+    a.w2 = static_cast<const uint16_t *>(up.call.b->device_ptr());
+    a.y = static_cast<float *>(gate.call.c->device_ptr());
+    a.y2 = static_cast<float *>(up.call.c->device_ptr());
+    a.rows = res[i].m;
+    a.n = res[i].n;
+    a.k = res[i].k;
+    a.kchunk = kMlpRowsA;
+    a.kchunks = g.kch_a;
+    a.flags = TA_GEMV_PACKED;
+    if (gate.epilogue.bias) {
+      a.flags |= TA_FLAG_BIAS;
+      a.bias = static_cast<const float *>(gate.epilogue.bias->device_ptr());
+    }
+    a.act = (uint32_t)gate.epilogue.activation;
+    a.alpha = gate.call.alpha;
+    a.partial = static_cast<float *>(scratch.partial);
+    a.counters = scratch.counters + g.cnt_a;
+    a.ready = scratch.counters + g.ready;
+    GemvArgs &b = m.b;
+    b.x = static_cast<const float *>(down.call.a->device_ptr());
+    b.w = static_cast<const uint16_t *>(down.call.b->device_ptr());
+    b.y = static_cast<float *>(down.call.c->device_ptr());
+    b.rows = res[i + 2].m;
+    b.n = res[i + 2].n;
+    b.k = res[i + 2].k;
+    b.kchunk = kMlpRowsB;
+    b.kchunks = g.kch_b;
+    b.flags = TA_GEMV_PACKED | (down.call.accumulate ? TA_FLAG_ACCUMULATE : 0u);
+    if (down.epilogue.bias) {
+      b.flags |= TA_FLAG_BIAS;
+      b.bias = static_cast<const float *>(down.epilogue.bias->device_ptr());
+    }
+    b.act = (uint32_t)down.epilogue.activation;
+    b.binary = (uint32_t)down.epilogue.binary.kind;
+    if (const Tensor *dt = down.epilogue.d_tensor())
+      b.d = static_cast<const float *>(dt->device_ptr());
+    b.beta = down.epilogue.binary.beta;
+    b.alpha = down.call.alpha;
+    b.partial = reinterpret_cast<float *>(static_cast<char *>(scratch.partial) + g.part_a_bytes);
+    b.counters = scratch.counters + g.cnt_b;
+    b.ready = scratch.counters + g.ready;
+    b.acks = scratch.counters + g.acks;
+    b.x_tile = 64;
+    b.x_readers = g.tiles_b; // the one window covering a producer tile, per down tile
+    b.spin_limit = 1u << 20; // ~0.2 s of polling (0.2 us per poll) before giving up
+    void *dev_status = nullptr;
+    hip_check(hipHostGetDevicePointer(&dev_status, host_status, 0), "hipHostGetDevicePointer");
+    b.status = static_cast<uint32_t *>(dev_status);
+    m.units_a = g.tiles_a * g.kch_a;
+    m.units_b = g.tiles_b * g.kch_b;
+    m.tiles_a = g.tiles_a;
+    m.tiles_b = g.tiles_b;
+    launch("ta_decode_mlp_f16_t64_m" + std::to_string(g.mr), m.units_a + m.units_b, 1, 1, 256, &m,
+           stream);
+  }
+
+  static bool has_mlp(const std::vector<OpPlan> &plans) {
+    for (const auto &p : plans)
+      if (p.role == 3)
+        return true;
+    return false;
+  }
+
   void record(const std::vector<MatmulOp> &ops, const std::vector<ResolvedMatmul> &res,
-              const std::vector<OpPlan> &plans, Scratch &scratch, hipStream_t stream) const {
+              const std::vector<OpPlan> &plans, Scratch &scratch, uint32_t *host_status,
+              hipStream_t stream) const {
     for (size_t i = 0; i < ops.size(); ++i) {
       const OpPlan &p = plans[i];
-      if (p.role == 1)
-        continue; // produced by the dual launch of op i+1
+      if (p.role == 1 || p.role == 4)
+        continue; // produced by the dual launch of op i+1 / the MLP launch
+      if (p.role == 3) {
+        for (size_t j = i; j < i + 3; ++j)
+          check_supported(KERNEL_SPECS[plans[j].kernel], res[j]);
+        launch_mlp(ops, res, i, scratch, host_status, stream);
+        continue;
+      }
       const KernelSpec &s = KERNEL_SPECS[p.kernel];
       check_supported(s, res[i]);
       if (s.is_gemv())
@@ -408,11 +573,13 @@ struct ExecutorImpl {
     ScratchNeed need = total_need(res, plans);
     slot->scratch.ensure(need.splitk, need.partial, need.counters);
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
-    record(ops, res, plans, slot->scratch, slot->stream);
+    record(ops, res, plans, slot->scratch, slot->host_status, slot->stream);
     hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
     hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
     float ms = 0.f;
     hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
+    if (has_mlp(plans))
+      check_host_status(slot->host_status);
     return (uint64_t)((double)ms * 1e6);
   }
 
@@ -647,8 +814,7 @@ struct ExecutorImpl {
     if (graph)
       mark_fusions(ops, plans);
     for (size_t i = 0; i < ops.size(); ++i)
-      if (plans[i].role != 1)
-        check_supported(KERNEL_SPECS[plans[i].kernel], res[i]);
+      check_supported(KERNEL_SPECS[plans[i].kernel], res[i]);
 
     std::unique_ptr<PreparedOps> p(new PreparedOps());
     p->exec_ = owner;
@@ -667,12 +833,14 @@ struct ExecutorImpl {
     ScratchNeed need = total_need(res, plans);
     scratch.ensure(need.splitk, need.partial, need.counters);
     p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters};
+    if (has_mlp(plans))
+      p->status_ = alloc_host_status();
 
     hipGraph_t g = nullptr;
     hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal),
               "hipStreamBeginCapture");
     try {
-      record(ops, res, plans, scratch, stream);
+      record(ops, res, plans, scratch, static_cast<uint32_t *>(p->status_), stream);
     } catch (...) {
       (void)hipStreamEndCapture(stream, &g);
       if (g)
@@ -715,6 +883,7 @@ Executor::Executor(std::shared_ptr<Context> ctx, KernelSelection selection, Exec
     hip_check(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
     hip_check(hipEventCreate(&s->start), "hipEventCreate");
     hip_check(hipEventCreate(&s->end), "hipEventCreate");
+    s->host_status = alloc_host_status();
     impl_->all_slots.push_back(s);
     impl_->free_slots.push_back(s);
   }
@@ -747,6 +916,8 @@ Executor::~Executor() {
     (void)hipEventDestroy(s->start);
     (void)hipEventDestroy(s->end);
     (void)hipStreamDestroy(s->stream);
+    if (s->host_status)
+      (void)hipHostFree(s->host_status);
     delete s;
   }
 }
@@ -893,6 +1064,8 @@ PreparedOps::~PreparedOps() {
     (void)hipEventDestroy(static_cast<hipEvent_t>(ev_start_));
   if (ev_end_)
     (void)hipEventDestroy(static_cast<hipEvent_t>(ev_end_));
+  if (status_)
+    (void)hipHostFree(status_);
   if (s)
     (void)hipStreamDestroy(s);
 }
@@ -906,6 +1079,8 @@ void PreparedOps::run_silent() {
   submit();
   hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "hipStreamSynchronize");
   in_flight_ = false;
+  if (status_)
+    check_host_status(static_cast<uint32_t *>(status_));
 }
 
 // src/executor/prepared.rs:293-307.
@@ -931,6 +1106,8 @@ RunStats PreparedOps::wait() {
   hip_check(hipEventElapsedTime(&ms, static_cast<hipEvent_t>(ev_start_),
                                 static_cast<hipEvent_t>(ev_end_)),
             "hipEventElapsedTime");
+  if (status_)
+    check_host_status(static_cast<uint32_t *>(status_));
   return RunStats{(uint64_t)((double)ms * 1e6), n_calls_, flops_};
 }
 

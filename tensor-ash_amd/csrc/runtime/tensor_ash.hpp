@@ -237,6 +237,7 @@ private:
   void *graph_exec_ = nullptr;
   void *ev_start_ = nullptr, *ev_end_ = nullptr;
   std::vector<void *> scratch_;
+  void *status_ = nullptr; // decode-MLP wait status word, when the graph has one
   bool in_flight_ = false;
   bool submitted_once_ = false;
   size_t n_calls_ = 0;

@@ -75,11 +75,15 @@ def test_packed_gemv_epilogues(ta, ex, oracle, m, epi):
     check_f16(ex.download(ty), ref, k, oracle)
 
 
-@pytest.mark.parametrize("m", [1, 4, 8])
-def test_swiglu_mlp_graph(ta, ex, oracle, m):
+@pytest.mark.parametrize("m", [1, 3, 4, 8])
+def test_swiglu_mlp_graph(ta, ex, oracle, m, monkeypatch):
     """up; gate with SiLU*Mul{up}; down with +residual, as
     one dependent op graph (tools/llama-ash forward/mod.rs:186-210).  The
-    up/gate pair is fused into one dual-GEMV launch."""
+    three ops run as one persistent decode-MLP launch.  The gate/up outputs
+    are bit-identical to the unfused launches (same K windows); the
+    down-proj sums K in 512-row windows inside the MLP launch and in the
+    planner's windows standalone, so both are checked against the oracle,
+    and repeated MLP launches must repeat their bits."""
     hdim, ffn = 2048, 5632
     wg, wgr = f16_weights(oracle, hdim, ffn, 101)
     wu, wur = f16_weights(oracle, hdim, ffn, 102)
@@ -112,6 +116,45 @@ def test_swiglu_mlp_graph(ta, ex, oracle, m):
     ex.run_ops([ta.MatmulOp(tx, tg, h2, epilogue=ta.Epilogue(activation=2, binary=2, d=up2), packed_b=True)])
     np.testing.assert_array_equal(ex.download(up2), ex.download(up))
     np.testing.assert_array_equal(ex.download(h2), ex.download(h))
+    y_mlp = ex.download(y).copy()
+    monkeypatch.setenv("TA_NO_MLP", "1")
+    y2 = ex.tensor([m, hdim])
+    ex.run_op_graph(ops[:2] + [ta.MatmulOp(h, td, y2, epilogue=ops[2].epilogue, packed_b=True)])
+    check_f16(ex.download(y2), ref_y, ffn, oracle)
+    monkeypatch.delenv("TA_NO_MLP")
+    # repeated launches reuse the self-resetting tickets and flags
+    for _ in range(3):
+        ex.run_op_graph(ops)
+        np.testing.assert_array_equal(ex.download(y), y_mlp)
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_decode_mlp_down_epilogue(ta, ex, oracle, m):
+    """Persistent MLP with a general down-proj epilogue (bias + GELU) and a
+    gate bias, on non-square dims (H=768, F=1536)."""
+    hdim, ffn = 768, 1536
+    wg, wgr = f16_weights(oracle, hdim, ffn, 201)
+    wu, wur = f16_weights(oracle, hdim, ffn, 202)
+    wd, wdr = f16_weights(oracle, ffn, hdim, 203)
+    x = oracle.fill_det(m * hdim, 204)
+    bg, bd = oracle.fill_det(ffn, 205), oracle.fill_det(hdim, 206)
+    pk = lambda w, k, n: ex.tensor_from(ta.pack_f16w_row_tiles(w, k, n, 64), shape=[k, n], f16=True)
+    tg, tu, td = pk(wg, hdim, ffn), pk(wu, hdim, ffn), pk(wd, ffn, hdim)
+    tx = ex.tensor_from(x, shape=[m, hdim])
+    tbg, tbd = ex.tensor_from(bg, shape=[ffn]), ex.tensor_from(bd, shape=[hdim])
+    up, h, y = ex.tensor([m, ffn]), ex.tensor([m, ffn]), ex.tensor([m, hdim])
+    ex.run_op_graph([
+        ta.MatmulOp(tx, tu, up, alpha=0.5, packed_b=True),
+        ta.MatmulOp(tx, tg, h, alpha=0.5, epilogue=ta.Epilogue(bias=tbg, activation=2, binary=2, d=up),
+                    packed_b=True),
+        ta.MatmulOp(h, td, y, epilogue=ta.Epilogue(bias=tbd, activation=3), packed_b=True),
+    ])
+    ref_up = oracle.cpu_bmm(x, wur, None, 1, m, ffn, hdim, 0.5)
+    ref_h = oracle.reference_gemm(x, wgr, 1, m, ffn, hdim, 0.5, bias=bg, act=2, binary=2, d=ref_up)
+    check_f16(ex.download(up), ref_up, hdim, oracle)
+    check_f16(ex.download(h), ref_h, hdim, oracle)
+    ref_y = oracle.reference_gemm(ex.download(h).reshape(-1), wdr, 1, m, hdim, ffn, bias=bd, act=3)
+    check_f16(ex.download(y), ref_y, ffn, oracle)
 
 
 @pytest.mark.parametrize("f16", [True, False])
