@@ -75,11 +75,16 @@ def headline(ta, ex, steps: int, warmup: int):
     )
 
 
-def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=60):
+def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=30, layers=10):
     """Config 3: h = silu(x@Wg) * (x@Wu); y = h@Wd + res, packed f16 weights.
-    The op graph is prepared once per weight copy (hipGraph: one dual
-    gate/up GEMV launch + one down GEMV launch) and copies are rotated so
-    the working set (5 x 69 MB) exceeds the 256 MB last-level cache."""
+
+    A decode forward runs its layers back to back, so the step is timed the
+    same way: one prepared op graph (hipGraph) chains `layers` MLP layers,
+    layer l reading the previous layer's y as x and as residual, over
+    `copies` weight sets rotated so the working set exceeds the 256 MB
+    last-level cache (every layer reads its weights from HBM).  step_us is
+    the graph's GPU time / layers.  launch_us is one layer prepared alone,
+    where the events also bracket the graph launch latency."""
     hdim, ffn = 2048, 5632
     w_bytes = 2 * (2 * hdim * ffn) + 2 * ffn * hdim
     copies = max(5, math.ceil(LLC_BYTES / w_bytes) + 1)
@@ -92,33 +97,41 @@ def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=60):
             ws.append(ex.tensor_from(ta.pack_f16w_row_tiles(w, kk, nn, ta.f16w_row_tile_n(kk, nn)),
                                      shape=[kk, nn], f16=True))
         weights.append(ws)
+
+    def layer_ops(x, y, up, h, w):
+        wg, wu, wd = w
+        return [ta.MatmulOp(x, wu, up, packed_b=True),
+                ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=ta.ACTIVATION_SILU,
+                                                           binary=ta.BINARY_MUL, d=up), packed_b=True),
+                ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0),
+                            packed_b=True)]
+
     out = {}
     for m in rows_list:
-        x = ex.tensor_from(rng.uniform(-1, 1, (m, hdim)).astype(np.float32))
-        res = ex.tensor_from(rng.uniform(-1, 1, (m, hdim)).astype(np.float32))
-        up, h, y = ex.tensor([m, ffn]), ex.tensor([m, ffn]), ex.tensor([m, hdim])
-        preps = []
-        for (wg, wu, wd) in weights:
-            ops = [ta.MatmulOp(x, wu, up, packed_b=True),
-                   ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=ta.ACTIVATION_SILU,
-                                                              binary=ta.BINARY_MUL, d=up), packed_b=True),
-                   ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=res, beta=1.0),
-                               packed_b=True)]
-            preps.append(ex.prepare_op_graph(ops))
-        for i in range(2 * copies):
-            preps[i % copies].run()
+        bufs = [ex.tensor_from(rng.uniform(-1, 1, (m, hdim)).astype(np.float32)) for _ in range(2)]
+        up, h = ex.tensor([m, ffn]), ex.tensor([m, ffn])
+        ops = []
+        for l in range(layers):
+            ops += layer_ops(bufs[l % 2], bufs[(l + 1) % 2], up, h, weights[l % copies])
+        chain = ex.prepare_op_graph(ops)
+        single = ex.prepare_op_graph(layer_ops(bufs[0], bufs[1], up, h, weights[0]))
+        for _ in range(3):
+            chain.run()
+            single.run()
         stats = []
         t0 = time.perf_counter()
         for i in range(iters):
-            stats.append(preps[i % copies].run())
+            stats.append(chain.run())
         wall = time.perf_counter() - t0
+        single_ns = median_ns([single.run() for _ in range(iters)])
         bytes_step = w_bytes + 4 * m * (hdim + 2 * ffn + 2 * hdim)
-        step_ns = median_ns(stats)
+        step_ns = median_ns(stats) / layers
         out[f"M{m}"] = dict(step_us=step_ns / 1e3, gbps=bytes_step / step_ns,
                             frac_hbm=bytes_step / step_ns / PEAK_HBM, bytes_per_step=bytes_step,
-                            wall_us_per_step=wall / iters * 1e6)
-        for p in preps:
-            p.close()
+                            layers_per_graph=layers, launch_us=single_ns / 1e3,
+                            wall_us_per_step=wall / iters / layers * 1e6)
+        chain.close()
+        single.close()
     return out
 
 

@@ -50,8 +50,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
-// Standalone launch, decode-MLP producer (signals per-tile readiness of its
-// outputs), decode-MLP consumer (waits for the producer tiles its X reads).
+// Standalone launch, decode-MLP producer (gate/up, publishes tagged h),
+// decode-MLP consumer (down-proj, polls the tagged h its window reads).
 enum { kStandalone = 0, kProducer = 1, kConsumer = 2 };
 
 TA_DEVICE float coherent_load(const float *p) {
@@ -59,6 +59,48 @@ TA_DEVICE float coherent_load(const float *p) {
 }
 TA_DEVICE void coherent_store(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Decode-MLP hand-off word: f32 value bits low, launch tag high; one
+// naturally aligned 64-bit access, so a reader sees value and tag together.
+TA_DEVICE uint64_t tag_word(float v, uint32_t tag) {
+  return ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
+}
+TA_DEVICE uint64_t load_word(const uint64_t *p) {
+  return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+TA_DEVICE void store_word(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every thread reads N tagged words (address at(j), needed when need(j));
+// the workgroup re-reads them all until every needed word of every thread
+// carries `tag`, sleeping ~0.05 us between rounds.  out[] holds the values
+// of the last round.  Bounded: after spin_limit rounds the wait gives up
+// and raises the host-visible status word (the launch's results are then
+// invalid).
+template <int N, class At, class Need>
+TA_DEVICE void poll_words(At at, Need need, uint32_t tag, float (&out)[N], const MlpArgs &m) {
+  for (uint32_t polls = 0;;) {
+    uint64_t w[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      w[j] = load_word(at(j));
+    int ok = 1;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      ok &= (!need(j) || (uint32_t)(w[j] >> 32) == tag) ? 1 : 0;
+      out[j] = __builtin_bit_cast(float, (uint32_t)w[j]);
+    }
+    if (__syncthreads_and(ok))
+      return;
+    if (++polls >= m.spin_limit) {
+      if (threadIdx.x == 0)
+        __hip_atomic_store(m.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
 }
 
 template <int MR, bool DUAL, int TW, bool WF32, int MODE, int XROWS, int UNROLL = 16>
@@ -94,59 +136,17 @@ struct Gemv {
     }
   }
 
-  // Consumer: wait until every producer tile covering X columns
-  // [k0, kend) has published its outputs.  Polling starts only once this
-  // workgroup's own weight loads have landed (vmcnt(0)) and sleeps ~0.2 us
-  // between polls, so waiting units do not flood the memory system.
-  // Bounded: after spin_limit polls the wait gives up and raises the
-  // host-visible status word (the launch's results are then invalid).
-  static TA_DEVICE void wait_ready(const GemvArgs &p, uint32_t k0, uint32_t kend) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // One lane per producer tile polls its flag (all polls in parallel).
-    const uint32_t t_lo = k0 / p.x_tile, t_hi = (kend - 1) / p.x_tile;
-    if (threadIdx.x <= t_hi - t_lo) {
-      {
-        const uint32_t t = t_lo + threadIdx.x;
-        uint32_t polls = 0;
-        while (__hip_atomic_load(&p.ready[t * TA_GEMV_COUNTER_STRIDE], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-          __builtin_amdgcn_s_sleep(8);
-          if (++polls >= p.spin_limit) {
-            __hip_atomic_store(p.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            break;
-          }
-        }
-      }
-    }
-    __syncthreads();
-    TA_GEMV_TRACE(6);
-  }
-
-  // Consumer, after X is read: count this unit as a reader of each
-  // producer tile; the last reader clears the tile's flag (and its count)
-  // for the next launch.
-  static TA_DEVICE void ack_ready(const GemvArgs &p, uint32_t k0, uint32_t kend) {
-    const uint32_t t_lo = k0 / p.x_tile, t_hi = (kend - 1) / p.x_tile;
-    if (threadIdx.x <= t_hi - t_lo) {
-      {
-        const uint32_t t = t_lo + threadIdx.x;
-        uint32_t *ack = &p.acks[t * TA_GEMV_COUNTER_STRIDE];
-        if (__hip_atomic_fetch_add(ack, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            p.x_readers - 1) {
-          __hip_atomic_store(ack, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(&p.ready[t * TA_GEMV_COUNTER_STRIDE], 0u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
-  }
-
-  static TA_DEVICE void unit(const GemvArgs &p, uint32_t tile, uint32_t chunk, Smem &sm) {
+  static TA_DEVICE void unit(const GemvArgs &p, uint32_t tile, uint32_t chunk, Smem &sm,
+                             const MlpArgs *mlp = nullptr) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t tiles = (p.n + TW - 1) / TW;
     const uint32_t k0 = chunk * p.kchunk;
     const uint32_t kend = min(p.k, k0 + p.kchunk);
     const bool packed = p.flags & TA_GEMV_PACKED;
+    // Decode MLP: this launch's hand-off tag (read before any hand-off).
+    uint32_t tag = 0;
+    if constexpr (MODE != kStandalone)
+      tag = __hip_atomic_load(mlp->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     TA_GEMV_TRACE(0);
 
     const uint32_t cp = lane % LPR, r0 = lane / LPR;
@@ -182,39 +182,54 @@ struct Gemv {
     // X window: XPT values per thread, clamped index + select (no branch).
     constexpr int XPT = XROWS * MR / kThreads;
     float xr[XPT];
-    auto load_x = [&]() {
-#pragma unroll
-      for (int j = 0; j < XPT; ++j) {
-        const uint32_t i = tid + j * kThreads;
-        const uint32_t kk = i / MR, m = i % MR;
-        const bool ok = i < p.kchunk * MR && m < p.rows && k0 + kk < kend;
-        const float *src = p.x + (ok ? (uint64_t)m * p.k + k0 + kk : 0);
-        if constexpr (MODE == kConsumer)
-          xr[j] = coherent_load(src); // written by producer units of this launch
-        else
-          xr[j] = *src;
-        xr[j] = ok ? xr[j] : 0.0f;
-      }
+    auto x_index = [&](int j, bool &ok) {
+      const uint32_t i = tid + j * kThreads;
+      const uint32_t kk = i / MR, m = i % MR;
+      ok = i < p.kchunk * MR && m < p.rows && k0 + kk < kend;
+      return ok ? (uint64_t)m * p.k + k0 + kk : 0;
     };
 
     uint64_t cur[WAYS][kUnroll];
     if constexpr (MODE == kConsumer) {
-      // Weights first (they do not depend on X), then wait for X.
+      // Weights first (they do not depend on X), then poll the tagged h
+      // words of the window ([k][MR] order) until all carry this launch's
+      // tag; vmcnt retires in order, so the first poll lands after them.
       issue(0, cur);
-      wait_ready(p, k0, kend);
-      load_x();
+      poll_words<XPT>(
+          [&](int j) {
+            bool ok;
+            (void)x_index(j, ok);
+            const uint32_t i = tid + j * kThreads;
+            return mlp->tag_h + (ok ? (uint64_t)k0 * MR + i : 0);
+          },
+          [&](int j) {
+            bool ok;
+            (void)x_index(j, ok);
+            return ok;
+          },
+          tag, xr, *mlp);
+#pragma unroll
+      for (int j = 0; j < XPT; ++j) {
+        bool ok;
+        (void)x_index(j, ok);
+        xr[j] = ok ? xr[j] : 0.0f;
+      }
     } else {
       // X loads go out first, then the first weight group: vmcnt retires
       // in issue order, so staging X into LDS then waits only for X.
-      load_x();
+#pragma unroll
+      for (int j = 0; j < XPT; ++j) {
+        bool ok;
+        const uint64_t xi = x_index(j, ok);
+        xr[j] = p.x[xi];
+        xr[j] = ok ? xr[j] : 0.0f;
+      }
       issue(0, cur);
     }
 #pragma unroll
     for (int j = 0; j < XPT; ++j)
       sm.xs[tid + j * kThreads] = xr[j];
-    __syncthreads(); // all of X is in registers/LDS: the unit's reads are done
-    if constexpr (MODE == kConsumer)
-      ack_ready(p, k0, kend);
+    __syncthreads();
     TA_GEMV_TRACE(1);
 
     float acc[WAYS][MR][CPL];
@@ -226,35 +241,47 @@ struct Gemv {
         for (int c = 0; c < CPL; ++c)
           acc[w][m][c] = 0.0f;
 
+    // X rows are read from LDS in batches of XB (8 floats), all reads of
+    // a batch before any use, so their latencies overlap.
+    constexpr int XB = MR >= 8 ? 1 : 8 / MR;
+    static_assert(kUnroll % XB == 0, "whole X batches per group");
     auto consume = [&](uint32_t kb, const uint64_t (&raw)[WAYS][kUnroll]) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const uint32_t kk = kb + u * RPW + my_first;
-        const bool ok = k0 + kk < kend && col_ok;
-        float xv[MR];
-        if constexpr (MR >= 4) {
+      for (int u0 = 0; u0 < kUnroll; u0 += XB) {
+        float xv[XB][MR];
 #pragma unroll
-          for (int q = 0; q < MR / 4; ++q) {
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(&sm.xs[kk * MR + 4 * q]);
-            xv[4 * q] = v[0];
-            xv[4 * q + 1] = v[1];
-            xv[4 * q + 2] = v[2];
-            xv[4 * q + 3] = v[3];
+        for (int b = 0; b < XB; ++b) {
+          const uint32_t kk = kb + (u0 + b) * RPW + my_first;
+          if constexpr (MR >= 4) {
+#pragma unroll
+            for (int q = 0; q < MR / 4; ++q) {
+              const f32x4 v = *reinterpret_cast<const f32x4 *>(&sm.xs[kk * MR + 4 * q]);
+              xv[b][4 * q] = v[0];
+              xv[b][4 * q + 1] = v[1];
+              xv[b][4 * q + 2] = v[2];
+              xv[b][4 * q + 3] = v[3];
+            }
+          } else {
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+              xv[b][m] = sm.xs[kk * MR + m];
           }
-        } else {
-#pragma unroll
-          for (int m = 0; m < MR; ++m)
-            xv[m] = sm.xs[kk * MR + m];
         }
 #pragma unroll
-        for (int w = 0; w < WAYS; ++w) {
-          float wv[CPL];
-          unpack(ok ? raw[w][u] : 0ull, wv);
+        for (int b = 0; b < XB; ++b) {
+          const int u = u0 + b;
+          const uint32_t kk = kb + u * RPW + my_first;
+          const bool ok = k0 + kk < kend && col_ok;
 #pragma unroll
-          for (int m = 0; m < MR; ++m)
+          for (int w = 0; w < WAYS; ++w) {
+            float wv[CPL];
+            unpack(ok ? raw[w][u] : 0ull, wv);
 #pragma unroll
-            for (int c = 0; c < CPL; ++c)
-              acc[w][m][c] = fmaf(xv[m], wv[c], acc[w][m][c]);
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+              for (int c = 0; c < CPL; ++c)
+                acc[w][m][c] = fmaf(xv[b][m], wv[c], acc[w][m][c]);
+          }
         }
       }
     };
@@ -305,78 +332,152 @@ struct Gemv {
       part[i] = s;
     }
 
-    if (p.kchunks > 1) {
-      uint32_t *counter = &p.counters[tile * TA_GEMV_COUNTER_STRIDE];
-      float *mine = p.partial + ((uint64_t)chunk * tiles + tile) * OUTS;
-#pragma unroll
-      for (int i = 0; i < OPT; ++i) {
-        const uint32_t o = tid + i * kThreads;
-        if (o < OUTS)
-          coherent_store(mine + o, part[i]);
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      TA_GEMV_TRACE(3);
-      if (tid == 0) {
-        const uint32_t seen =
-            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sm.last_flag = (seen == p.kchunks - 1) ? 1u : 0u;
-      }
-      __syncthreads();
-      TA_GEMV_TRACE(4);
-      if (!sm.last_flag)
+    if constexpr (MODE == kStandalone) {
+      if (p.kchunks > 1 && !standalone_reduce(p, tile, chunk, tiles, part, sm))
         return;
-      // Sum the windows in order 0..kchunks-1.  A batch of NB windows is
-      // loaded at once (16 loads per thread, one memory round trip) into the
-      // X window's LDS, which is free now; then each output adds its
-      // windows sequentially.
-      const uint64_t step = (uint64_t)tiles * OUTS;
-      const float *tsrc = p.partial + (uint64_t)tile * OUTS;
-      constexpr uint32_t NB = PSTAGE / OUTS; // windows per batch
-      static_assert(NB >= 1, "staging holds at least one partial");
-      float sum[OPT];
-#pragma unroll
-      for (int i = 0; i < OPT; ++i)
-        sum[i] = 0.0f;
-      for (uint32_t c0 = 0; c0 < p.kchunks; c0 += NB) {
-        const uint32_t nb = min(NB, p.kchunks - c0);
-        __syncthreads(); // previous batch fully consumed
-        float v[PSTAGE / kThreads];
-#pragma unroll
-        for (int j = 0; j < PSTAGE / kThreads; ++j) {
-          const uint32_t e = tid + j * kThreads;
-          const bool ok = e < nb * OUTS;
-          const uint32_t c = c0 + (ok ? e / OUTS : 0), o = ok ? e % OUTS : 0;
-          v[j] = coherent_load(tsrc + c * step + o);
-        }
-#pragma unroll
-        for (int j = 0; j < PSTAGE / kThreads; ++j)
-          sm.xs[tid + j * kThreads] = v[j];
-        __syncthreads();
+      epilogue(p, tile, part, sm, nullptr, 0);
+    } else {
+      // Decode MLP: windows other than the tile's last store tagged
+      // partials and finish; the last window's unit (highest workgroup
+      // id of the tile) polls them, sums windows 0..kchunks-1 in order and
+      // applies the epilogue.
+      uint64_t *tbuf = MODE == kProducer ? mlp->tag_a : mlp->tag_b;
+      if (chunk + 1 < p.kchunks) {
+        uint64_t *mine = tbuf + ((uint64_t)chunk * tiles + tile) * OUTS;
 #pragma unroll
         for (int i = 0; i < OPT; ++i) {
           const uint32_t o = tid + i * kThreads;
           if (o < OUTS)
-            for (uint32_t c = 0; c < nb; ++c)
-              sum[i] = (c0 + c == 0) ? sm.xs[o] : sum[i] + sm.xs[c * OUTS + o];
+            store_word(mine + o, tag_word(part[i], tag));
+        }
+        TA_GEMV_TRACE(3);
+        return;
+      }
+      if (p.kchunks > 1) {
+        // Poll the other windows' words with all threads (NB windows per
+        // round of 16 loads per thread), stage them in the X window's LDS,
+        // then each output adds its windows in order.
+        constexpr uint32_t NB = PSTAGE / OUTS;
+        float sum[OPT];
+        for (uint32_t c0 = 0; c0 + 1 < p.kchunks; c0 += NB) {
+          const uint32_t nb = min(NB, p.kchunks - 1 - c0);
+          float v[PSTAGE / kThreads];
+          poll_words<PSTAGE / kThreads>(
+              [&](int j) {
+                const uint32_t e = tid + j * kThreads;
+                const bool ok = e < nb * OUTS;
+                const uint32_t c = c0 + (ok ? e / OUTS : 0), o = ok ? e % OUTS : 0;
+                return tbuf + ((uint64_t)c * tiles + tile) * OUTS + o;
+              },
+              [&](int j) { return tid + j * kThreads < nb * OUTS; }, tag, v, *mlp);
+          __syncthreads(); // previous round's values consumed
+#pragma unroll
+          for (int j = 0; j < PSTAGE / kThreads; ++j)
+            sm.xs[tid + j * kThreads] = v[j];
+          __syncthreads();
+#pragma unroll
+          for (int i = 0; i < OPT; ++i) {
+            const uint32_t o = tid + i * kThreads;
+            if (o < OUTS)
+              for (uint32_t c = 0; c < nb; ++c)
+                sum[i] = (c0 + c == 0) ? sm.xs[o] : sum[i] + sm.xs[c * OUTS + o];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < OPT; ++i)
+          part[i] = sum[i] + part[i];
+      }
+      TA_GEMV_TRACE(5);
+      epilogue(p, tile, part, sm, MODE == kProducer ? mlp->tag_h : nullptr, tag);
+      if constexpr (MODE == kConsumer) {
+        // The last down tile of the launch advances the generation: every
+        // unit has read it by then (each one's hand-off words, which carry
+        // the tag, are what this tile's inputs waited for).
+        if (tid == 0 && __hip_atomic_fetch_add(mlp->done, 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT) == mlp->tiles_b - 1) {
+          __hip_atomic_store(mlp->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(mlp->gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-#pragma unroll
-      for (int i = 0; i < OPT; ++i)
-        part[i] = sum[i];
-      if (tid == 0)
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
 
-    TA_GEMV_TRACE(5);
-    // Epilogue (shaders/matmul_epilogue_common.glsl:14-21 order).  A
-    // producer publishes its outputs with coherent stores, then its flag.
-    auto put = [&](float *dst, float v) {
-      if constexpr (MODE == kProducer)
-        coherent_store(dst, v);
-      else
-        *dst = v;
-    };
+  // Standalone K-window reduction: store this window's partial; the last
+  // unit of the tile to arrive (integer counter) sums windows
+  // 0..kchunks-1 in order into `part` and returns true.
+  static TA_DEVICE bool standalone_reduce(const GemvArgs &p, uint32_t tile, uint32_t chunk,
+                                          uint32_t tiles, float (&part)[OPT], Smem &sm) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t *counter = &p.counters[tile * TA_GEMV_COUNTER_STRIDE];
+    float *mine = p.partial + ((uint64_t)chunk * tiles + tile) * OUTS;
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+      const uint32_t o = tid + i * kThreads;
+      if (o < OUTS)
+        coherent_store(mine + o, part[i]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    TA_GEMV_TRACE(3);
+    if (tid == 0) {
+      const uint32_t seen =
+          __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sm.last_flag = (seen == p.kchunks - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    TA_GEMV_TRACE(4);
+    if (!sm.last_flag)
+      return false;
+    // Sum the windows in order 0..kchunks-1.  A batch of NB windows is
+    // loaded at once (16 loads per thread, one memory round trip) into the
+    // X window's LDS, which is free now; then each output adds its
+    // windows sequentially.
+    const uint64_t step = (uint64_t)tiles * OUTS;
+    const float *tsrc = p.partial + (uint64_t)tile * OUTS;
+    constexpr uint32_t NB = PSTAGE / OUTS; // windows per batch
+    static_assert(NB >= 1, "staging holds at least one partial");
+    float sum[OPT];
+#pragma unroll
+    for (int i = 0; i < OPT; ++i)
+      sum[i] = 0.0f;
+    for (uint32_t c0 = 0; c0 < p.kchunks; c0 += NB) {
+      const uint32_t nb = min(NB, p.kchunks - c0);
+      __syncthreads(); // previous batch fully consumed
+      float v[PSTAGE / kThreads];
+#pragma unroll
+      for (int j = 0; j < PSTAGE / kThreads; ++j) {
+        const uint32_t e = tid + j * kThreads;
+        const bool ok = e < nb * OUTS;
+        const uint32_t c = c0 + (ok ? e / OUTS : 0), o = ok ? e % OUTS : 0;
+        v[j] = coherent_load(tsrc + c * step + o);
+      }
+#pragma unroll
+      for (int j = 0; j < PSTAGE / kThreads; ++j)
+        sm.xs[tid + j * kThreads] = v[j];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < OPT; ++i) {
+        const uint32_t o = tid + i * kThreads;
+        if (o < OUTS)
+          for (uint32_t c = 0; c < nb; ++c)
+            sum[i] = (c0 + c == 0) ? sm.xs[o] : sum[i] + sm.xs[c * OUTS + o];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < OPT; ++i)
+      part[i] = sum[i];
+    if (tid == 0)
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+
+  // Epilogue (shaders/matmul_epilogue_common.glsl:14-21 order) on the
+  // tile's K-summed outputs.  Dual mode writes U and Y; with `h_tag` it
+  // also publishes Y as tagged words [col][MR] for the decode MLP's down
+  // units.
+  static TA_DEVICE void epilogue(const GemvArgs &p, uint32_t tile, const float (&part)[OPT],
+                                 Smem &sm, uint64_t *h_tag, uint32_t tag) {
+    const uint32_t tid = threadIdx.x;
     if constexpr (DUAL) {
       __syncthreads();
 #pragma unroll
@@ -395,8 +496,11 @@ struct Gemv {
         float g = p.alpha * sm.red[o];
         if (p.flags & TA_FLAG_BIAS)
           g += p.bias[c];
-        put(p.y2 + yi, u);
-        put(p.y + yi, ta_activate(g, p.act) * u);
+        const float h = ta_activate(g, p.act) * u;
+        p.y2[yi] = u;
+        p.y[yi] = h;
+        if (h_tag)
+          store_word(h_tag + (uint64_t)c * MR + m, tag_word(h, tag));
       }
     } else {
 #pragma unroll
@@ -416,15 +520,8 @@ struct Gemv {
           v = fmaf(p.beta, p.d[yi], v);
         else if (p.binary == TA_BIN_MUL)
           v *= p.d[yi];
-        put(p.y + yi, v);
+        p.y[yi] = v;
       }
-    }
-    if constexpr (MODE == kProducer) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (tid == 0)
-        __hip_atomic_store(&p.ready[tile * TA_GEMV_COUNTER_STRIDE], 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
@@ -439,15 +536,17 @@ struct Gemv {
 template <int MR> constexpr int standalone_rows() { return 4096 / MR; }
 
 // Persistent decode MLP.  Workgroup ids below units_a run gate/up
-// (producer) units, the rest run down-proj (consumer) units.  Producers
-// never wait, and each XCD dispatches its workgroups in id order, so every
-// producer a consumer waits for has been dispatched before that consumer
-// and runs to completion; the bounded wait is a safety net only.  No
-// launch-wide counter exists (one hot atomic would serialise the starts).
+// (producer) units, the rest run down-proj (consumer) units.  Every wait
+// is on units with lower workgroup ids (down units on gate/up units; the
+// last K window of a tile, which has the tile's highest id, on the tile's
+// other windows), and workgroups are dispatched in id order, so a waited-on
+// unit has always been dispatched and never waits on its waiter; the
+// bounded wait is a safety net only.  No launch-wide counter is touched at
+// unit start (one hot atomic would serialise the starts).
 // K windows: gate/up units take 256 rows (one group of 16 loads per
 // matrix); down units take 512 rows (one group of 32 loads) so they are
-// fewer, every workgroup of the launch is resident at once, and a down
-// unit's whole weight window is in flight before it starts waiting.
+// fewer and a down unit's whole weight window is in flight before it
+// starts waiting.
 constexpr int kMlpRowsA = 256;
 constexpr int kMlpRowsB = 512;
 
@@ -464,9 +563,9 @@ template <int MR> struct DecodeMlp {
     const uint32_t r = blockIdx.x;
     TA_GEMV_TRACE_ROLE(r);
     if (r < p.units_a)
-      A::unit(p.a, r % p.tiles_a, r / p.tiles_a, sm.a);
+      A::unit(p.a, r % p.tiles_a, r / p.tiles_a, sm.a, &p);
     else
-      B::unit(p.b, (r - p.units_a) % p.tiles_b, (r - p.units_a) / p.tiles_b, sm.b);
+      B::unit(p.b, (r - p.units_a) % p.tiles_b, (r - p.units_a) / p.tiles_b, sm.b, &p);
   }
 };
 
@@ -489,12 +588,15 @@ TA_GEMV_ROWS(ta_gemv_f16_t32, false, 32, false)
 TA_GEMV_ROWS(ta_gemv_f16_t32_dual, true, 32, false)
 TA_GEMV_ROWS(ta_gemv_f32_t64, false, 64, true)
 
-#define TA_MLP(MR)                                                                 \
-  extern "C" __global__ __launch_bounds__(kThreads) void ta_decode_mlp_f16_t64_m##MR( \
-      MlpArgs p) {                                                                 \
+// WAVES: waves per SIMD the register budget must allow, so every
+// workgroup of the launch can be resident (4: <= 128 VGPRs, 3: <= 168).
+#define TA_MLP(MR, WAVES)                                                          \
+  extern "C" __global__ __launch_bounds__(kThreads)                                \
+      __attribute__((amdgpu_waves_per_eu(WAVES))) void ta_decode_mlp_f16_t64_m##MR( \
+          MlpArgs p) {                                                             \
     DecodeMlp<MR>::run(p);                                                         \
   }
-TA_MLP(1)
-TA_MLP(2)
-TA_MLP(4)
-TA_MLP(8)
+TA_MLP(1, 4)
+TA_MLP(2, 4)
+TA_MLP(4, 4)
+TA_MLP(8, 3)

@@ -88,9 +88,6 @@ typedef struct GemvArgs {
   const float *bias;
   float *partial;     // [kchunks][tiles][ways][MR][TW]
   uint32_t *counters; // [tiles * TA_GEMV_COUNTER_STRIDE]
-  uint32_t *ready;    // decode MLP: per producer tile "outputs written" flags
-  uint32_t *acks;     // decode MLP consumer: per producer tile reader count
-  uint32_t *status;   // decode MLP consumer: host-mapped, 1 if a wait gave up
   uint32_t rows, n, k;
   uint32_t kchunk;
   uint32_t kchunks;
@@ -99,21 +96,30 @@ typedef struct GemvArgs {
   uint32_t binary;
   float alpha;
   float beta;
-  uint32_t x_tile;     // decode MLP consumer: column tile width of X's producer
-  uint32_t spin_limit; // decode MLP consumer: polls before giving up
-  uint32_t x_readers;  // decode MLP consumer: units reading each producer tile
-  uint32_t pad;
 } GemvArgs;
 
 // Persistent decode SwiGLU MLP in one launch: `a` is the dual gate/up GEMV
 // (producer of h = act(x Wg) * (x Wu)), `b` the down-proj GEMV reading h.
-// Workgroups 0..units_a-1 run `a` units, the rest run `b` units, which wait
-// on the `a` tiles they read (flags in a.ready, reset by their last reader).
+// Workgroups 0..units_a-1 run `a` units (tile-major: unit u is tile
+// u % tiles_a, K window u / tiles_a), the rest run `b` units likewise.
+// Units hand data over as 64-bit words {f32 value, launch tag} that the
+// reader polls until the tag matches; the tag is *gen + 1, and the last
+// `b` tile to finish (counted in *done) advances *gen, so no hand-off word
+// ever needs clearing.  a.partial/a.counters and b.partial/b.counters are
+// unused: the tagged buffers below replace them.
 typedef struct MlpArgs {
   GemvArgs a;
   GemvArgs b;
+  uint64_t *tag_a;  // [kch_a][tiles_a][2][MR][64] gate/up window partials
+  uint64_t *tag_h;  // [K_b][MR] h = act(gate) * up, as the down units read it
+  uint64_t *tag_b;  // [kch_b][tiles_b][MR][64] down window partials
+  uint32_t *gen;    // launch generation (zero-initialised)
+  uint32_t *done;   // `b` tiles finished in this launch (zero between launches)
+  uint32_t *status; // host-mapped; set to 1 if a wait gave up
   uint32_t units_a, units_b;
   uint32_t tiles_a, tiles_b;
+  uint32_t spin_limit; // polls before a wait gives up
+  uint32_t pad;
 } MlpArgs;
 
 #ifdef __cplusplus

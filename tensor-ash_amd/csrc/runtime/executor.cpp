@@ -36,6 +36,10 @@ struct Scratch {
   uint64_t partial_bytes = 0;
   uint32_t *counters = nullptr;
   uint64_t counters_len = 0;
+  // Decode-MLP region (generation words + tagged hand-off words), used by
+  // no other kernel and zeroed when allocated or reset.
+  void *mlp = nullptr;
+  uint64_t mlp_bytes = 0;
 
   void release() {
     if (splitk)
@@ -44,9 +48,27 @@ struct Scratch {
       (void)hipFree(partial);
     if (counters)
       (void)hipFree(counters);
-    splitk = partial = nullptr;
+    if (mlp)
+      (void)hipFree(mlp);
+    splitk = partial = mlp = nullptr;
     counters = nullptr;
-    splitk_bytes = partial_bytes = counters_len = 0;
+    splitk_bytes = partial_bytes = counters_len = mlp_bytes = 0;
+  }
+  void ensure_mlp(uint64_t bytes) {
+    if (bytes <= mlp_bytes)
+      return;
+    if (mlp)
+      hip_check(hipFree(mlp), "hipFree");
+    mlp = nullptr;
+    hip_check(hipMalloc(&mlp, bytes), "hipMalloc (decode-MLP scratch)");
+    mlp_bytes = bytes;
+    reset_mlp();
+  }
+  // Zeroed again after a launch that gave up waiting (its hand-off words
+  // may carry the generation the next launch would use).
+  void reset_mlp() {
+    if (mlp)
+      hip_check(hipMemset(mlp, 0, mlp_bytes), "hipMemset (decode-MLP scratch)");
   }
   // Grow to at least the given sizes.  Counters start at zero (the GEMV
   // kernels reset them themselves after use).
@@ -92,11 +114,13 @@ uint32_t *alloc_host_status() {
   return static_cast<uint32_t *>(p);
 }
 
-void check_host_status(uint32_t *word) {
+void check_host_status(uint32_t *word, void *mlp, uint64_t mlp_bytes) {
   volatile uint32_t *w = word;
   if (*w != 0) {
     *w = 0;
-    fail("decode MLP: a down-proj unit gave up waiting for the gate/up outputs");
+    if (mlp)
+      hip_check(hipMemset(mlp, 0, mlp_bytes), "hipMemset (decode-MLP scratch)");
+    fail("decode MLP: a unit gave up waiting for its inputs");
   }
 }
 
@@ -113,11 +137,12 @@ struct OpPlan {
 uint32_t gemm_threads(const KernelSpec &s) { return s.tile_m == 256 && s.tile_n == 256 ? 512 : 256; }
 
 struct ScratchNeed {
-  uint64_t splitk = 0, partial = 0, counters = 0;
+  uint64_t splitk = 0, partial = 0, counters = 0, mlp = 0;
   void merge(const ScratchNeed &o) {
     splitk = std::max(splitk, o.splitk);
     partial = std::max(partial, o.partial);
     counters = std::max(counters, o.counters);
+    mlp = std::max(mlp, o.mlp);
   }
 };
 
@@ -411,8 +436,7 @@ struct ExecutorImpl {
       if (plans[i].role == 3) {
         MlpGeom g = mlp_geom(res[i], res[i + 2]);
         ScratchNeed m;
-        m.partial = g.partial_bytes;
-        m.counters = g.counters_len;
+        m.mlp = g.bytes;
         need.merge(m);
       } else if (plans[i].role != 1 && plans[i].role != 4) {
         need.merge(scratch_need(res[i], plans[i]));
@@ -422,11 +446,12 @@ struct ExecutorImpl {
   }
 
   // ---- persistent decode MLP: [up, gate*act*up, down] in one launch ----
+  // Byte offsets into Scratch::mlp: generation word, done counter (own
+  // 128-byte lines), then the tagged words of the gate/up partials, of h
+  // and of the down partials.
   struct MlpGeom {
     uint32_t mr, tiles_a, kch_a, tiles_b, kch_b;
-    uint64_t part_a_bytes, partial_bytes;
-    // u32 offsets into the counters buffer
-    uint64_t cnt_a, cnt_b, ready, acks, counters_len;
+    uint64_t gen, done, tag_a, tag_h, tag_b, bytes;
   };
   // K windows of the two phases (kernel constants kMlpRowsA / kMlpRowsB).
   static constexpr uint32_t kMlpRowsA = 256, kMlpRowsB = 512;
@@ -438,14 +463,13 @@ struct ExecutorImpl {
     g.kch_a = (up.k + kMlpRowsA - 1) / kMlpRowsA;
     g.tiles_b = down.n / 64;
     g.kch_b = (down.k + kMlpRowsB - 1) / kMlpRowsB;
-    g.part_a_bytes = ((uint64_t)g.kch_a * g.tiles_a * 2 * g.mr * 64 * 4 + 255) / 256 * 256;
-    g.partial_bytes = g.part_a_bytes + (uint64_t)g.kch_b * g.tiles_b * g.mr * 64 * 4;
-    const uint64_t S = TA_GEMV_COUNTER_STRIDE;
-    g.cnt_a = 0;
-    g.cnt_b = g.cnt_a + g.tiles_a * S;
-    g.ready = g.cnt_b + g.tiles_b * S;
-    g.acks = g.ready + g.tiles_a * S;
-    g.counters_len = g.acks + g.tiles_a * S;
+    auto al = [](uint64_t v) { return (v + 255) / 256 * 256; };
+    g.gen = 0;
+    g.done = 128;
+    g.tag_a = 256;
+    g.tag_h = al(g.tag_a + (uint64_t)g.kch_a * g.tiles_a * 2 * g.mr * 64 * 8);
+    g.tag_b = al(g.tag_h + (uint64_t)down.k * g.mr * 8);
+    g.bytes = al(g.tag_b + (uint64_t)g.kch_b * g.tiles_b * g.mr * 64 * 8);
     return g;
   }
 
@@ -473,7 +497,7 @@ struct ExecutorImpl {
                   size_t i, Scratch &scratch, uint32_t *host_status, hipStream_t stream) const {
     const MatmulOp &up = ops[i], &gate = ops[i + 1], &down = ops[i + 2];
     MlpGeom g = mlp_geom(res[i], res[i + 2]);
-    if (scratch.partial_bytes < g.partial_bytes || scratch.counters_len < g.counters_len)
+    if (scratch.mlp_bytes < g.bytes)
       fail("internal: decode-MLP scratch not reserved");
     if (!host_status)
       fail("internal: decode-MLP status word missing");
@@ -496,9 +520,6 @@ struct ExecutorImpl {
     }
     a.act = (uint32_t)gate.epilogue.activation;
     a.alpha = gate.call.alpha;
-    a.partial = static_cast<float *>(scratch.partial);
-    a.counters = scratch.counters + g.cnt_a;
-    a.ready = scratch.counters + g.ready;
     GemvArgs &b = m.b;
     b.x = static_cast<const float *>(down.call.a->device_ptr());
     b.w = static_cast<const uint16_t *>(down.call.b->device_ptr());
@@ -519,16 +540,16 @@ struct ExecutorImpl {
       b.d = static_cast<const float *>(dt->device_ptr());
     b.beta = down.epilogue.binary.beta;
     b.alpha = down.call.alpha;
-    b.partial = reinterpret_cast<float *>(static_cast<char *>(scratch.partial) + g.part_a_bytes);
-    b.counters = scratch.counters + g.cnt_b;
-    b.ready = scratch.counters + g.ready;
-    b.acks = scratch.counters + g.acks;
-    b.x_tile = 64;
-    b.x_readers = g.tiles_b; // the one window covering a producer tile, per down tile
-    b.spin_limit = 1u << 20; // ~0.2 s of polling (0.2 us per poll) before giving up
+    char *base = static_cast<char *>(scratch.mlp);
+    m.gen = reinterpret_cast<uint32_t *>(base + g.gen);
+    m.done = reinterpret_cast<uint32_t *>(base + g.done);
+    m.tag_a = reinterpret_cast<uint64_t *>(base + g.tag_a);
+    m.tag_h = reinterpret_cast<uint64_t *>(base + g.tag_h);
+    m.tag_b = reinterpret_cast<uint64_t *>(base + g.tag_b);
+    m.spin_limit = 1u << 20; // ~1 s of polling (a round is about a memory round trip)
     void *dev_status = nullptr;
     hip_check(hipHostGetDevicePointer(&dev_status, host_status, 0), "hipHostGetDevicePointer");
-    b.status = static_cast<uint32_t *>(dev_status);
+    m.status = static_cast<uint32_t *>(dev_status);
     m.units_a = g.tiles_a * g.kch_a;
     m.units_b = g.tiles_b * g.kch_b;
     m.tiles_a = g.tiles_a;
@@ -572,6 +593,7 @@ struct ExecutorImpl {
                            const std::vector<OpPlan> &plans) const {
     ScratchNeed need = total_need(res, plans);
     slot->scratch.ensure(need.splitk, need.partial, need.counters);
+    slot->scratch.ensure_mlp(need.mlp);
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
     record(ops, res, plans, slot->scratch, slot->host_status, slot->stream);
     hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
@@ -579,7 +601,7 @@ struct ExecutorImpl {
     float ms = 0.f;
     hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
     if (has_mlp(plans))
-      check_host_status(slot->host_status);
+      check_host_status(slot->host_status, slot->scratch.mlp, slot->scratch.mlp_bytes);
     return (uint64_t)((double)ms * 1e6);
   }
 
@@ -832,7 +854,10 @@ struct ExecutorImpl {
     Scratch scratch;
     ScratchNeed need = total_need(res, plans);
     scratch.ensure(need.splitk, need.partial, need.counters);
-    p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters};
+    scratch.ensure_mlp(need.mlp);
+    p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters, scratch.mlp};
+    p->mlp_scratch_ = scratch.mlp;
+    p->mlp_bytes_ = scratch.mlp_bytes;
     if (has_mlp(plans))
       p->status_ = alloc_host_status();
 
@@ -1080,7 +1105,7 @@ void PreparedOps::run_silent() {
   hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "hipStreamSynchronize");
   in_flight_ = false;
   if (status_)
-    check_host_status(static_cast<uint32_t *>(status_));
+    check_host_status(static_cast<uint32_t *>(status_), mlp_scratch_, mlp_bytes_);
 }
 
 // src/executor/prepared.rs:293-307.
@@ -1107,7 +1132,7 @@ RunStats PreparedOps::wait() {
                                 static_cast<hipEvent_t>(ev_end_)),
             "hipEventElapsedTime");
   if (status_)
-    check_host_status(static_cast<uint32_t *>(status_));
+    check_host_status(static_cast<uint32_t *>(status_), mlp_scratch_, mlp_bytes_);
   return RunStats{(uint64_t)((double)ms * 1e6), n_calls_, flops_};
 }
 

@@ -237,6 +237,8 @@ private:
   void *graph_exec_ = nullptr;
   void *ev_start_ = nullptr, *ev_end_ = nullptr;
   std::vector<void *> scratch_;
+  void *mlp_scratch_ = nullptr; // decode-MLP region inside scratch_
+  uint64_t mlp_bytes_ = 0;
   void *status_ = nullptr; // decode-MLP wait status word, when the graph has one
   bool in_flight_ = false;
   bool submitted_once_ = false;
