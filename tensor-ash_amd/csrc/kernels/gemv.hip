@@ -137,16 +137,16 @@ struct Gemv {
   }
 
   static TA_DEVICE void unit(const GemvArgs &p, uint32_t tile, uint32_t chunk, Smem &sm,
-                             const MlpArgs *mlp = nullptr) {
+                             const MlpArgs *mlp = nullptr, uint32_t layer = 0) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t tiles = (p.n + TW - 1) / TW;
     const uint32_t k0 = chunk * p.kchunk;
     const uint32_t kend = min(p.k, k0 + p.kchunk);
     const bool packed = p.flags & TA_GEMV_PACKED;
-    // Decode MLP: this launch's hand-off tag (read before any hand-off).
+    // Decode MLP: this layer's hand-off tag (read before any hand-off).
     uint32_t tag = 0;
     if constexpr (MODE != kStandalone)
-      tag = __hip_atomic_load(mlp->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+      tag = __hip_atomic_load(mlp->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + layer + 1u;
     TA_GEMV_TRACE(0);
 
     const uint32_t cp = lane % LPR, r0 = lane / LPR;
@@ -208,6 +208,29 @@ struct Gemv {
             return ok;
           },
           tag, xr, *mlp);
+#pragma unroll
+      for (int j = 0; j < XPT; ++j) {
+        bool ok;
+        (void)x_index(j, ok);
+        xr[j] = ok ? xr[j] : 0.0f;
+      }
+    } else if (MODE == kProducer && layer > 0) {
+      // Chained layer: weights first, then X = the previous layer's y from
+      // its tagged words ([k][MR] order, the previous layer's tag).
+      issue(0, cur);
+      poll_words<XPT>(
+          [&](int j) {
+            bool ok;
+            (void)x_index(j, ok);
+            const uint32_t i = tid + j * kThreads;
+            return mlp->tag_y + (ok ? (uint64_t)k0 * MR + i : 0);
+          },
+          [&](int j) {
+            bool ok;
+            (void)x_index(j, ok);
+            return ok;
+          },
+          tag - 1u, xr, *mlp);
 #pragma unroll
       for (int j = 0; j < XPT; ++j) {
         bool ok;
@@ -388,13 +411,15 @@ struct Gemv {
           part[i] = sum[i] + part[i];
       }
       TA_GEMV_TRACE(5);
-      epilogue(p, tile, part, sm, MODE == kProducer ? mlp->tag_h : nullptr, tag);
+      epilogue(p, tile, part, sm, MODE == kProducer ? mlp->tag_h : mlp->tag_y, tag);
       if constexpr (MODE == kConsumer) {
-        // The last down tile of the launch advances the generation: every
-        // unit has read it by then (each one's hand-off words, which carry
-        // the tag, are what this tile's inputs waited for).
-        if (tid == 0 && __hip_atomic_fetch_add(mlp->done, 1u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT) == mlp->tiles_b - 1) {
+        // The last down tile of the last layer advances the generation past
+        // every tag of the launch: every unit has read it by then (each
+        // one's hand-off words, which carry the tag, are what this tile's
+        // inputs waited for, directly or through earlier layers).
+        if (tid == 0 && layer + 1 == mlp->layers &&
+            __hip_atomic_fetch_add(mlp->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                mlp->tiles_b - 1) {
           __hip_atomic_store(mlp->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store(mlp->gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -473,8 +498,11 @@ struct Gemv {
 
   // Epilogue (shaders/matmul_epilogue_common.glsl:14-21 order) on the
   // tile's K-summed outputs.  Dual mode writes U and Y; with `h_tag` it
-  // also publishes Y as tagged words [col][MR] for the decode MLP's down
-  // units.
+  // also publishes Y as tagged words [col][MR] (for the decode MLP's down
+  // units, or, from a down unit, for the next chained layer).  A decode-MLP
+  // down unit reads Y_old and D, which earlier chained layers may have
+  // written in this launch, and writes Y, which later ones may read, with
+  // agent-scope accesses.
   static TA_DEVICE void epilogue(const GemvArgs &p, uint32_t tile, const float (&part)[OPT],
                                  Smem &sm, uint64_t *h_tag, uint32_t tag) {
     const uint32_t tid = threadIdx.x;
@@ -497,8 +525,15 @@ struct Gemv {
         if (p.flags & TA_FLAG_BIAS)
           g += p.bias[c];
         const float h = ta_activate(g, p.act) * u;
-        p.y2[yi] = u;
-        p.y[yi] = h;
+        if constexpr (MODE == kStandalone) {
+          p.y2[yi] = u;
+          p.y[yi] = h;
+        } else {
+          // Agent-scope stores: a later chained layer may rewrite or read
+          // these buffers.
+          coherent_store(p.y2 + yi, u);
+          coherent_store(p.y + yi, h);
+        }
         if (h_tag)
           store_word(h_tag + (uint64_t)c * MR + m, tag_word(h, tag));
       }
@@ -510,17 +545,25 @@ struct Gemv {
         if (o >= OUTS || m >= p.rows || c >= p.n)
           continue;
         const uint64_t yi = (uint64_t)m * p.n + c;
+        constexpr bool kCoherent = MODE == kConsumer;
+        auto rd = [&](const float *q) { return kCoherent ? coherent_load(q) : *q; };
         float v = p.alpha * part[i];
         if (p.flags & TA_FLAG_ACCUMULATE)
-          v += p.y[yi];
+          v += rd(p.y + yi);
         if (p.flags & TA_FLAG_BIAS)
           v += p.bias[c];
         v = ta_activate(v, p.act);
         if (p.binary == TA_BIN_ADD_SCALED)
-          v = fmaf(p.beta, p.d[yi], v);
+          v = fmaf(p.beta, rd(p.d + yi), v);
         else if (p.binary == TA_BIN_MUL)
-          v *= p.d[yi];
-        p.y[yi] = v;
+          v *= rd(p.d + yi);
+        if constexpr (kCoherent) {
+          coherent_store(p.y + yi, v);
+          if (h_tag)
+            store_word(h_tag + (uint64_t)c * MR + m, tag_word(v, tag));
+        } else {
+          p.y[yi] = v;
+        }
       }
     }
   }
@@ -535,13 +578,18 @@ struct Gemv {
 // Rows of X staged per standalone unit: 16 KiB of LDS.
 template <int MR> constexpr int standalone_rows() { return 4096 / MR; }
 
-// Persistent decode MLP.  Workgroup ids below units_a run gate/up
-// (producer) units, the rest run down-proj (consumer) units.  Every wait
-// is on units with lower workgroup ids (down units on gate/up units; the
-// last K window of a tile, which has the tile's highest id, on the tile's
-// other windows), and workgroups are dispatched in id order, so a waited-on
-// unit has always been dispatched and never waits on its waiter; the
-// bounded wait is a safety net only.  No launch-wide counter is touched at
+// Persistent decode MLP chain.  Per layer, the first units_a workgroups run
+// gate/up (producer) units, the rest down-proj (consumer) units; layers
+// follow each other in workgroup id.  Every wait is on units with lower
+// workgroup ids (down units on gate/up units of their layer; gate/up units
+// on the previous layer's down units; the last K window of a tile, which has
+// the tile's highest id, on the tile's other windows), and workgroups are
+// dispatched in id order, so a waited-on unit has always been dispatched and
+// never waits on its waiter; the bounded wait is a safety net only.  A
+// layer's gate/up units are dispatched as the previous layer's gate/up units
+// exit and issue their weight reads before waiting for their x, so HBM
+// streams the next layer's weights through the previous layer's hand-off
+// tail.  No launch-wide counter is touched at
 // unit start (one hot atomic would serialise the starts).
 // K windows: gate/up units take 256 rows (one group of 16 loads per
 // matrix); down units take 512 rows (one group of 32 loads) so they are
@@ -560,12 +608,14 @@ template <int MR> struct DecodeMlp {
 
   static TA_DEVICE void run(const MlpArgs &p) {
     __shared__ __attribute__((aligned(16))) Smem sm;
-    const uint32_t r = blockIdx.x;
-    TA_GEMV_TRACE_ROLE(r);
+    const uint32_t per_layer = p.units_a + p.units_b;
+    const uint32_t layer = blockIdx.x / per_layer, r = blockIdx.x % per_layer;
+    TA_GEMV_TRACE_ROLE(blockIdx.x);
     if (r < p.units_a)
-      A::unit(p.a, r % p.tiles_a, r / p.tiles_a, sm.a, &p);
+      A::unit(p.layer[layer].a, r % p.tiles_a, r / p.tiles_a, sm.a, &p, layer);
     else
-      B::unit(p.b, (r - p.units_a) % p.tiles_b, (r - p.units_a) / p.tiles_b, sm.b, &p);
+      B::unit(p.layer[layer].b, (r - p.units_a) % p.tiles_b, (r - p.units_a) / p.tiles_b, sm.b, &p,
+              layer);
   }
 };
 

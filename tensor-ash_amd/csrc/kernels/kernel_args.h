@@ -98,28 +98,38 @@ typedef struct GemvArgs {
   float beta;
 } GemvArgs;
 
-// Persistent decode SwiGLU MLP in one launch: `a` is the dual gate/up GEMV
-// (producer of h = act(x Wg) * (x Wu)), `b` the down-proj GEMV reading h.
-// Workgroups 0..units_a-1 run `a` units (tile-major: unit u is tile
-// u % tiles_a, K window u / tiles_a), the rest run `b` units likewise.
-// Units hand data over as 64-bit words {f32 value, launch tag} that the
-// reader polls until the tag matches; the tag is *gen + 1, and the last
-// `b` tile to finish (counted in *done) advances *gen, so no hand-off word
-// ever needs clearing.  a.partial/a.counters and b.partial/b.counters are
-// unused: the tagged buffers below replace them.
-typedef struct MlpArgs {
+// Persistent decode SwiGLU MLP chain in one launch: `layers` MLPs, layer
+// l+1 reading layer l's output y as its x.  In a layer, `a` is the dual
+// gate/up GEMV (producer of h = act(x Wg) * (x Wu)) and `b` the down-proj
+// GEMV reading h.  Workgroup r serves layer r / (units_a + units_b); within
+// a layer the first units_a run `a` units (tile-major: unit u is tile
+// u % tiles_a, K window u / tiles_a), the rest `b` units likewise.  Every
+// layer has the same shape.
+// Units hand data over as 64-bit words {f32 value, tag} that the reader
+// polls until the tag matches; layer l's tag is *gen + l + 1, and the last
+// tile of the last layer (counted in *done) advances *gen by `layers`, so
+// no hand-off word ever needs clearing.  The a/b partial and counters
+// fields are unused: the tagged buffers replace them.
+#define TA_MLP_MAX_LAYERS 16
+
+typedef struct MlpLayer {
   GemvArgs a;
   GemvArgs b;
+} MlpLayer;
+
+typedef struct MlpArgs {
   uint64_t *tag_a;  // [kch_a][tiles_a][2][MR][64] gate/up window partials
-  uint64_t *tag_h;  // [K_b][MR] h = act(gate) * up, as the down units read it
+  uint64_t *tag_h;  // [K_b][MR] h, as the down units read it
   uint64_t *tag_b;  // [kch_b][tiles_b][MR][64] down window partials
+  uint64_t *tag_y;  // [N_b][MR] y, as the next layer's gate/up units read it
   uint32_t *gen;    // launch generation (zero-initialised)
-  uint32_t *done;   // `b` tiles finished in this launch (zero between launches)
+  uint32_t *done;   // last-layer `b` tiles finished (zero between launches)
   uint32_t *status; // host-mapped; set to 1 if a wait gave up
   uint32_t units_a, units_b;
   uint32_t tiles_a, tiles_b;
   uint32_t spin_limit; // polls before a wait gives up
-  uint32_t pad;
+  uint32_t layers;
+  MlpLayer layer[TA_MLP_MAX_LAYERS];
 } MlpArgs;
 
 #ifdef __cplusplus

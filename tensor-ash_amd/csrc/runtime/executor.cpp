@@ -130,8 +130,10 @@ struct OpPlan {
   std::optional<uint32_t> splitk2;
   // Launch role: 0 = normal, 1 = fused into the next op's dual GEMV,
   // 2 = dual GEMV that also produces the previous op's output,
-  // 3 = decode-MLP launch covering this op and the next two, 4 = covered.
+  // 3 = decode-MLP launch covering this op and the next 3 * mlp_layers - 1,
+  // 4 = covered.
   int role = 0;
+  uint32_t mlp_layers = 0;
 };
 
 uint32_t gemm_threads(const KernelSpec &s) { return s.tile_m == 256 && s.tile_n == 256 ? 512 : 256; }
@@ -397,7 +399,8 @@ struct ExecutorImpl {
     return gate.call.c->buffer_id() != up.call.c->buffer_id();
   }
 
-  void mark_fusions(const std::vector<MatmulOp> &ops, std::vector<OpPlan> &plans) const {
+  void mark_fusions(const std::vector<MatmulOp> &ops, const std::vector<ResolvedMatmul> &res,
+                    std::vector<OpPlan> &plans) const {
     if (std::getenv("TA_NO_FUSE"))
       return;
     for (size_t i = 0; i + 1 < ops.size(); ++i) {
@@ -407,6 +410,7 @@ struct ExecutorImpl {
           fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1]) &&
           mlp_tail_ok(ops[i], ops[i + 1], plans[i + 1], ops[i + 2], plans[i + 2])) {
         plans[i].role = 3;
+        plans[i].mlp_layers = 1;
         plans[i + 1].role = 4;
         plans[i + 2].role = 4;
         i += 2;
@@ -418,6 +422,49 @@ struct ExecutorImpl {
         ++i;
       }
     }
+    if (std::getenv("TA_NO_MLP_CHAIN"))
+      return;
+    // Decode-MLP chains: consecutive MLP launches where each reads the
+    // previous one's output as x become one launch.
+    for (size_t i = 0; i < ops.size(); ++i) {
+      if (plans[i].role != 3)
+        continue;
+      size_t j = i + 3;
+      while (plans[i].mlp_layers < TA_MLP_MAX_LAYERS && j < ops.size() && plans[j].role == 3 &&
+             mlp_chain_ok(ops, res, i, j)) {
+        plans[j].role = 4;
+        plans[j].mlp_layers = 0;
+        ++plans[i].mlp_layers;
+        j += 3;
+      }
+      i = j - 1;
+    }
+  }
+
+  // May the MLP at ops[j..j+2] join the chain that starts at ops[i] and
+  // ends just before j?  Same shapes; its x is the previous layer's y (read
+  // through the tagged hand-off); its biases, read with plain loads, are
+  // not written by the chain.  Every other buffer is safe: chained layers
+  // write their outputs with agent-scope stores, read the residual with
+  // agent-scope loads, and run after every earlier layer has finished.
+  static bool mlp_chain_ok(const std::vector<MatmulOp> &ops,
+                           const std::vector<ResolvedMatmul> &res, size_t i, size_t j) {
+    for (size_t k = 0; k < 3; ++k)
+      if (res[j + k].m != res[i + k].m || res[j + k].n != res[i + k].n ||
+          res[j + k].k != res[i + k].k)
+        return false;
+    const Tensor *prev_y = ops[j - 1].call.c, *x = ops[j].call.a;
+    if (x->buffer_id() != prev_y->buffer_id() || x->shape() != prev_y->shape() ||
+        ops[j + 1].call.a->buffer_id() != x->buffer_id())
+      return false;
+    for (const Tensor *bias : {ops[j + 1].epilogue.bias, ops[j + 2].epilogue.bias}) {
+      if (!bias)
+        continue;
+      for (size_t k = i; k < j; ++k)
+        if (bias->buffer_id() == ops[k].call.c->buffer_id())
+          return false;
+    }
+    return true;
   }
 
   void check_supported(const KernelSpec &s, const ResolvedMatmul &d) const {
@@ -451,7 +498,7 @@ struct ExecutorImpl {
   // and of the down partials.
   struct MlpGeom {
     uint32_t mr, tiles_a, kch_a, tiles_b, kch_b;
-    uint64_t gen, done, tag_a, tag_h, tag_b, bytes;
+    uint64_t gen, done, tag_a, tag_h, tag_b, tag_y, bytes;
   };
   // K windows of the two phases (kernel constants kMlpRowsA / kMlpRowsB).
   static constexpr uint32_t kMlpRowsA = 256, kMlpRowsB = 512;
@@ -469,13 +516,17 @@ struct ExecutorImpl {
     g.tag_a = 256;
     g.tag_h = al(g.tag_a + (uint64_t)g.kch_a * g.tiles_a * 2 * g.mr * 64 * 8);
     g.tag_b = al(g.tag_h + (uint64_t)down.k * g.mr * 8);
-    g.bytes = al(g.tag_b + (uint64_t)g.kch_b * g.tiles_b * g.mr * 64 * 8);
+    g.tag_y = al(g.tag_b + (uint64_t)g.kch_b * g.tiles_b * g.mr * 64 * 8);
+    g.bytes = al(g.tag_y + (uint64_t)down.n * g.mr * 8);
     return g;
   }
 
   // ops[i] = x@Wu, ops[i+1] = act(x@Wg) * up (a fusable pair), ops[i+2] =
   // h@Wd reading the pair's output h, all on the packed 64-column decode
-  // GEMV.  The down op keeps its full epilogue.
+  // GEMV.  The down op keeps its full epilogue.  Its output may not be a
+  // buffer the pair writes (plain and agent-scope stores would race) or
+  // reads as x; its bias (plain loads) and residual may not be a pair
+  // output.
   static bool mlp_tail_ok(const MatmulOp &up, const MatmulOp &gate, const OpPlan &pg,
                           const MatmulOp &down, const OpPlan &pd) {
     const KernelSpec &sg = KERNEL_SPECS[pg.kernel], &sd = KERNEL_SPECS[pd.kernel];
@@ -484,68 +535,76 @@ struct ExecutorImpl {
     if (!down.packed_b || down.call.a->buffer_id() != gate.call.c->buffer_id() ||
         down.call.a->shape() != gate.call.c->shape())
       return false;
-    auto aliases = [&](const Tensor *t) {
+    auto pair_out = [&](const Tensor *t) {
       return t && (t->buffer_id() == up.call.c->buffer_id() ||
-                   t->buffer_id() == gate.call.c->buffer_id() ||
-                   t->buffer_id() == up.call.a->buffer_id());
+                   t->buffer_id() == gate.call.c->buffer_id());
     };
-    return !aliases(down.call.c) && !aliases(down.epilogue.bias) &&
-           !aliases(down.epilogue.d_tensor());
+    return !pair_out(down.call.c) && down.call.c->buffer_id() != up.call.a->buffer_id() &&
+           !pair_out(down.epilogue.bias) && !pair_out(down.epilogue.d_tensor());
   }
 
+  // Decode-MLP chain of `layers` layers starting at ops[i] (each layer is
+  // the op triple [up, gate, down]).
   void launch_mlp(const std::vector<MatmulOp> &ops, const std::vector<ResolvedMatmul> &res,
-                  size_t i, Scratch &scratch, uint32_t *host_status, hipStream_t stream) const {
-    const MatmulOp &up = ops[i], &gate = ops[i + 1], &down = ops[i + 2];
+                  size_t i, uint32_t layers, Scratch &scratch, uint32_t *host_status,
+                  hipStream_t stream) const {
     MlpGeom g = mlp_geom(res[i], res[i + 2]);
     if (scratch.mlp_bytes < g.bytes)
       fail("internal: decode-MLP scratch not reserved");
     if (!host_status)
       fail("internal: decode-MLP status word missing");
+    if (layers < 1 || layers > TA_MLP_MAX_LAYERS || i + 3 * layers > ops.size())
+      fail("internal: bad decode-MLP chain length");
     MlpArgs m{};
-    GemvArgs &a = m.a;
-    a.x = static_cast<const float *>(gate.call.a->device_ptr());
-    a.w = static_cast<const uint16_t *>(gate.call.b->device_ptr());
-    a.w2 = static_cast<const uint16_t *>(up.call.b->device_ptr());
-    a.y = static_cast<float *>(gate.call.c->device_ptr());
-    a.y2 = static_cast<float *>(up.call.c->device_ptr());
-    a.rows = res[i].m;
-    a.n = res[i].n;
-    a.k = res[i].k;
-    a.kchunk = kMlpRowsA;
-    a.kchunks = g.kch_a;
-    a.flags = TA_GEMV_PACKED;
-    if (gate.epilogue.bias) {
-      a.flags |= TA_FLAG_BIAS;
-      a.bias = static_cast<const float *>(gate.epilogue.bias->device_ptr());
+    for (uint32_t l = 0; l < layers; ++l) {
+      const size_t o = i + 3 * (size_t)l;
+      const MatmulOp &up = ops[o], &gate = ops[o + 1], &down = ops[o + 2];
+      GemvArgs &a = m.layer[l].a;
+      a.x = static_cast<const float *>(gate.call.a->device_ptr());
+      a.w = static_cast<const uint16_t *>(gate.call.b->device_ptr());
+      a.w2 = static_cast<const uint16_t *>(up.call.b->device_ptr());
+      a.y = static_cast<float *>(gate.call.c->device_ptr());
+      a.y2 = static_cast<float *>(up.call.c->device_ptr());
+      a.rows = res[o].m;
+      a.n = res[o].n;
+      a.k = res[o].k;
+      a.kchunk = kMlpRowsA;
+      a.kchunks = g.kch_a;
+      a.flags = TA_GEMV_PACKED;
+      if (gate.epilogue.bias) {
+        a.flags |= TA_FLAG_BIAS;
+        a.bias = static_cast<const float *>(gate.epilogue.bias->device_ptr());
+      }
+      a.act = (uint32_t)gate.epilogue.activation;
+      a.alpha = gate.call.alpha;
+      GemvArgs &b = m.layer[l].b;
+      b.x = static_cast<const float *>(down.call.a->device_ptr());
+      b.w = static_cast<const uint16_t *>(down.call.b->device_ptr());
+      b.y = static_cast<float *>(down.call.c->device_ptr());
+      b.rows = res[o + 2].m;
+      b.n = res[o + 2].n;
+      b.k = res[o + 2].k;
+      b.kchunk = kMlpRowsB;
+      b.kchunks = g.kch_b;
+      b.flags = TA_GEMV_PACKED | (down.call.accumulate ? TA_FLAG_ACCUMULATE : 0u);
+      if (down.epilogue.bias) {
+        b.flags |= TA_FLAG_BIAS;
+        b.bias = static_cast<const float *>(down.epilogue.bias->device_ptr());
+      }
+      b.act = (uint32_t)down.epilogue.activation;
+      b.binary = (uint32_t)down.epilogue.binary.kind;
+      if (const Tensor *dt = down.epilogue.d_tensor())
+        b.d = static_cast<const float *>(dt->device_ptr());
+      b.beta = down.epilogue.binary.beta;
+      b.alpha = down.call.alpha;
     }
-    a.act = (uint32_t)gate.epilogue.activation;
-    a.alpha = gate.call.alpha;
-    GemvArgs &b = m.b;
-    b.x = static_cast<const float *>(down.call.a->device_ptr());
-    b.w = static_cast<const uint16_t *>(down.call.b->device_ptr());
-    b.y = static_cast<float *>(down.call.c->device_ptr());
-    b.rows = res[i + 2].m;
-    b.n = res[i + 2].n;
-    b.k = res[i + 2].k;
-    b.kchunk = kMlpRowsB;
-    b.kchunks = g.kch_b;
-    b.flags = TA_GEMV_PACKED | (down.call.accumulate ? TA_FLAG_ACCUMULATE : 0u);
-    if (down.epilogue.bias) {
-      b.flags |= TA_FLAG_BIAS;
-      b.bias = static_cast<const float *>(down.epilogue.bias->device_ptr());
-    }
-    b.act = (uint32_t)down.epilogue.activation;
-    b.binary = (uint32_t)down.epilogue.binary.kind;
-    if (const Tensor *dt = down.epilogue.d_tensor())
-      b.d = static_cast<const float *>(dt->device_ptr());
-    b.beta = down.epilogue.binary.beta;
-    b.alpha = down.call.alpha;
     char *base = static_cast<char *>(scratch.mlp);
     m.gen = reinterpret_cast<uint32_t *>(base + g.gen);
     m.done = reinterpret_cast<uint32_t *>(base + g.done);
     m.tag_a = reinterpret_cast<uint64_t *>(base + g.tag_a);
     m.tag_h = reinterpret_cast<uint64_t *>(base + g.tag_h);
     m.tag_b = reinterpret_cast<uint64_t *>(base + g.tag_b);
+    m.tag_y = reinterpret_cast<uint64_t *>(base + g.tag_y);
     m.spin_limit = 1u << 20; // ~1 s of polling (a round is about a memory round trip)
     void *dev_status = nullptr;
     hip_check(hipHostGetDevicePointer(&dev_status, host_status, 0), "hipHostGetDevicePointer");
@@ -554,8 +613,9 @@ struct ExecutorImpl {
     m.units_b = g.tiles_b * g.kch_b;
     m.tiles_a = g.tiles_a;
     m.tiles_b = g.tiles_b;
-    launch("ta_decode_mlp_f16_t64_m" + std::to_string(g.mr), m.units_a + m.units_b, 1, 1, 256, &m,
-           stream);
+    m.layers = layers;
+    launch("ta_decode_mlp_f16_t64_m" + std::to_string(g.mr), layers * (m.units_a + m.units_b), 1,
+           1, 256, &m, stream);
   }
 
   static bool has_mlp(const std::vector<OpPlan> &plans) {
@@ -573,9 +633,9 @@ struct ExecutorImpl {
       if (p.role == 1 || p.role == 4)
         continue; // produced by the dual launch of op i+1 / the MLP launch
       if (p.role == 3) {
-        for (size_t j = i; j < i + 3; ++j)
+        for (size_t j = i; j < i + 3 * (size_t)p.mlp_layers; ++j)
           check_supported(KERNEL_SPECS[plans[j].kernel], res[j]);
-        launch_mlp(ops, res, i, scratch, host_status, stream);
+        launch_mlp(ops, res, i, p.mlp_layers, scratch, host_status, stream);
         continue;
       }
       const KernelSpec &s = KERNEL_SPECS[p.kernel];
@@ -772,7 +832,7 @@ struct ExecutorImpl {
       plans.push_back(plan_matmul(res[i], eligible));
     }
     if (graph)
-      mark_fusions(ops, plans);
+      mark_fusions(ops, res, plans);
     if (!graph && plans.size() == 1 && plans[0].splitk2)
       return run_split_k2(ops[0].call, *plans[0].splitk2);
 
@@ -834,7 +894,7 @@ struct ExecutorImpl {
     for (const auto &d : res)
       plans.push_back(plan_matmul(d, false));
     if (graph)
-      mark_fusions(ops, plans);
+      mark_fusions(ops, res, plans);
     for (size_t i = 0; i < ops.size(); ++i)
       check_supported(KERNEL_SPECS[plans[i].kernel], res[i]);
 

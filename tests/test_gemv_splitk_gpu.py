@@ -128,6 +128,100 @@ def test_swiglu_mlp_graph(ta, ex, oracle, m, monkeypatch):
         np.testing.assert_array_equal(ex.download(y), y_mlp)
 
 
+def _mlp_layer_ops(ta, x, wts, up, h, y, res):
+    wg, wu, wd = wts
+    return [
+        ta.MatmulOp(x, wu, up, packed_b=True),
+        ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up),
+                    packed_b=True),
+        ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=res, beta=1.0), packed_b=True),
+    ]
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_decode_mlp_chain(ta, ex, oracle, m, monkeypatch):
+    """Three config-3 decode layers in one op graph (layer l+1 reads layer
+    l's y as x and as residual) run as one persistent MLP-chain launch.
+    Every layer is checked against the oracle on the GPU's own layer input,
+    and the chain must give the bits of separate per-layer MLP launches,
+    eagerly and through a prepared graph, over repeated runs."""
+    hdim, ffn, layers = 2048, 5632, 3
+    pk = lambda w, k, n: ex.tensor_from(ta.pack_f16w_row_tiles(w, k, n, ta.f16w_row_tile_n(k, n)),
+                                        shape=[k, n], f16=True)
+    wts, refs = [], []
+    for l in range(layers):
+        wg, wgr = f16_weights(oracle, hdim, ffn, 301 + 3 * l)
+        wu, wur = f16_weights(oracle, hdim, ffn, 302 + 3 * l)
+        wd, wdr = f16_weights(oracle, ffn, hdim, 303 + 3 * l)
+        wts.append((pk(wg, hdim, ffn), pk(wu, hdim, ffn), pk(wd, ffn, hdim)))
+        refs.append((wgr, wur, wdr))
+    x0 = oracle.fill_det(m * hdim, 51)
+    xs = [ex.tensor_from(x0, shape=[m, hdim])] + [ex.tensor([m, hdim]) for _ in range(layers)]
+    ups = [ex.tensor([m, ffn]) for _ in range(layers)]
+    hs = [ex.tensor([m, ffn]) for _ in range(layers)]
+    ops = []
+    for l in range(layers):
+        ops += _mlp_layer_ops(ta, xs[l], wts[l], ups[l], hs[l], xs[l + 1], xs[l])
+    ex.run_op_graph(ops)
+    got = [ex.download(t).copy() for t in xs + ups + hs]
+    for l in range(layers):
+        wgr, wur, wdr = refs[l]
+        xin = got[l]
+        ref_up = oracle.cpu_bmm(xin, wur, None, 1, m, ffn, hdim)
+        ref_h = oracle.reference_gemm(xin, wgr, 1, m, ffn, hdim, act=2, binary=2, d=ref_up)
+        check_f16(got[layers + 1 + l], ref_up, hdim, oracle)
+        check_f16(got[2 * layers + 1 + l], ref_h, hdim, oracle)
+        ref_y = oracle.reference_gemm(got[2 * layers + 1 + l], wdr, 1, m, hdim, ffn, binary=1, d=xin,
+                                      beta=1.0)
+        check_f16(got[l + 1], ref_y, ffn, oracle)
+    for t in xs[1:] + ups + hs:
+        ex.upload(t, np.zeros(int(np.prod(t.shape)), np.float32))
+    monkeypatch.setenv("TA_NO_MLP_CHAIN", "1")
+    ex.run_op_graph(ops)
+    monkeypatch.delenv("TA_NO_MLP_CHAIN")
+    for a, b in zip([ex.download(t) for t in xs + ups + hs], got):
+        np.testing.assert_array_equal(a, b)
+    for _ in range(3):
+        ex.run_op_graph(ops)
+        np.testing.assert_array_equal(ex.download(xs[-1]), got[layers])
+    prep = ex.prepare_op_graph(ops)
+    for _ in range(3):
+        ex.upload(xs[-1], np.zeros(m * hdim, np.float32))
+        prep.run()
+        np.testing.assert_array_equal(ex.download(xs[-1]), got[layers])
+    prep.close()
+
+
+def test_decode_mlp_chain_long(ta, ex, oracle, monkeypatch):
+    """18 layers over two ping-pong activation buffers and shared up/h
+    buffers (the decode-forward form): the executor splits the chain into
+    launches of at most 16 layers; bits equal separate per-layer launches."""
+    m, hdim, ffn, layers = 2, 512, 1024, 18
+    pk = lambda w, k, n: ex.tensor_from(ta.pack_f16w_row_tiles(w, k, n, ta.f16w_row_tile_n(k, n)),
+                                        shape=[k, n], f16=True)
+    wts = [(pk(f16_weights(oracle, hdim, ffn, 400 + 3 * l)[0], hdim, ffn),
+            pk(f16_weights(oracle, hdim, ffn, 401 + 3 * l)[0], hdim, ffn),
+            pk(f16_weights(oracle, ffn, hdim, 402 + 3 * l)[0], ffn, hdim)) for l in range(3)]
+    x0 = oracle.fill_det(m * hdim, 52)
+    bufs = [ex.tensor([m, hdim]), ex.tensor([m, hdim])]
+    up, h = ex.tensor([m, ffn]), ex.tensor([m, ffn])
+    ops = []
+    for l in range(layers):
+        ops += _mlp_layer_ops(ta, bufs[l % 2], wts[l % 3], up, h, bufs[(l + 1) % 2], bufs[l % 2])
+    outs = []
+    for env in (None, "TA_NO_MLP_CHAIN"):
+        if env:
+            monkeypatch.setenv(env, "1")
+        ex.upload(bufs[0], x0)
+        ex.run_op_graph(ops)
+        outs.append([ex.download(t).copy() for t in bufs + [up, h]])
+        if env:
+            monkeypatch.delenv(env)
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    assert np.all(np.isfinite(outs[0][0]))
+
+
 @pytest.mark.parametrize("m", [1, 8])
 def test_decode_mlp_down_epilogue(ta, ex, oracle, m):
     """Persistent MLP with a general down-proj epilogue (bias + GELU) and a
