@@ -61,6 +61,16 @@ TA_DEVICE void coherent_store(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A workgroup-uniform pointer, moved to scalar registers so a load can use
+// it as its scalar base with a 32-bit per-lane offset.
+typedef __attribute__((address_space(1))) const char global_char;
+TA_DEVICE global_char *uniform_ptr(const char *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<global_char *>(((uint64_t)hi << 32) | lo);
+}
+
 // Decode-MLP hand-off word: f32 value bits low, launch tag high; one
 // naturally aligned 64-bit access, so a reader sees value and tag together.
 TA_DEVICE uint64_t tag_word(float v, uint32_t tag) {
@@ -165,9 +175,30 @@ struct Gemv {
     const uint32_t my_first = wave * RPI + r0;
     constexpr uint32_t G = RPW * kUnroll; // rows per unrolled group
 
+    // Decode-MLP units cover whole packed tiles and whole K windows (host
+    // contract), so no row or column is ragged: the loads address a
+    // uniform row base plus one per-lane 32-bit offset (scalar-base loads,
+    // one address register), and no value needs masking.
+    constexpr bool EXACT = MODE != kStandalone;
+    const char *wbase[WAYS];
+    wbase[0] = reinterpret_cast<const char *>(p.w) + tile_base * EB;
+    if constexpr (DUAL)
+      wbase[1] = reinterpret_cast<const char *>(p.w2) + tile_base * EB;
+    const uint32_t lane_b = my_first * (uint32_t)row_stride + CPL * cp * EB;
+
     // One group of loads; rows at or past kend re-read row k0 (valid, and
     // zeroed before use), so the loads carry no branches.
     auto issue = [&](uint32_t kb, uint64_t (&raw)[WAYS][kUnroll]) {
+      if constexpr (EXACT) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+          for (int w = 0; w < WAYS; ++w)
+            raw[w][u] = __builtin_nontemporal_load(
+                reinterpret_cast<__attribute__((address_space(1))) const uint64_t *>(
+                    uniform_ptr(wbase[w] + (uint64_t)(k0 + kb + u * RPW) * row_stride) + lane_b));
+        return;
+      }
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const uint32_t k = k0 + kb + u * RPW + my_first;
@@ -294,7 +325,7 @@ struct Gemv {
         for (int b = 0; b < XB; ++b) {
           const int u = u0 + b;
           const uint32_t kk = kb + u * RPW + my_first;
-          const bool ok = k0 + kk < kend && col_ok;
+          const bool ok = EXACT || (k0 + kk < kend && col_ok);
 #pragma unroll
           for (int w = 0; w < WAYS; ++w) {
             float wv[CPL];

@@ -532,6 +532,9 @@ struct ExecutorImpl {
     const KernelSpec &sg = KERNEL_SPECS[pg.kernel], &sd = KERNEL_SPECS[pd.kernel];
     if (!sg.packed() || !sd.packed() || sg.tile_n != 64 || sd.tile_n != 64 || pd.splitk2)
       return false;
+    // Whole K windows in both phases (the kernel does not mask rows).
+    if (gate.call.a->shape().back() % kMlpRowsA != 0 || down.call.a->shape().back() % kMlpRowsB != 0)
+      return false;
     if (!down.packed_b || down.call.a->buffer_id() != gate.call.c->buffer_id() ||
         down.call.a->shape() != gate.call.c->shape())
       return false;
