@@ -128,6 +128,9 @@ struct Gemv {
   // for the last unit of a tile: PSTAGE floats, 16 loads per thread.
   static constexpr int PSTAGE = 16 * kThreads;
   static constexpr int XS = XROWS * MR > PSTAGE ? XROWS * MR : PSTAGE;
+  // Decode-MLP tile reducers poll the other windows' words in rounds of
+  // MPOLL loads per thread (one round covers them all for M <= 2).
+  static constexpr int MPOLL = 8;
 
   struct Smem {
     float xs[XS]; // X window, later the partials of the last unit
@@ -409,14 +412,15 @@ struct Gemv {
       }
       if (p.kchunks > 1) {
         // Poll the other windows' words with all threads (NB windows per
-        // round of 16 loads per thread), stage them in the X window's LDS,
+        // round of MPOLL loads per thread), stage them in the X window's LDS,
         // then each output adds its windows in order.
-        constexpr uint32_t NB = PSTAGE / OUTS;
+        constexpr uint32_t NB = MPOLL * kThreads / OUTS;
+        static_assert(NB >= 1, "a poll round holds at least one window");
         float sum[OPT];
         for (uint32_t c0 = 0; c0 + 1 < p.kchunks; c0 += NB) {
           const uint32_t nb = min(NB, p.kchunks - 1 - c0);
-          float v[PSTAGE / kThreads];
-          poll_words<PSTAGE / kThreads>(
+          float v[MPOLL];
+          poll_words<MPOLL>(
               [&](int j) {
                 const uint32_t e = tid + j * kThreads;
                 const bool ok = e < nb * OUTS;
@@ -426,7 +430,7 @@ struct Gemv {
               [&](int j) { return tid + j * kThreads < nb * OUTS; }, tag, v, *mlp);
           __syncthreads(); // previous round's values consumed
 #pragma unroll
-          for (int j = 0; j < PSTAGE / kThreads; ++j)
+          for (int j = 0; j < MPOLL; ++j)
             sm.xs[tid + j * kThreads] = v[j];
           __syncthreads();
 #pragma unroll

@@ -407,6 +407,7 @@ struct ExecutorImpl {
       if (plans[i].role != 0 || plans[i + 1].role != 0)
         continue;
       if (!std::getenv("TA_NO_MLP") && i + 2 < ops.size() && plans[i + 2].role == 0 &&
+          res[i].batch == 1 && res[i].m <= mlp_max_rows() &&
           fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1]) &&
           mlp_tail_ok(ops[i], ops[i + 1], plans[i + 1], ops[i + 2], plans[i + 2])) {
         plans[i].role = 3;
@@ -439,6 +440,17 @@ struct ExecutorImpl {
       }
       i = j - 1;
     }
+  }
+
+  // Rows up to which op triples become decode-MLP launches.  Above 2 the
+  // per-layer FMA work on the vector ALUs outweighs the saved launch and
+  // hand-off (measured: the separate dual gate/up and down launches are
+  // faster at M = 4 and 8).  TA_MLP_MAX_ROWS overrides (at most 8).
+  static uint32_t mlp_max_rows() {
+    uint32_t rows = 2;
+    if (const char *env = std::getenv("TA_MLP_MAX_ROWS"))
+      rows = (uint32_t)std::strtoul(env, nullptr, 10);
+    return std::min<uint32_t>(rows, 8);
   }
 
   // May the MLP at ops[j..j+2] join the chain that starts at ops[i] and

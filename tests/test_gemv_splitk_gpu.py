@@ -84,6 +84,7 @@ def test_swiglu_mlp_graph(ta, ex, oracle, m, monkeypatch):
     down-proj sums K in 512-row windows inside the MLP launch and in the
     planner's windows standalone, so both are checked against the oracle,
     and repeated MLP launches must repeat their bits."""
+    monkeypatch.setenv("TA_MLP_MAX_ROWS", "8")  # the MLP launch at every M (default: M <= 2)
     hdim, ffn = 2048, 5632
     wg, wgr = f16_weights(oracle, hdim, ffn, 101)
     wu, wur = f16_weights(oracle, hdim, ffn, 102)
@@ -145,6 +146,7 @@ def test_decode_mlp_chain(ta, ex, oracle, m, monkeypatch):
     Every layer is checked against the oracle on the GPU's own layer input,
     and the chain must give the bits of separate per-layer MLP launches,
     eagerly and through a prepared graph, over repeated runs."""
+    monkeypatch.setenv("TA_MLP_MAX_ROWS", "8")
     hdim, ffn, layers = 2048, 5632, 3
     pk = lambda w, k, n: ex.tensor_from(ta.pack_f16w_row_tiles(w, k, n, ta.f16w_row_tile_n(k, n)),
                                         shape=[k, n], f16=True)
@@ -223,9 +225,10 @@ def test_decode_mlp_chain_long(ta, ex, oracle, monkeypatch):
 
 
 @pytest.mark.parametrize("m", [1, 8])
-def test_decode_mlp_down_epilogue(ta, ex, oracle, m):
+def test_decode_mlp_down_epilogue(ta, ex, oracle, m, monkeypatch):
     """Persistent MLP with a general down-proj epilogue (bias + GELU) and a
     gate bias, on non-square dims (H=768, F=1536)."""
+    monkeypatch.setenv("TA_MLP_MAX_ROWS", "8")
     hdim, ffn = 768, 1536
     wg, wgr = f16_weights(oracle, hdim, ffn, 201)
     wu, wur = f16_weights(oracle, hdim, ffn, 202)
