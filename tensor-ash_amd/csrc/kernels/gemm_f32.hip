@@ -169,14 +169,21 @@ struct GemmF32 {
     ta_tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
 
-    const uint32_t S = p.num_splits;
-    const uint32_t batch = blockIdx.z / S;
-    const uint32_t split = blockIdx.z % S;
+    const uint32_t P = p.num_splits;
+    const uint32_t batch = blockIdx.z / P;
+    const uint32_t split = blockIdx.z % P; // partial plane
     uint32_t klo = 0, khi = p.k;
-    if (S > 1) {
+    if (P > 1) {
+      // Window of split s (shaders/matmul_splitk2_kernel.glsl:138-142),
+      // then sub-window t of it by the same rule.
+      const uint32_t T = max(1u, p.sub_splits), S = P / T;
+      const uint32_t s = split / T, t = split % T;
       const uint32_t per = p.k / S, rem = p.k % S;
-      klo = split * per + min(split, rem);
-      khi = klo + per + (split < rem ? 1u : 0u);
+      const uint32_t lo = s * per + min(s, rem);
+      const uint32_t len = per + (s < rem ? 1u : 0u);
+      const uint32_t per2 = len / T, rem2 = len % T;
+      klo = lo + t * per2 + min(t, rem2);
+      khi = klo + per2 + (t < rem2 ? 1u : 0u);
     }
 
     const float *A = static_cast<const float *>(p.a) + (uint64_t)batch * p.stride_a;
@@ -247,3 +254,7 @@ TA_GEMM_F32_FAMILY(m256n128, 256, 128, 2, 2)
 TA_GEMM_F32_FAMILY(m128n128, 128, 128, 2, 2)
 TA_GEMM_F32_FAMILY(m128n64, 128, 64, 2, 2)
 TA_GEMM_F32_FAMILY(m64n64, 64, 64, 2, 2)
+// Skinny tiles (whole N of a deep-K split-K stage 1 in one tile, so A is
+// read once): 64x256 with 1x4 waves, 32x128 with 1x2 waves (128 threads).
+TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4)
+TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2)

@@ -45,11 +45,17 @@ typedef struct GemmArgs {
   uint32_t act;
   uint32_t binary;
   uint32_t bias_batch_stride; // 0 for [N] bias, N for [B, N]
-  uint32_t num_splits;        // 1 = plain GEMM
+  uint32_t num_splits;        // partial planes per batch (S * sub_splits); 1 = plain GEMM
   float alpha;
   float beta;
   uint32_t tiles_n; // ceil(N / BN): for the blockIdx -> tile remap
   uint32_t tiles_m; // ceil(M / BM)
+  // Split-K: each of the S = num_splits / sub_splits splits owns the
+  // reference window of K, cut again into sub_splits windows by the same
+  // rule; plane (batch * num_splits + s * sub_splits + t) holds window t of
+  // split s.
+  uint32_t sub_splits;
+  uint32_t pad;
 } GemmArgs;
 
 // Fixed-order reduction of split-K partial planes:

@@ -136,8 +136,6 @@ struct OpPlan {
   uint32_t mlp_layers = 0;
 };
 
-uint32_t gemm_threads(const KernelSpec &s) { return s.tile_m == 256 && s.tile_n == 256 ? 512 : 256; }
-
 struct ScratchNeed {
   uint64_t splitk = 0, partial = 0, counters = 0, mlp = 0;
   void merge(const ScratchNeed &o) {
@@ -268,7 +266,8 @@ struct ExecutorImpl {
     ScratchNeed need;
     const KernelSpec &s = KERNEL_SPECS[p.kernel];
     if (p.splitk2) {
-      need.splitk = (uint64_t)d.batch * d.m * d.n * *p.splitk2 * 4;
+      need.splitk = (uint64_t)d.batch * d.m * d.n * *p.splitk2 *
+                    splitk_sub_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, *p.splitk2) * 4;
     } else if (s.is_gemv()) {
       GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, p.role == 2,
                             gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, p.role == 2));
@@ -291,7 +290,10 @@ struct ExecutorImpl {
     a.n = d.n;
     a.k = d.k;
     a.alpha = op.call.alpha;
-    a.num_splits = std::max(1u, splits);
+    const uint32_t sub =
+        splits > 1 ? splitk_sub_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, splits) : 1;
+    a.num_splits = std::max(1u, splits) * sub;
+    a.sub_splits = sub;
     if (splits <= 1) {
       a.flags = op.call.accumulate ? TA_FLAG_ACCUMULATE : 0;
       if (op.epilogue.bias) {
@@ -321,10 +323,9 @@ struct ExecutorImpl {
       r.c = static_cast<float *>(op.call.c->device_ptr());
       r.mn = (uint64_t)d.m * d.n;
       r.total = r.mn * d.batch;
-      r.num_splits = splits;
+      r.num_splits = a.num_splits;
       const uint64_t quads = (r.total + 3) / 4;
-      const uint64_t groups =
-          std::min<uint64_t>((quads + kReduceThreads - 1) / kReduceThreads, 8ull * ctx->cu_count());
+      const uint64_t groups = std::min<uint64_t>((quads + 31) / 32, 8ull * ctx->cu_count());
       launch("ta_splitk_reduce", (uint32_t)std::max<uint64_t>(groups, 1), 1, 1, kReduceThreads,
              &r, stream);
     }

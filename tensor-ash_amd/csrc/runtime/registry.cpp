@@ -20,6 +20,8 @@ const KernelSpec KERNEL_SPECS[] = {
     {"f32_m128n128", 128, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m128n128", "medium"},
     {"f32_m128n64", 128, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m128n64", ""},
     {"f32_m64n64", 64, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m64n64", "small"},
+    {"f32_m64n256", 64, 256, 16, KernelKind::GemmF32, "ta_gemm_f32_m64n256", ""},
+    {"f32_m32n128", 32, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m32n128", ""},
     {"f16w_m256n256", 256, 256, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m256n256", ""},
     {"f16w_m256n128", 256, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m256n128", ""},
     {"f16w_m128n128", 128, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n128", ""},
@@ -176,8 +178,41 @@ std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims) {
 
 // ---- split-K (src/executor/splitk2.rs:36-271, retuned for 256 CUs) ----
 
+// Skinny split-K shapes take a tile spanning their whole N where possible
+// (A is then read once per window).
 const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n) {
-  return KERNEL_SPECS[registry_index(m >= 128 && n >= 128 ? "f32_m128n128" : "f32_m64n64")];
+  const char *name = m >= 128 && n >= 128 ? "f32_m128n128"
+                     : m <= 32            ? "f32_m32n128"
+                     : m <= 64 && n >= 256 ? "f32_m64n256"
+                                           : "f32_m64n64";
+  return KERNEL_SPECS[registry_index(name)];
+}
+
+uint32_t gemm_threads(const KernelSpec &s) {
+  if (s.tile_m == 256 && s.tile_n == 256)
+    return 512;
+  return s.tile_m == 32 ? 128 : 256;
+}
+
+// Sub-windows per split for stage 1.  A stage-1 workgroup keeps about one
+// 16-deep K slab of A and B in flight, so HBM needs several hundred of
+// them: aim for 4 workgroups per CU (8 for 128-thread tiles), with >= 256
+// K values per window, grid z <= 65535, u32 scratch addressing and at most
+// 256 MiB of partial planes.
+uint32_t splitk_sub_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                           uint32_t splits) {
+  if (splits < 2 || batch == 0)
+    return 1;
+  const KernelSpec &s = splitk_stage1_spec(m, n);
+  const uint64_t tiles = (uint64_t)batch * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
+  const uint64_t target = (uint64_t)cus * (gemm_threads(s) <= 128 ? 8 : 4);
+  uint64_t t = std::max<uint64_t>(1, (target + tiles * splits - 1) / (tiles * splits));
+  t = std::min<uint64_t>(t, std::max<uint64_t>(1, k / ((uint64_t)splits * 256)));
+  t = std::min<uint64_t>(t, 65535 / ((uint64_t)batch * splits));
+  const uint64_t plane = (uint64_t)batch * m * n;
+  t = std::min<uint64_t>(t, std::max<uint64_t>(1, ((uint64_t)UINT32_MAX + 1) / (plane * splits)));
+  t = std::min<uint64_t>(t, std::max<uint64_t>(1, (256ull << 20) / (plane * 4 * splits)));
+  return (uint32_t)std::max<uint64_t>(1, t);
 }
 
 // Deep-K shapes whose data-parallel grid covers less than half of the CUs
