@@ -76,11 +76,12 @@ TA_DEVICE void ta_tile_coords(uint32_t lin, uint32_t tiles_m, uint32_t tiles_n,
 // l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 // Split mode (num_splits > 1): alpha * partial to plane (batch*S + split).
 // C_F16: C is f16 storage (RNE), only alpha / accumulate apply.
+// Waves with `active` false hold no tile and only join the barriers.
 template <int WTM, int WTN, int FM, int FN, int T, bool C_F16>
 TA_DEVICE void ta_store_tile(float *smem, int smem_floats, const f32x16 (&acc)[FM][FN],
                              const GemmArgs &p, uint32_t lane, uint32_t wave, uint32_t wm,
                              uint32_t wn, uint32_t m0, uint32_t n0, uint32_t batch,
-                             uint32_t split) {
+                             uint32_t split, bool active = true) {
   constexpr int LDC = WTN + 4;
   (void)smem_floats;
   float *Cs = smem + wave * (32 * LDC);
@@ -90,16 +91,18 @@ TA_DEVICE void ta_store_tile(float *smem, int smem_floats, const f32x16 (&acc)[F
   const bool vec_out = (p.n & 3u) == 0u;
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
+    if (active) {
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
+      for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        Cs[(8 * (r / 4) + 4 * lg + (r % 4)) * LDC + fn * 32 + lr] = acc[fm][fn][r];
+        for (int r = 0; r < 16; ++r)
+          Cs[(8 * (r / 4) + 4 * lg + (r % 4)) * LDC + fn * 32 + lr] = acc[fm][fn][r];
+    }
     __syncthreads();
     const uint32_t row0 = m0 + wm * WTM + fm * 32;
     const uint32_t col0 = n0 + wn * WTN;
 #pragma unroll 2
-    for (int i = 0; i < 32 * WTN / 4 / 64; ++i) {
+    for (int i = 0; i < (active ? 32 * WTN / 4 / 64 : 0); ++i) {
       const uint32_t e = lane + 64u * i;
       const uint32_t lrow = e / (WTN / 4), c4 = (e % (WTN / 4)) * 4;
       const uint32_t row = row0 + lrow, col = col0 + c4;

@@ -189,6 +189,201 @@ struct GemmH16 {
   }
 };
 
+
+// ---------------------------------------------------------------------
+// Pipelined f16 x f16 GEMM (both operands f16 in memory), the fast path
+// for K % BK == 0 and N % 8 == 0.  The f16w route gets its f16 A from
+// ta_cvt_f32_f16 (RNE, the same rounding as staging-time conversion), the
+// a16 route reads its A directly.
+//
+//  * Global -> LDS with gfx950's direct loads (global_load_lds_dwordx4):
+//    no register staging; NS stages of BK k-values, NS - 1 of them in
+//    flight, one barrier per stage.  The loads are issued from inline asm
+//    with explicit vmcnt waits: the compiler would otherwise wait for every
+//    outstanding direct load before each LDS read, serialising the
+//    pipeline.
+//  * A stage: As[m][BK] f16, B stage: Bs[BK][BN] f16 exactly as B lies in
+//    memory (n contiguous).  A wave instruction writes 1 KiB of LDS
+//    contiguously (lane l at +16 l), so the bank-conflict swizzles are
+//    applied to which 16-byte global chunk a lane fetches: LDS slot c of
+//    row r holds global chunk c ^ swz(r).
+//  * Waves: WGM x WGN, each owning a WTM x WTN sub-tile of FM x FN MFMA
+//    blocks of 32x32.
+//  * A operand: one ds_read_b128 per 32x32x16 MFMA (row, 8 k).  B operand:
+//    two ds_read_b64_tr_b16 (the CDNA4 LDS transpose read): in each group
+//    of 16 lanes, lane i receives element i % 4 of the 8-byte pieces the
+//    group's lanes 4j + i / 4 address (j = 0..3), so addressing row
+//    k0 + t / 4, columns nb + 4 (t % 4) from lane t hands lane i the
+//    column nb + i over rows k0..k0+3 - the MFMA's B layout, read from a
+//    row-major tile.  All reads of a stage are issued before its MFMAs.
+//  * Rows past M and column chunks past N read clamped (valid) addresses:
+//    their products only reach outputs the store guards drop.
+template <int BM, int BN, int BK, int WGM, int WGN, int NS, bool C_F16>
+struct GemmH16Lds {
+  static constexpr int T = 64 * WGM * WGN;
+  static constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int KS = BK / 16; // MFMA k-steps per stage
+  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int CPA = BK / 8, CPR = BN / 8; // 16-byte chunks per A / B row
+  static constexpr int A_LD = A_BYTES / 16 / T, B_LD = B_BYTES / 16 / T;
+  static constexpr int LD = A_LD + B_LD; // direct loads per thread per stage
+  static_assert(A_LD * T * 16 == A_BYTES && B_LD * T * 16 == B_BYTES, "stages split evenly");
+  static_assert(CPA == 8 || CPA == 16, "BK is 64 or 128");
+  static_assert(CPR >= 8, "B swizzle needs >= 8 chunks per row");
+  static_assert(FM >= 1 && FN >= 1, "wave tile must be a multiple of 32");
+  static constexpr int SMEM_BYTES = NS * STAGE;
+  static_assert(WGM * WGN * 32 * (WTN + 4) * 4 <= SMEM_BYTES, "C staging fits in LDS");
+  static_assert(NS >= 2 && (NS - 2) * LD <= 63, "vmcnt range");
+
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+
+  // Swizzles (in 16-byte chunks), conflict-free whether the LDS serves
+  // 128 or 256 bytes per cycle.  A (ds_read_b128, 8 or 16 lanes per
+  // cycle on consecutive rows, one chunk column): the rows' chunks must
+  // land in distinct slots modulo 8 for 8 consecutive rows and in distinct
+  // (row parity, slot) pairs for 16.  B (transpose reads, 16 or 32 lanes
+  // per cycle on 4 consecutive rows x 2 or 4 chunks): row j of the four
+  // is XORed with a pattern that separates the rows in chunk bits (b1,b2)
+  // and in (b2,b3) - for 8-chunk rows, bit b2 together with the row parity.
+  static TA_DEVICE uint32_t swz_a(uint32_t row) {
+    return CPA == 8 ? (row & 7u) ^ ((row >> 3) & 1u) : row & 15u;
+  }
+  static TA_DEVICE uint32_t swz_b(uint32_t row) {
+    return CPR >= 16 ? (0xACA60u >> (4u * (row & 3u))) & 15u : 2u * (row & 3u);
+  }
+
+  static TA_DEVICE void load16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                 : "memory", "m0");
+  }
+
+  static TA_DEVICE void run(const GemmArgs &p) {
+    __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WGN, wn = wave % WGN;
+    uint32_t tm, tn;
+    ta_tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t batch = blockIdx.z;
+    const _Float16 *A = static_cast<const _Float16 *>(p.a) + (uint64_t)batch * p.stride_a;
+    const _Float16 *B = static_cast<const _Float16 *>(p.b) + (uint64_t)batch * p.stride_b;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+
+    // Per-thread source pointers of its direct loads (advanced per stage).
+    const char *asrc[A_LD];
+    const char *bsrc[B_LD];
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const uint32_t q = i * T + tid, row = q / CPA, c = (q % CPA) ^ swz_a(row);
+      const uint32_t gm = min(m0 + row, p.m - 1);
+      asrc[i] = reinterpret_cast<const char *>(A + (uint64_t)gm * p.k + 8 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const uint32_t q = i * T + tid, row = q / CPR, c = (q % CPR) ^ swz_b(row);
+      const uint32_t gn = min(n0 + 8 * c, p.n - 8);
+      bsrc[i] = reinterpret_cast<const char *>(B + (uint64_t)row * p.n + gn);
+    }
+    const uint64_t b_step = (uint64_t)BK * p.n * 2;
+
+    auto issue = [&](uint32_t stage) {
+      const uint32_t base = lds0 + stage * STAGE + wave * 64 * 16;
+#pragma unroll
+      for (int i = 0; i < A_LD; ++i) {
+        load16(asrc[i], base + i * T * 16);
+        asrc[i] += BK * 2;
+      }
+#pragma unroll
+      for (int i = 0; i < B_LD; ++i) {
+        load16(bsrc[i], base + A_BYTES + i * T * 16);
+        bsrc[i] += b_step;
+      }
+    };
+
+    // Per-lane LDS read offsets within a stage.
+    const uint32_t lr = lane & 31u, lg = lane >> 5;
+    uint32_t a_off[KS][FM];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const uint32_t row = wm * WTM + fm * 32 + lr;
+        a_off[ks][fm] = row * (BK * 2) + 16u * ((2u * ks + lg) ^ swz_a(row));
+      }
+    const uint32_t g = lane >> 4, t = lane & 15u;
+    uint32_t b_off[KS][FN][2];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const uint32_t row = ks * 16 + 8 * (g >> 1) + 4 * rr + (t >> 2);
+          const uint32_t col = wn * WTN + fn * 32 + 16 * (g & 1u) + 4 * (t & 3u);
+          b_off[ks][fn][rr] = A_BYTES + row * (BN * 2) + 16u * ((col >> 3) ^ swz_b(row)) +
+                             (col & 7u) * 2;
+        }
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[fm][fn][r] = 0.0f;
+
+    const uint32_t kts = p.k / BK;
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+      if (s < (int)kts)
+        issue(s);
+
+    for (uint32_t kt = 0; kt < kts; ++kt) {
+      if (kt + NS - 2 < kts)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * LD) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (kt + NS - 1 < kts)
+        issue((kt + NS - 1) % NS);
+      const uint32_t st = lds0 + (kt % NS) * STAGE;
+      f16x8 a[KS][FM], b[KS][FN];
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+          a[j][fm] = *(lds_f16x8 *)(uintptr_t)(st + a_off[j][fm]);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][0]));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][1]));
+          b[j][fn] = __builtin_bit_cast(
+              f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < KS; ++j)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+            acc[fm][fn] =
+                __builtin_amdgcn_mfma_f32_32x32x16_f16(a[j][fm], b[j][fn], acc[fm][fn], 0, 0, 0);
+    }
+    __syncthreads();
+    ta_store_tile<WTM, WTN, FM, FN, T, C_F16>(reinterpret_cast<float *>(smem), SMEM_BYTES / 4, acc,
+                                              p, lane, wave, wm, wn, m0, n0, batch, 0);
+  }
+};
+
 } // namespace
 
 #define TA_GEMM_H16(NAME, BM, BN, WGM, WGN, VEC, A_F16)                             \
@@ -206,3 +401,46 @@ TA_GEMM_H16_FAMILY(m128n128, 128, 128, 2, 2)
 TA_GEMM_H16_FAMILY(m128n64, 128, 64, 2, 2)
 TA_GEMM_H16_FAMILY(m64n128, 64, 128, 2, 2)
 TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
+
+// Pipelined kernels: ta_gemm_h16_<tile>_lds (A pre-rounded to f16 by
+// ta_cvt_f32_f16, f32 C with the fused epilogue) and ta_gemm_a16_<tile>_lds
+// (f16 A, f16 C).
+#define TA_GEMM_LDS(TAG, BM, BN, BK, WGM, WGN, NS)                                        \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void ta_gemm_h16_##TAG##_lds(   \
+      GemmArgs p) {                                                                       \
+    GemmH16Lds<BM, BN, BK, WGM, WGN, NS, false>::run(p);                                  \
+  }                                                                                       \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void ta_gemm_a16_##TAG##_lds(   \
+      GemmArgs p) {                                                                       \
+    GemmH16Lds<BM, BN, BK, WGM, WGN, NS, true>::run(p);                                   \
+  }
+
+#ifndef TA_LDS_TILES
+TA_GEMM_LDS(m256n256, 256, 256, 64, 2, 4, 2)
+TA_GEMM_LDS(m128n128, 128, 128, 64, 2, 2, 3)
+TA_GEMM_LDS(m128n64, 128, 64, 64, 2, 2, 4)
+TA_GEMM_LDS(m64n128, 64, 128, 64, 2, 2, 4)
+TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4)
+#else
+TA_LDS_TILES
+#endif
+
+// f32 -> f16 (RNE) of n elements, 8 per thread: the A pre-pass of the
+// pipelined f16w kernels.
+extern "C" __global__ __launch_bounds__(256) void ta_cvt_f32_f16(CvtArgs p) {
+  const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i + 8 <= p.n) {
+    const f32x4 lo = *reinterpret_cast<const f32x4 *>(p.src + i);
+    const f32x4 hi = *reinterpret_cast<const f32x4 *>(p.src + i + 4);
+    f16x8 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      o[c] = (_Float16)lo[c];
+      o[c + 4] = (_Float16)hi[c];
+    }
+    *reinterpret_cast<f16x8 *>(reinterpret_cast<_Float16 *>(p.dst) + i) = o;
+  } else {
+    for (uint64_t j = i; j < p.n; ++j)
+      reinterpret_cast<_Float16 *>(p.dst)[j] = (_Float16)p.src[j];
+  }
+}

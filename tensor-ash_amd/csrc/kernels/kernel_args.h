@@ -69,6 +69,13 @@ typedef struct SplitReduceArgs {
   uint32_t pad;
 } SplitReduceArgs;
 
+// Element-wise f32 -> f16 (RNE) conversion: dst[i] = src[i], i < n.
+typedef struct CvtArgs {
+  const float *src;
+  uint16_t *dst;
+  uint64_t n;
+} CvtArgs;
+
 // Decode GEMV over packed f16 weights W[N/TW][K][TW] (or row-major):
 // Y[m, :] = epilogue(alpha * X[m, :] @ W) for m < rows (rows <= 8).
 // With `w2` set (dual mode) the same launch also computes

@@ -273,8 +273,17 @@ struct ExecutorImpl {
                             gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, p.role == 2));
       need.partial = g.partial_bytes;
       need.counters = (uint64_t)g.tiles * TA_GEMV_COUNTER_STRIDE;
+    } else if (s.kind == KernelKind::GemmF16Mfma && gemm_lds_ok(d)) {
+      need.splitk = a16_bytes(d);
     }
     return need;
+  }
+
+  // f16 copy of A for the pipelined f16w route (one plane when A is
+  // broadcast), kept in the split-K region: ops run in stream order.
+  static uint64_t a16_bytes(const ResolvedMatmul &d) {
+    const uint64_t planes = d.batch_stride_a ? d.batch : 1;
+    return (planes * d.m * d.k * 2 + 255) / 256 * 256;
   }
 
   void launch_gemm(const KernelSpec &s, const ResolvedMatmul &d, const MatmulOp &op,
@@ -314,9 +323,23 @@ struct ExecutorImpl {
     if (gz > 65535 || gx > 0x7fffffffull)
       fail("matmul grid (" + std::to_string(gx) + ", 1, " + std::to_string(gz) +
            ") exceeds the HIP launch limits");
+    const bool lds = (s.kind == KernelKind::GemmF16Mfma || s.kind == KernelKind::GemmA16) &&
+                     gemm_lds_ok(d);
+    if (lds && s.kind == KernelKind::GemmF16Mfma) {
+      // A -> f16 (RNE) pre-pass into scratch; the GEMM then reads f16 A.
+      CvtArgs cv{};
+      cv.src = static_cast<const float *>(a.a);
+      cv.dst = static_cast<uint16_t *>(splitk_scratch);
+      cv.n = (d.batch_stride_a ? (uint64_t)d.batch : 1) * d.m * d.k;
+      const uint64_t blocks = (cv.n + 8 * 256 - 1) / (8 * 256);
+      if (blocks > 0x7fffffffull)
+        fail("f16 conversion grid exceeds the HIP launch limits");
+      launch("ta_cvt_f32_f16", (uint32_t)blocks, 1, 1, 256, &cv, stream);
+      a.a = splitk_scratch;
+    }
     const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
-    launch(std::string(s.symbol) + (vec ? "_vec" : "_gen"), (uint32_t)gx, 1, (uint32_t)gz,
-           gemm_threads(s), &a, stream);
+    launch(std::string(s.symbol) + (lds ? "_lds" : vec ? "_vec" : "_gen"), (uint32_t)gx, 1,
+           (uint32_t)gz, gemm_threads(s), &a, stream);
     if (splits > 1) {
       SplitReduceArgs r{};
       r.scratch = static_cast<const float *>(splitk_scratch);

@@ -27,6 +27,7 @@ const KernelSpec KERNEL_SPECS[] = {
     {"f16w_m128n128", 128, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n128", ""},
     {"f16w_m128n64", 128, 64, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n64", ""},
     {"f16w_m64n64", 64, 64, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m64n64", ""},
+    {"f16w_mfma_m256n256", 256, 256, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m256n256", ""},
     {"f16w_mfma_m128n128", 128, 128, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m128n128",
      "f16w_coopmat_aligned"},
     {"f16w_mfma_m128n64", 128, 64, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m128n64",
@@ -35,6 +36,7 @@ const KernelSpec KERNEL_SPECS[] = {
      "f16w_coopmat_m64n128"},
     {"f16w_mfma_m64n64", 64, 64, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m64n64",
      "f16w_coopmat_m64n64"},
+    {"f16w_a16_m256n256", 256, 256, 64, KernelKind::GemmA16, "ta_gemm_a16_m256n256", ""},
     {"f16w_a16_m128n128", 128, 128, 64, KernelKind::GemmA16, "ta_gemm_a16_m128n128",
      "f16w_a16_coopmat_aligned"},
     {"f16w_a16_m128n64", 128, 64, 64, KernelKind::GemmA16, "ta_gemm_a16_m128n64",
@@ -102,7 +104,15 @@ namespace {
 uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 } // namespace
 
+// Shapes the pipelined f16-MFMA kernels (`_lds` code objects) take: whole
+// 64-deep K stages and 16-byte B rows.
+bool gemm_lds_ok(const ResolvedMatmul &d) { return d.k > 0 && d.k % 64 == 0 && d.n % 8 == 0; }
+
 bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
+  // The 256x256 f16-MFMA tiles exist only as pipelined kernels.
+  if ((s.kind == KernelKind::GemmF16Mfma || s.kind == KernelKind::GemmA16) && s.tile_m == 256 &&
+      !gemm_lds_ok(d))
+    return false;
   if (d.a_f16)
     return s.kind == KernelKind::GemmA16;
   if (d.packed_b)
@@ -138,32 +148,50 @@ static size_t pick_tile(const char *const *names, int count, uint32_t cus, uint3
   return registry_index(names[count - 1]);
 }
 
-// Shape heuristic for 256-CU MI355X (role of src/pipeline/mod.rs:293-360
-// and selection.rs:89-172; the reference's NVIDIA-tuned tables are not a
-// target): decode shapes (M <= 8, one batch) stream the weights through
-// the GEMV; f16 weights with M, N >= 64 run on the f16 MFMA (A rounded to
-// f16 at staging, like the reference's coopmat route), smaller f16-weight
-// shapes widen B exactly on the FP32 MFMA; f16 activations take the a16
-// kernels.  Tiles: the largest whose grid still covers every CU once.
-size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
-                              bool b_f16, bool packed_b, bool a_f16) {
-  (void)k;
-  static const char *f32_tiles[] = {"f32_m256n256", "f32_m256n128", "f32_m128n128",
-                                    "f32_m128n64", "f32_m64n64"};
-  static const char *f16w_tiles[] = {"f16w_m256n256", "f16w_m256n128", "f16w_m128n128",
-                                     "f16w_m128n64", "f16w_m64n64"};
+// f16-MFMA tile: pipelined shapes take 256x256 when that grid still covers
+// every CU, 128x128 when it covers them twice, else 64x64 (measured on
+// M = 512 prefill shapes: smaller tiles win while the grid is small);
+// other shapes take the largest register-staged tile covering every CU.
+static size_t pick_f16_mfma(bool a16, uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
+                            uint32_t k) {
   static const char *mfma16_tiles[] = {"f16w_mfma_m128n128", "f16w_mfma_m128n64",
                                        "f16w_mfma_m64n128", "f16w_mfma_m64n64"};
   static const char *a16_tiles[] = {"f16w_a16_m128n128", "f16w_a16_m128n64",
                                     "f16w_a16_m64n128", "f16w_a16_m64n64"};
+  ResolvedMatmul d;
+  d.m = m;
+  d.n = n;
+  d.k = k;
+  if (!gemm_lds_ok(d))
+    return pick_tile(a16 ? a16_tiles : mfma16_tiles, 4, cus, batch, m, n);
+  const std::string pre = a16 ? "f16w_a16_" : "f16w_mfma_";
+  const uint64_t t256 = (uint64_t)batch * div_ceil(m, 256) * div_ceil(n, 256);
+  const uint64_t t128 = (uint64_t)batch * div_ceil(m, 128) * div_ceil(n, 128);
+  const char *tile = t256 >= cus ? "m256n256" : t128 >= 2ull * cus ? "m128n128" : "m64n64";
+  return registry_index((pre + tile).c_str());
+}
+
+// Shape heuristic for 256-CU MI355X (role of src/pipeline/mod.rs:293-360
+// and selection.rs:89-172; the reference's NVIDIA-tuned tables are not a
+// target): decode shapes (M <= 8, one batch) stream the weights through
+// the GEMV; f16 weights with M, N >= 64 run on the f16 MFMA (A rounded to
+// f16 RNE, like the reference's coopmat route), smaller f16-weight
+// shapes widen B exactly on the FP32 MFMA; f16 activations take the a16
+// kernels.  FP32 tiles: the largest whose grid still covers every CU once.
+size_t heuristic_kernel_index(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                              bool b_f16, bool packed_b, bool a_f16) {
+  static const char *f32_tiles[] = {"f32_m256n256", "f32_m256n128", "f32_m128n128",
+                                    "f32_m128n64", "f32_m64n64"};
+  static const char *f16w_tiles[] = {"f16w_m256n256", "f16w_m256n128", "f16w_m128n128",
+                                     "f16w_m128n64", "f16w_m64n64"};
   if (a_f16)
-    return pick_tile(a16_tiles, 4, cus, batch, m, n);
+    return pick_f16_mfma(true, cus, batch, m, n, k);
   if (packed_b)
     return registry_index(n % 64 == 0 ? "f16w_gemv_packed_t64" : "f16w_gemv_packed_t32");
   if (batch == 1 && m <= kGemvMaxRows && n % (b_f16 ? 4 : 2) == 0)
     return registry_index(b_f16 ? "f16w_gemv_row" : "f32_gemv_row");
   if (b_f16 && m >= 64 && n >= 64)
-    return pick_tile(mfma16_tiles, 4, cus, batch, m, n);
+    return pick_f16_mfma(false, cus, batch, m, n, k);
   return pick_tile(b_f16 ? f16w_tiles : f32_tiles, 5, cus, batch, m, n);
 }
 

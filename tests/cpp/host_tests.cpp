@@ -132,8 +132,12 @@ static void test_routing() {
   CHECK(name(8, 2048, 2048, 2048, false, false) == "f32_m256n256");
   CHECK(name(1, 512, 512, 512, false, false) == "f32_m64n64");
   CHECK(name(1, 512, 2560, 2048, true, false) == "f16w_mfma_m64n64");
-  CHECK(name(1, 512, 5632, 2048, true, false) == "f16w_mfma_m128n64");
-  CHECK(name(1, 4096, 4096, 4096, true, false) == "f16w_mfma_m128n128");
+  CHECK(name(1, 512, 5632, 2048, true, false) == "f16w_mfma_m64n64");
+  CHECK(name(1, 4096, 4096, 4096, true, false) == "f16w_mfma_m256n256");
+  CHECK(name(1, 2048, 4096, 4096, true, false) == "f16w_mfma_m128n128");
+  // Ragged K or N: register-staged tiles only (no 256x256).
+  CHECK(name(1, 4096, 4096, 4000, true, false) == "f16w_mfma_m128n128");
+  CHECK(name(1, 4096, 4100, 4096, true, false) == "f16w_mfma_m128n128");
   CHECK(name(1, 32, 4096, 4096, true, false) == "f16w_m64n64"); // M < 64: exact widening path
   CHECK(std::string(KERNEL_SPECS[heuristic_kernel_index(cus, 1, 512, 256, 2048, true, false, true)]
                         .name) == "f16w_a16_m64n64");

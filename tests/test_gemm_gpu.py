@@ -213,6 +213,8 @@ def test_f16_mfma_gemm(ta, ctx, ex, oracle, shape):
     hbias = oracle.fill_det(n, 93)
     refs = f16_mfma_refs(ha, hb, 1, m, n, k, oracle, bias=hbias, act=2)
     names = [n_ for n_ in ta.kernel_names() if n_.startswith("f16w_mfma")] if m * n * k <= 1 << 24 else []
+    if k % 64 or n % 8:  # the 256x256 tile exists only as a pipelined kernel
+        names = [n_ for n_ in names if "m256n256" not in n_]
     for name in [None] + names:
         kex = ex if name is None else ta.Executor(ctx, kernel_selection=name, tune=False)
         if name is None:
@@ -222,6 +224,34 @@ def test_f16_mfma_gemm(ta, ctx, ex, oracle, shape):
         bias, c = kex.tensor_from(hbias, shape=[n]), kex.tensor([m, n])
         kex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_SILU))])
         check_f16_mfma(kex.download(c), refs, k, oracle)
+
+
+@pytest.mark.parametrize("name", ["f16w_mfma_m64n64", "f16w_mfma_m128n128", "f16w_mfma_m256n256"])
+@pytest.mark.parametrize("epi", ["bias_bn_gelu", "add_scaled", "mul", "broadcast_a"])
+def test_f16_mfma_pipelined_epilogues(ta, ctx, oracle, name, epi):
+    """Pipelined f16-MFMA kernels (K % 64 == 0, N % 8 == 0): ragged M and N
+    tiles, batched [B, N] bias, both binaries and a broadcast A plane (its
+    f16 copy is one plane)."""
+    kex = ta.Executor(ctx, kernel_selection=name, tune=False)
+    bt, m, n, k = 2, 300, 264, 192
+    ha = oracle.fill_det((1 if epi == "broadcast_a" else bt) * m * k, 7100)
+    hb = oracle.fill_normal(bt * k * n, 7101, 0.05)
+    hbias, hd = oracle.fill_det(bt * n, 7102), oracle.fill_det(bt * m * n, 7103)
+    a = kex.tensor_from(ha, shape=[m, k] if epi == "broadcast_a" else [bt, m, k])
+    b = kex.tensor_from(hb, shape=[bt, k, n], f16=True)
+    c = kex.tensor([bt, m, n])
+    d = kex.tensor_from(hd, shape=[bt, m, n])
+    if epi == "bias_bn_gelu":
+        e, kw = ta.Epilogue(bias=kex.tensor_from(hbias, shape=[bt, n]), activation=ta.ACTIVATION_GELU), \
+            dict(bias=hbias, bias_batch_stride=n, act=3)
+    elif epi == "add_scaled":
+        e, kw = ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=d, beta=-0.5), dict(binary=1, d=hd, beta=-0.5)
+    else:
+        e, kw = ta.Epilogue(binary=ta.BINARY_MUL, d=d), dict(binary=2, d=hd)
+    kex.run_ops([ta.MatmulOp(a, b, c, epilogue=e, alpha=1.25)])
+    ha_full = np.tile(ha, bt) if epi == "broadcast_a" else ha
+    refs = f16_mfma_refs(ha_full, hb, bt, m, n, k, oracle, alpha=1.25, **kw)
+    check_f16_mfma(kex.download(c), refs, k, oracle)
 
 
 def test_f16_mfma_batched_alpha_accumulate(ta, ex, oracle):
