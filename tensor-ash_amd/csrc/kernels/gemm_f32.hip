@@ -9,7 +9,8 @@
 // Design (one workgroup per BM x BN output tile, 64-wide waves):
 //  * v_mfma_f32_32x32x2_f32: each wave owns a (BM/WGM) x (BN/WGN) sub-tile
 //    as FM x FN blocks of 32x32 accumulators (16 floats per lane per block).
-//  * K is walked in slabs of BK=16.  A slab of A is staged in LDS as
+//  * K is walked in slabs of BK = 16 (32 for the 256x256 tile), each
+//    processed as 16-deep halves.  A slab of A is staged in LDS as
 //    As[m][k] (k contiguous, +4 pad) so a lane reads its eight k values for
 //    one slab with two 128-bit LDS reads; B is staged as Bs[k][n] (+4 pad)
 //    and read 32 consecutive columns per half-wave.  The MFMA k index a lane
@@ -28,9 +29,9 @@
 
 namespace {
 
-template <int BM, int BN, int WGM, int WGN, bool VEC, bool HALF_B>
+template <int BM, int BN, int WGM, int WGN, bool VEC, bool HALF_B, int BK_ = 16>
 struct GemmF32 {
-  static constexpr int BK = 16;
+  static constexpr int BK = BK_;
   static constexpr int T = 64 * WGM * WGN;
   static constexpr int WTM = BM / WGM;
   static constexpr int WTN = BN / WGN;
@@ -131,6 +132,15 @@ struct GemmF32 {
   static TA_DEVICE void compute(const float *As, const float *Bs, uint32_t lane,
                                 uint32_t wm, uint32_t wn,
                                 f32x16 (&acc)[FM][FN]) {
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16)
+      compute16(As + kk, Bs + kk * LDB, lane, wm, wn, acc);
+  }
+
+  // One 16-deep part of the slab (As / Bs offset to its first k).
+  static TA_DEVICE void compute16(const float *As, const float *Bs, uint32_t lane,
+                                  uint32_t wm, uint32_t wn,
+                                  f32x16 (&acc)[FM][FN]) {
     const uint32_t lr = lane & 31u, lg = lane >> 5;
     float a[FM][8], b[FN][8];
 #pragma unroll
@@ -236,25 +246,29 @@ struct GemmF32 {
   }
 };
 
+
 } // namespace
 
-#define TA_GEMM_F32(NAME, BM, BN, WGM, WGN, VEC, HALF_B)                          \
+#define TA_GEMM_F32(NAME, BM, BN, WGM, WGN, VEC, HALF_B, BK)                      \
   extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(GemmArgs p) { \
-    GemmF32<BM, BN, WGM, WGN, VEC, HALF_B>::run(p);                              \
+    GemmF32<BM, BN, WGM, WGN, VEC, HALF_B, BK>::run(p);                          \
   }
 
-#define TA_GEMM_F32_FAMILY(TAG, BM, BN, WGM, WGN)                               \
-  TA_GEMM_F32(ta_gemm_f32_##TAG##_vec, BM, BN, WGM, WGN, true, false)           \
-  TA_GEMM_F32(ta_gemm_f32_##TAG##_gen, BM, BN, WGM, WGN, false, false)          \
-  TA_GEMM_F32(ta_gemm_f16w_##TAG##_vec, BM, BN, WGM, WGN, true, true)           \
-  TA_GEMM_F32(ta_gemm_f16w_##TAG##_gen, BM, BN, WGM, WGN, false, true)
+#define TA_GEMM_F32_FAMILY(TAG, BM, BN, WGM, WGN, BK)                           \
+  TA_GEMM_F32(ta_gemm_f32_##TAG##_vec, BM, BN, WGM, WGN, true, false, BK)       \
+  TA_GEMM_F32(ta_gemm_f32_##TAG##_gen, BM, BN, WGM, WGN, false, false, BK)      \
+  TA_GEMM_F32(ta_gemm_f16w_##TAG##_vec, BM, BN, WGM, WGN, true, true, BK)       \
+  TA_GEMM_F32(ta_gemm_f16w_##TAG##_gen, BM, BN, WGM, WGN, false, true, BK)
 
-TA_GEMM_F32_FAMILY(m256n256, 256, 256, 2, 4)
-TA_GEMM_F32_FAMILY(m256n128, 256, 128, 2, 2)
-TA_GEMM_F32_FAMILY(m128n128, 128, 128, 2, 2)
-TA_GEMM_F32_FAMILY(m128n64, 128, 64, 2, 2)
-TA_GEMM_F32_FAMILY(m64n64, 64, 64, 2, 2)
+// The 256x256 tile walks K in 32-deep slabs (half the barriers; its two
+// 70 KiB LDS buffers still fit), the others in 16-deep slabs.
+TA_GEMM_F32_FAMILY(m256n256, 256, 256, 2, 4, 32)
+TA_GEMM_F32_FAMILY(m256n128, 256, 128, 2, 2, 16)
+TA_GEMM_F32_FAMILY(m128n128, 128, 128, 2, 2, 16)
+TA_GEMM_F32_FAMILY(m128n64, 128, 64, 2, 2, 16)
+TA_GEMM_F32_FAMILY(m64n64, 64, 64, 2, 2, 16)
 // Skinny tiles (whole N of a deep-K split-K stage 1 in one tile, so A is
 // read once): 64x256 with 1x4 waves, 32x128 with 1x2 waves (128 threads).
-TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4)
-TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2)
+TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4, 16)
+TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2, 16)
+

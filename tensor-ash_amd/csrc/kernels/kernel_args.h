@@ -66,7 +66,7 @@ typedef struct SplitReduceArgs {
   uint64_t total; // batch * mn
   uint64_t mn;
   uint32_t num_splits;
-  uint32_t pad;
+  uint32_t groups; // plane groups per element: power of two <= min(num_splits, 256)
 } SplitReduceArgs;
 
 // Element-wise f32 -> f16 (RNE) conversion: dst[i] = src[i], i < n.

@@ -4,19 +4,22 @@
 // Contract (the reference's reduce, shaders/matmul_f32_splitk2_reduce.comp:
 // 44-75, sums the S planes of batch b in order; here there are P planes,
 // S splits of P / S windows each): the P planes of batch b are cut into
-// G = min(P, 8) contiguous groups by the split-window rule; each group is
-// summed in plane order, then the group sums are added in group order.
-// No atomics anywhere, so the result is bit-identical from run to run for
-// a fixed P.
+// G = `groups` contiguous groups by the split-window rule; each group is
+// summed in plane order, then the group sums are added pairwise in a fixed
+// tree (g0 + g1, g2 + g3, ..., then those pairs, ...).
+// The host derives G from the shape alone (enough threads to cover the
+// chip), and nothing here uses atomics, so the result is bit-identical
+// from run to run for a fixed shape and P.
 //
-// HBM-bound: it reads every plane once and writes one.  A workgroup owns
-// 32 quads (four consecutive elements, one 128-bit load per plane when
-// mn % 4 == 0) and spreads the G groups over its threads, so the plane
-// loads of all groups are in flight together; group sums meet in LDS.
+// HBM-bound: it reads every plane once and writes one.  A workgroup of
+// 256 threads owns 256 / G quads (four consecutive elements, one 128-bit
+// load per plane when mn % 4 == 0); thread (g, quad) sums group g of its
+// quad with up to 8 plane loads in flight ahead of the in-order adds, and
+// the G group sums meet in LDS for the tree.
 #include "common.h"
 
 namespace {
-constexpr int kGroups = 8, kQuads = 32;
+constexpr int kThreads = 256, kBatch = 8;
 
 TA_DEVICE f32x4 load_quad(const SplitReduceArgs &p, bool vec, uint64_t base, uint32_t plane) {
   if (vec) {
@@ -35,30 +38,45 @@ TA_DEVICE f32x4 load_quad(const SplitReduceArgs &p, bool vec, uint64_t base, uin
 }
 } // namespace
 
-extern "C" __global__ __launch_bounds__(256) void ta_splitk_reduce(SplitReduceArgs p) {
-  __shared__ f32x4 part[kGroups][kQuads];
+extern "C" __global__ __launch_bounds__(kThreads) void ta_splitk_reduce(SplitReduceArgs p) {
+  __shared__ f32x4 part[kThreads];
   const uint64_t quads = (p.total + 3) / 4;
   const bool vec = (p.mn & 3u) == 0u;
   const uint32_t P = p.num_splits;
-  const uint32_t G = min((uint32_t)kGroups, P);
-  const uint32_t g = threadIdx.x / kQuads, ql = threadIdx.x % kQuads;
+  const uint32_t G = p.groups; // power of two <= min(P, 256), host-checked
+  const uint32_t QW = kThreads / G; // quads per workgroup pass
+  const uint32_t g = threadIdx.x / QW, ql = threadIdx.x % QW;
   const uint32_t per = P / G, rem = P % G;
   const uint32_t lo = g * per + min(g, rem);
-  const uint32_t hi = g < G ? lo + per + (g < rem ? 1u : 0u) : lo;
-  for (uint64_t qb = blockIdx.x; qb * kQuads < quads; qb += gridDim.x) {
-    const uint64_t q = qb * kQuads + ql;
-    if (q < quads && lo < hi) {
+  const uint32_t hi = lo + per + (g < rem ? 1u : 0u);
+  for (uint64_t qb = blockIdx.x; qb * QW < quads; qb += gridDim.x) {
+    const uint64_t q = qb * QW + ql;
+    if (q < quads) {
+      // Planes lo..hi-1 in order, loaded kBatch at a time ahead of their
+      // adds so the loads overlap; the adds keep the plane order.
       const uint64_t base = q * 4;
       f32x4 acc = load_quad(p, vec, base, lo);
-      for (uint32_t s = lo + 1; s < hi; ++s)
-        acc += load_quad(p, vec, base, s);
-      part[g][ql] = acc;
+      for (uint32_t s0 = lo + 1; s0 < hi; s0 += kBatch) {
+        f32x4 v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+          v[j] = s0 + j < hi ? load_quad(p, vec, base, s0 + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+          if (s0 + j < hi)
+            acc += v[j];
+      }
+      part[g * QW + ql] = acc;
+    }
+    // Group sums: fixed pairwise tree ((g0 + g1) + (g2 + g3)) + ...
+    for (uint32_t step = 1; step < G; step *= 2) {
+      __syncthreads();
+      if ((g & (2 * step - 1)) == 0 && q < quads)
+        part[g * QW + ql] += part[(g + step) * QW + ql];
     }
     __syncthreads();
     if (g == 0 && q < quads) {
-      f32x4 r = part[0][ql];
-      for (uint32_t gg = 1; gg < G; ++gg)
-        r += part[gg][ql];
+      const f32x4 r = part[ql];
       const uint64_t base = q * 4;
       if (vec) {
         *reinterpret_cast<f32x4 *>(p.c + base) = r;

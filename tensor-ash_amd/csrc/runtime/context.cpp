@@ -152,10 +152,16 @@ void *Context::function(const std::string &symbol) const {
   for (const auto &[name, f] : fns)
     if (name == symbol)
       return f;
+  // A miss in one code object sets HIP's thread-local last error; clear it
+  // again (unless an error was already pending) so the probe leaves no
+  // trace for the host application's own error checks.
+  const bool clean = hipPeekAtLastError() == hipSuccess;
   for (void *m : modules_) {
     hipFunction_t f = nullptr;
-    if (hipModuleGetFunction(&f, static_cast<hipModule_t>(m), symbol.c_str()) == hipSuccess &&
-        f) {
+    const hipError_t e = hipModuleGetFunction(&f, static_cast<hipModule_t>(m), symbol.c_str());
+    if (e != hipSuccess && clean)
+      (void)hipGetLastError();
+    if (e == hipSuccess && f) {
       fns.emplace_back(symbol, f);
       return f;
     }

@@ -348,9 +348,11 @@ struct ExecutorImpl {
       r.total = r.mn * d.batch;
       r.num_splits = a.num_splits;
       const uint64_t quads = (r.total + 3) / 4;
-      const uint64_t groups = std::min<uint64_t>((quads + 31) / 32, 8ull * ctx->cu_count());
-      launch("ta_splitk_reduce", (uint32_t)std::max<uint64_t>(groups, 1), 1, 1, kReduceThreads,
-             &r, stream);
+      r.groups = splitk_reduce_groups(ctx->cu_count(), quads, r.num_splits);
+      const uint64_t per_wg = kReduceThreads / r.groups;
+      const uint64_t wgs = std::min<uint64_t>((quads + per_wg - 1) / per_wg, 8ull * ctx->cu_count());
+      launch("ta_splitk_reduce", (uint32_t)std::max<uint64_t>(wgs, 1), 1, 1, kReduceThreads, &r,
+             stream);
     }
   }
 

@@ -71,6 +71,7 @@ uint32_t splitk_sub_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
                            uint32_t splits);
 std::optional<uint32_t> heuristic_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
                                          uint32_t k);
+uint32_t splitk_reduce_groups(uint32_t cus, uint64_t quads, uint32_t planes);
 uint32_t default_num_k_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k);
 bool auto_route_fits(uint32_t batch, uint32_t m, uint32_t n, uint32_t k, uint32_t splits);
 void validate_scratch_geometry(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,

@@ -15,14 +15,14 @@ namespace tensor_ash {
 // add "_vec" / "_gen" (aligned / ragged loads), GEMV entries add "_m1",
 // "_m2", "_m4", "_m8" (rows per launch) and "_dual" (SwiGLU pair).
 const KernelSpec KERNEL_SPECS[] = {
-    {"f32_m256n256", 256, 256, 16, KernelKind::GemmF32, "ta_gemm_f32_m256n256", "large"},
+    {"f32_m256n256", 256, 256, 32, KernelKind::GemmF32, "ta_gemm_f32_m256n256", "large"},
     {"f32_m256n128", 256, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m256n128", ""},
     {"f32_m128n128", 128, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m128n128", "medium"},
     {"f32_m128n64", 128, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m128n64", ""},
     {"f32_m64n64", 64, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m64n64", "small"},
     {"f32_m64n256", 64, 256, 16, KernelKind::GemmF32, "ta_gemm_f32_m64n256", ""},
     {"f32_m32n128", 32, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m32n128", ""},
-    {"f16w_m256n256", 256, 256, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m256n256", ""},
+    {"f16w_m256n256", 256, 256, 32, KernelKind::GemmF16w, "ta_gemm_f16w_m256n256", ""},
     {"f16w_m256n128", 256, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m256n128", ""},
     {"f16w_m128n128", 128, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n128", ""},
     {"f16w_m128n64", 128, 64, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n64", ""},
@@ -241,6 +241,20 @@ uint32_t splitk_sub_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
   t = std::min<uint64_t>(t, std::max<uint64_t>(1, ((uint64_t)UINT32_MAX + 1) / (plane * splits)));
   t = std::min<uint64_t>(t, std::max<uint64_t>(1, (256ull << 20) / (plane * 4 * splits)));
   return (uint32_t)std::max<uint64_t>(1, t);
+}
+
+// Plane groups per element for the split-K reduce: at least 8, then
+// doubled (up to the plane count and 256) until quads * groups threads
+// give every CU about two workgroups' worth of loads, so small outputs
+// with many planes still spread over the chip.  A function of the shape
+// only, which keeps the summation order fixed.
+uint32_t splitk_reduce_groups(uint32_t cus, uint64_t quads, uint32_t planes) {
+  uint32_t g = 8;
+  while (g < 256 && 2 * g <= planes && quads * g < 512ull * cus)
+    g *= 2;
+  while (g > 1 && g > planes)
+    g /= 2;
+  return g;
 }
 
 // Deep-K shapes whose data-parallel grid covers less than half of the CUs

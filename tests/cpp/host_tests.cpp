@@ -158,6 +158,19 @@ static void test_routing() {
 }
 
 static void test_splitk() {
+  // Reduce plane groups: a power of two within [1, min(planes, 256)], a pure
+  // function of the shape (fixed summation order), and more groups for
+  // small outputs.
+  CHECK(splitk_reduce_groups(256, 4096, 256) == 32);
+  CHECK(splitk_reduce_groups(256, 1024, 256) == 128);
+  CHECK(splitk_reduce_groups(256, 1u << 20, 64) == 8);
+  CHECK(splitk_reduce_groups(256, 16, 3) == 2);
+  CHECK(splitk_reduce_groups(256, 16, 2) == 2);
+  for (uint32_t planes : {2u, 3u, 7u, 8u, 100u, 256u, 4096u})
+    for (uint64_t quads : {1ull, 100ull, 4096ull, 1ull << 22}) {
+      const uint32_t g = splitk_reduce_groups(256, quads, planes);
+      CHECK(g >= 1 && g <= planes && g <= 256 && (g & (g - 1)) == 0);
+    }
   const uint32_t cus = 256;
   // Behaviour (targets are this build's own, for 256 CUs):
   CHECK(heuristic_splits(cus, 1, 64, 256, 65536) == 128u); // 4 tiles -> ~2 WGs per CU

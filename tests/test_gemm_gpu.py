@@ -287,3 +287,19 @@ def test_a16_rejects_epilogue(ta, ex):
     bias = ex.tensor([64])
     with pytest.raises(ta.TensorAshError, match="cannot fuse"):
         ex.run_ops([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias))])
+
+
+def test_leaves_no_pending_hip_error(ta, ctx, oracle):
+    """Kernel lookups probe every code object; a miss must not leave HIP's
+    thread-local last error set for the host application (torch and other
+    HIP users check it after their own calls)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipGetLastError.restype = ctypes.c_int
+    hip.hipGetLastError()
+    kex = ta.Executor(ctx, tune=False)
+    a, b, c = kex.tensor_from(oracle.fill_det(64 * 64, 1), shape=[64, 64]), \
+        kex.tensor_from(oracle.fill_det(64 * 64, 2), shape=[64, 64], f16=True), kex.tensor([64, 64])
+    kex.run_ops([ta.MatmulOp(a, b, c)])
+    kex.run_matmuls_split_k2(kex.tensor([64, 2048]), kex.tensor([2048, 64]), kex.tensor([64, 64]), 4)
+    assert hip.hipGetLastError() == 0
