@@ -144,8 +144,14 @@ struct Gemv {
       v[1] = __builtin_bit_cast(float, (uint32_t)(raw >> 32));
     } else {
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < 4; ++c) {
         v[c] = (float)__builtin_bit_cast(_Float16, (uint16_t)(raw >> (16 * c)));
+        // Keep the widening a separate v_cvt_f32_f16: folded into every
+        // FMA it becomes v_fma_mix_f32, which issues at half the rate of
+        // v_fma_f32 on gfx950, and each weight feeds MR FMAs.
+        if constexpr (MR > 1)
+          asm volatile("" : "+v"(v[c]));
+      }
     }
   }
 
@@ -612,6 +618,11 @@ struct Gemv {
 
 // Rows of X staged per standalone unit: 16 KiB of LDS.
 template <int MR> constexpr int standalone_rows() { return 4096 / MR; }
+// Standalone launches with 4 or 8 rows load groups of 8 per matrix (their
+// accumulators take the registers a deeper group would: 8 rows of a dual
+// launch then fit 3 workgroups per CU instead of 2); 1 and 2 rows load
+// groups of 16.  The host's gemv_unit() mirrors this group size.
+template <int MR> constexpr int standalone_unroll() { return MR >= 4 ? 8 : 16; }
 
 // Persistent decode MLP chain.  Per layer, the first units_a workgroups run
 // gate/up (producer) units, the rest down-proj (consumer) units; layers
@@ -658,7 +669,8 @@ template <int MR> struct DecodeMlp {
 
 #define TA_GEMV(NAME, MR, DUAL, TW, WF32)                                          \
   extern "C" __global__ __launch_bounds__(kThreads) void NAME(GemvArgs p) {        \
-    Gemv<MR, DUAL, TW, WF32, kStandalone, standalone_rows<MR>()>::run(p);         \
+    Gemv<MR, DUAL, TW, WF32, kStandalone, standalone_rows<MR>(),                  \
+         standalone_unroll<MR>()>::run(p);                                        \
   }
 
 #define TA_GEMV_ROWS(PREFIX, DUAL, TW, WF32)                                       \

@@ -270,7 +270,7 @@ struct ExecutorImpl {
                     splitk_sub_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, *p.splitk2) * 4;
     } else if (s.is_gemv()) {
       GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, p.role == 2,
-                            gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, p.role == 2));
+                            gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, p.role == 2, d.m));
       need.partial = g.partial_bytes;
       need.counters = (uint64_t)g.tiles * TA_GEMV_COUNTER_STRIDE;
     } else if (s.kind == KernelKind::GemmF16Mfma && gemm_lds_ok(d)) {
@@ -362,7 +362,7 @@ struct ExecutorImpl {
                    const MatmulOp *up, Scratch &scratch, hipStream_t stream) const {
     const bool dual = up != nullptr;
     GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, dual,
-                          gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, dual));
+                          gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, dual, d.m));
     GemvArgs a{};
     a.x = static_cast<const float *>(op.call.a->device_ptr());
     a.w = static_cast<const uint16_t *>(op.call.b->device_ptr());

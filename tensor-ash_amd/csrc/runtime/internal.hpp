@@ -83,7 +83,7 @@ struct GemvPlan {
   uint32_t tw = 64, mr = 1, tiles = 0, kchunk = 0, kchunks = 1;
   uint64_t partial_bytes = 0; // 0 when kchunks == 1
 };
-uint32_t gemv_unit(uint32_t tw, bool f32_weights, bool dual);
+uint32_t gemv_unit(uint32_t tw, bool f32_weights, bool dual, uint32_t rows);
 GemvPlan plan_gemv(uint32_t cus, uint32_t rows, uint32_t n, uint32_t k, uint32_t tw, bool dual,
                    uint32_t unit);
 

@@ -333,10 +333,11 @@ std::optional<uint64_t> checked_auto_scratch_end(uint64_t offset, uint64_t bytes
 
 // ---- GEMV geometry ----
 // K granularity of a GEMV window: one unrolled load group of the kernel
-// (4 waves x 64/(TW/CPL) rows x 16 loads; CPL = 4 for f16, 2 for f32).
-uint32_t gemv_unit(uint32_t tw, bool f32_weights, bool /*dual*/) {
+// (4 waves x 64/(TW/CPL) rows x loads per group; CPL = 4 for f16, 2 for
+// f32; 16 loads per group for 1-2 rows, 8 for 4-8 rows).
+uint32_t gemv_unit(uint32_t tw, bool f32_weights, bool /*dual*/, uint32_t rows) {
   const uint32_t cpl = f32_weights ? 2 : 4;
-  return 4 * (64 / (tw / cpl)) * 16;
+  return 4 * (64 / (tw / cpl)) * (rows > 2 ? 8 : 16);
 }
 
 // ~3 workgroups per CU: K windows of at most 512 rows, a multiple of the

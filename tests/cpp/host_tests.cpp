@@ -209,7 +209,8 @@ static void test_gemv_plan() {
       for (bool dual : {false, true})
         for (uint32_t rows : {1u, 3u, 8u})
           for (uint32_t k : {64u, 300u, 2048u, 5632u, 65536u}) {
-            const uint32_t unit = gemv_unit(tw, f32w, dual);
+            const uint32_t unit = gemv_unit(tw, f32w, dual, rows);
+            CHECK(unit == 4 * (64 / (tw / (f32w ? 2 : 4))) * (rows > 2 ? 8 : 16));
             GemvPlan p = plan_gemv(256, rows, 5632, k, tw, dual, unit);
             CHECK(p.kchunk % unit == 0 && p.kchunk >= unit);
             CHECK((uint64_t)p.kchunk * p.kchunks >= k && (uint64_t)p.kchunk * (p.kchunks - 1) < k);
