@@ -233,6 +233,52 @@ ta_prepared *ta_prepared_create_v2(const ta_executor *exec,
                                    const ta_matmul_op_v2 *ops, size_t n_ops,
                                    uint32_t as_graph);
 
+/* Decode fusions of MatmulOp (src/matmul/api.rs:107-299), which the
+ * reference exposes in its Rust API only (MatmulOp::with_normed_a,
+ * with_store_rope, with_store_scatter, with_store_rope_scatter):
+ *  - norm_weight != NULL: C = rms_norm(A, norm_weight, norm_eps) @ B on a
+ *    decode GEMV route (M <= 8, batch 1); excludes an epilogue bias and
+ *    the add_scaled binary;
+ *  - store_kind (M = 1, f16 B, no epilogue, no accumulate): RoPE-rotate
+ *    the output row and store it to C, and/or scatter it into store_dst
+ *    (f32 or f16) at P * pos_scale + (c / head_dim) * stride_head +
+ *    (c % head_dim) * stride_dim, P = pos_base + *pos_addr (pos_addr: a
+ *    device address from ta_tensor_device_address, or 0). */
+enum {
+  TA_STORE_NONE = 0,
+  TA_STORE_ROPE = 1,
+  TA_STORE_SCATTER = 2,
+  TA_STORE_ROPE_SCATTER = 3,
+};
+typedef struct ta_store_desc { /* MatmulStoreDesc, src/matmul/api.rs:117-133 */
+  uint32_t head_dim;
+  uint32_t pos_base;
+  uint32_t pos_scale;
+  uint32_t stride_head;
+  uint32_t stride_dim;
+  uint32_t reserved; /* must be zero */
+  uint64_t pos_addr;
+} ta_store_desc;
+typedef struct ta_matmul_op_v3 {
+  ta_matmul_op_v2 v2;
+  const ta_tensor *norm_weight; /* f32 [K], or NULL */
+  float norm_eps;
+  uint32_t store_kind;          /* TA_STORE_* */
+  const ta_tensor *store_table; /* f32 [T_max, head_dim/2, 2] (rope kinds) */
+  const ta_tensor *store_dst;   /* scatter kinds */
+  ta_store_desc store;
+} ta_matmul_op_v3;
+int ta_run_ops_v3(const ta_executor *exec, const ta_matmul_op_v3 *ops,
+                  size_t n_ops, ta_run_stats *stats);
+int ta_run_op_graph_v3(const ta_executor *exec, const ta_matmul_op_v3 *ops,
+                       size_t n_ops, ta_run_stats *stats);
+ta_prepared *ta_prepared_create_v3(const ta_executor *exec,
+                                   const ta_matmul_op_v3 *ops, size_t n_ops,
+                                   uint32_t as_graph);
+/* Tensor::device_address (src/tensor.rs): the allocation's device address
+ * (0 for NULL), e.g. for ta_store_desc.pos_addr. */
+uint64_t ta_tensor_device_address(const ta_tensor *tensor);
+
 /* pack_f16w_row_tiles (src/matmul/api.rs:324-344): row-major [K, N] ->
  * [N/tile_n][K][tile_n]; dst holds K*N floats. */
 int ta_pack_f16w_row_tiles(const float *src, size_t k, size_t n,

@@ -176,3 +176,61 @@ def reference_gemm(a, b, batch, m, n, k, alpha=1.0, c_init=None, accumulate=Fals
     """cpu_bmm followed by the f64 epilogue: the full fused-op reference."""
     c = cpu_bmm(a, b, c_init, batch, m, n, k, alpha, accumulate)
     return epilogue(c, n, m * n, bias, bias_batch_stride, act, binary, d, beta)
+
+
+# ---- decode fusions (numpy restatements; pinned in tests/test_oracle.py) ----
+
+def rms_norm_rows(x, w, m: int, k: int, eps: float) -> np.ndarray:
+    """Normed-A reference of tests/correctness/fusion.rs:15-24
+    (cpu_rms_norm_f64): per row, x * w / sqrt(mean(x^2) + eps) in f64,
+    rounded to f32."""
+    x64 = np.asarray(x, dtype=np.float32).reshape(m, k).astype(np.float64)
+    w64 = np.asarray(w, dtype=np.float32).reshape(k).astype(np.float64)
+    inv = 1.0 / np.sqrt((x64 * x64).sum(axis=1, keepdims=True) / k + float(np.float32(eps)))
+    return (x64 * inv * w64).astype(np.float32).reshape(-1)
+
+
+def _fma32(a, b, c):
+    """f32 fused multiply-add: the product of two f32 is exact in f64; the
+    sum is then rounded to f64 and to f32 (a double rounding that can
+    differ from a single one only on exact f32 midpoints)."""
+    return (np.asarray(a, np.float32).astype(np.float64) * np.asarray(b, np.float32).astype(np.float64)
+            + np.asarray(c, np.float32).astype(np.float64)).astype(np.float32)
+
+
+def rope_pairs(y, table, pos: int, head_dim: int) -> np.ndarray:
+    """Store-time RoPE of one output row (shaders/matmul_row_bda_kernel.glsl:
+    163-176): column c with partner c ^ 1 and dim = c % head_dim takes the
+    (cos, sin) at table[(pos * head_dim/2 + dim/2) * 2 + {0, 1}];
+    even dim: fma(v, cos, -partner*sin); odd dim: fma(partner, sin, v*cos)."""
+    y = np.asarray(y, dtype=np.float32).reshape(-1)
+    t = np.asarray(table, dtype=np.float32).reshape(-1)
+    c = np.arange(y.size)
+    dim = c % head_dim
+    angle = (pos * (head_dim // 2) + dim // 2) * 2
+    cos_t, sin_t = t[angle], t[angle + 1]
+    partner = y[c ^ 1]
+    even = _fma32(y, cos_t, (-partner * sin_t).astype(np.float32))
+    odd = _fma32(partner, sin_t, (y * cos_t).astype(np.float32))
+    return np.where(dim % 2 == 0, even, odd).astype(np.float32)
+
+
+def scatter_index(pos: int, n: int, head_dim: int, pos_scale: int, stride_head: int,
+                  stride_dim: int) -> np.ndarray:
+    """Store-scatter element index of each output column c
+    (src/matmul/api.rs:107-116): pos * pos_scale + (c / head_dim) *
+    stride_head + (c % head_dim) * stride_dim."""
+    c = np.arange(n, dtype=np.int64)
+    return pos * pos_scale + (c // head_dim) * stride_head + (c % head_dim) * stride_dim
+
+
+def store_scatter(dst, y, pos: int, head_dim: int, pos_scale: int, stride_head: int,
+                  stride_dim: int, f16: bool = False) -> np.ndarray:
+    """dst with the row y scattered in; an f16 destination holds the
+    RNE-rounded values (returned widened to f32)."""
+    out = np.array(dst, dtype=np.float32).reshape(-1).copy()
+    v = np.asarray(y, dtype=np.float32).reshape(-1)
+    if f16:
+        v = round_via_f16(v)
+    out[scatter_index(pos, v.size, head_dim, pos_scale, stride_head, stride_dim)] = v
+    return out

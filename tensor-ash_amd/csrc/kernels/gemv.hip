@@ -156,7 +156,8 @@ struct Gemv {
   }
 
   static TA_DEVICE void unit(const GemvArgs &p, uint32_t tile, uint32_t chunk, Smem &sm,
-                             const MlpArgs *mlp = nullptr, uint32_t layer = 0) {
+                             const MlpArgs *mlp = nullptr, uint32_t layer = 0,
+                             const GemvFusion *fu = nullptr) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t tiles = (p.n + TW - 1) / TW;
     const uint32_t k0 = chunk * p.kchunk;
@@ -288,6 +289,10 @@ struct Gemv {
         xr[j] = ok ? xr[j] : 0.0f;
       }
       issue(0, cur);
+      if constexpr (MODE == kStandalone) {
+        if (fu && fu->norm_w)
+          normalize_x(p, *fu, k0, xr, sm);
+      }
     }
 #pragma unroll
     for (int j = 0; j < XPT; ++j)
@@ -398,7 +403,10 @@ struct Gemv {
     if constexpr (MODE == kStandalone) {
       if (p.kchunks > 1 && !standalone_reduce(p, tile, chunk, tiles, part, sm))
         return;
-      epilogue(p, tile, part, sm, nullptr, 0);
+      if (fu && fu->store_mode)
+        store_epilogue(p, *fu, tile, part);
+      else
+        epilogue(p, tile, part, sm, nullptr, 0);
     } else {
       // Decode MLP: windows other than the tile's last store tagged
       // partials and finish; the last window's unit (highest workgroup
@@ -464,6 +472,85 @@ struct Gemv {
           __hip_atomic_store(mlp->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store(mlp->gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+      }
+    }
+  }
+
+  // Normed-A preamble (src/matmul/api.rs:213-222; the reference's row
+  // kernel, shaders/matmul_row_bda_kernel.glsl:212-234): each unit
+  // reduces the sum of squares of its X rows over all of K (every thread
+  // strides K, fixed-order tree over the workgroup), then scales the
+  // staged window values: x' = (x * s_m) * w[k], s_m = 1 / sqrt(sumsq / K
+  // + eps).  The whole rows are re-read per unit; they are small and
+  // L2-resident.  The X window's LDS (not yet staged) is the scratch.
+  static TA_DEVICE void normalize_x(const GemvArgs &p, const GemvFusion &f, uint32_t k0,
+                                    float (&xr)[XROWS * MR / kThreads], Smem &sm) {
+    constexpr int XPT = XROWS * MR / kThreads;
+    static_assert(XS >= kThreads, "reduction scratch");
+    const uint32_t tid = threadIdx.x;
+    __shared__ float scale[MR];
+    for (uint32_t m = 0; m < p.rows; ++m) {
+      const float *row = p.x + (uint64_t)m * p.k;
+      float ss = 0.0f;
+      for (uint32_t kk = tid; kk < p.k; kk += kThreads) {
+        const float a = row[kk];
+        ss = fmaf(a, a, ss);
+      }
+      sm.xs[tid] = ss;
+      __syncthreads();
+#pragma unroll
+      for (uint32_t step = kThreads / 2; step > 0; step >>= 1) {
+        if (tid < step)
+          sm.xs[tid] += sm.xs[tid + step];
+        __syncthreads();
+      }
+      if (tid == 0)
+        scale[m] = 1.0f / sqrtf(sm.xs[0] / (float)p.k + f.norm_eps);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+      const uint32_t i = tid + j * kThreads;
+      const uint32_t kk = i / MR, m = i % MR;
+      if (i < p.kchunk * MR && m < p.rows && k0 + kk < p.k)
+        xr[j] = (xr[j] * scale[m]) * f.norm_w[k0 + kk];
+    }
+  }
+
+  // Fused store epilogue (M = 1, plain alpha * acc; host-validated): RoPE
+  // of the interleaved (even, odd) output pairs with the reference's fma
+  // order (shaders/matmul_row_bda_kernel.glsl:163-176), then a store to Y
+  // or a scatter into the destination cache (:150-161).  Output o of the
+  // tile is thread o, so its pair partner o ^ 1 is the adjacent lane.
+  static TA_DEVICE void store_epilogue(const GemvArgs &p, const GemvFusion &f, uint32_t tile,
+                                       const float (&part)[OPT]) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t pos = f.pos_base + (f.pos_addr ? *f.pos_addr : 0u);
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+      const uint32_t o = tid + i * kThreads;
+      const uint32_t m = o / TW, c = tile * TW + o % TW;
+      const bool ok = o < OUTS && m < p.rows && c < p.n;
+      float v = p.alpha * part[i];
+      const float partner = __shfl_xor(v, 1);
+      if (!ok)
+        continue;
+      if (f.store_mode != 2) {
+        const uint32_t dim = c % f.head_dim;
+        const uint32_t angle = (pos * (f.head_dim / 2) + dim / 2) * 2;
+        const float cos_t = f.rope_table[angle], sin_t = f.rope_table[angle + 1];
+        v = (dim & 1u) == 0 ? fmaf(v, cos_t, -partner * sin_t) : fmaf(partner, sin_t, v * cos_t);
+      }
+      if (f.store_mode == 1) {
+        p.y[(uint64_t)m * p.n + c] = v;
+      } else {
+        const uint64_t idx = (uint64_t)pos * f.pos_scale +
+                             (uint64_t)(c / f.head_dim) * f.stride_head +
+                             (uint64_t)(c % f.head_dim) * f.stride_dim;
+        if (f.store_dst_f16)
+          static_cast<_Float16 *>(f.store_dst)[idx] = (_Float16)v;
+        else
+          static_cast<float *>(f.store_dst)[idx] = v;
       }
     }
   }
@@ -609,10 +696,10 @@ struct Gemv {
     }
   }
 
-  static TA_DEVICE void run(const GemvArgs &p) {
+  static TA_DEVICE void run(const GemvArgs &p, const GemvFusion &f) {
     __shared__ __attribute__((aligned(16))) Smem sm;
     const uint32_t tiles = (p.n + TW - 1) / TW;
-    unit(p, blockIdx.x % tiles, blockIdx.x / tiles, sm);
+    unit(p, blockIdx.x % tiles, blockIdx.x / tiles, sm, nullptr, 0, &f);
   }
 };
 
@@ -668,9 +755,10 @@ template <int MR> struct DecodeMlp {
 } // namespace
 
 #define TA_GEMV(NAME, MR, DUAL, TW, WF32)                                          \
-  extern "C" __global__ __launch_bounds__(kThreads) void NAME(GemvArgs p) {        \
+  extern "C" __global__ __launch_bounds__(kThreads) void NAME(GemvArgs p,          \
+                                                              GemvFusion f) {      \
     Gemv<MR, DUAL, TW, WF32, kStandalone, standalone_rows<MR>(),                  \
-         standalone_unroll<MR>()>::run(p);                                        \
+         standalone_unroll<MR>()>::run(p, f);                                     \
   }
 
 #define TA_GEMV_ROWS(PREFIX, DUAL, TW, WF32)                                       \

@@ -111,6 +111,29 @@ typedef struct GemvArgs {
   float beta;
 } GemvArgs;
 
+// Decode fusions of a standalone GEMV launch (its second kernel argument;
+// src/matmul/api.rs:107-299 semantics):
+//  * norm_w != null: RMSNorm of every X row folded in before the product,
+//    X'[m, k] = (X[m, k] * s_m) * norm_w[k], s_m = 1 / sqrt(mean_k X[m, k]^2
+//    + norm_eps);
+//  * store_mode (M = 1): 1 = RoPE-rotate the output pairs and store to Y,
+//    2 = scatter Y into store_dst, 3 = rotate then scatter (Y untouched in
+//    modes 2 and 3).  Position P = pos_base + (pos_addr ? *pos_addr : 0).
+typedef struct GemvFusion {
+  const float *norm_w;
+  float norm_eps;
+  uint32_t store_mode;
+  uint32_t store_dst_f16;
+  uint32_t head_dim;
+  uint32_t pos_base;
+  uint32_t pos_scale;
+  uint32_t stride_head;
+  uint32_t stride_dim;
+  const uint32_t *pos_addr;
+  const float *rope_table; // [T_max, head_dim / 2, 2] (cos, sin)
+  void *store_dst;         // f32 or f16 elements
+} GemvFusion;
+
 // Persistent decode SwiGLU MLP chain in one launch: `layers` MLPs, layer
 // l+1 reading layer l's output y as its x.  In a layer, `a` is the dual
 // gate/up GEMV (producer of h = act(x Wg) * (x Wu)) and `b` the down-proj

@@ -140,6 +140,51 @@ std::vector<MatmulOp> checked_ops_v2(const ta_executor &e, const ta_matmul_op_v2
   return out;
 }
 
+std::vector<MatmulOp> checked_ops_v3(const ta_executor &e, const ta_matmul_op_v3 *ops, size_t n,
+                                     const std::string &op) {
+  if (n > 0 && !ops)
+    fail(op + ": ops is null");
+  std::vector<MatmulOp> out;
+  for (size_t i = 0; i < n; ++i) {
+    const std::string where = op + ": op " + std::to_string(i);
+    const ta_matmul_op_v3 &v = ops[i];
+    std::vector<MatmulOp> base = checked_ops_v2(e, &v.v2, 1, where);
+    MatmulOp o = base[0];
+    if (v.norm_weight)
+      o.normed_a = NormedA{checked_tensor(e, v.norm_weight, where, "norm_weight"), v.norm_eps};
+    if (v.store.reserved)
+      fail(where + ": store.reserved must be zero");
+    MatmulStoreDesc d;
+    d.head_dim = v.store.head_dim;
+    d.pos_base = v.store.pos_base;
+    d.pos_scale = v.store.pos_scale;
+    d.stride_head = v.store.stride_head;
+    d.stride_dim = v.store.stride_dim;
+    d.pos_addr = v.store.pos_addr;
+    switch (v.store_kind) {
+    case TA_STORE_NONE:
+      if (v.store_table || v.store_dst)
+        fail(where + ": store tensors are set but store_kind is 0 (none)");
+      break;
+    case TA_STORE_ROPE:
+      o = o.with_store_rope(*checked_tensor(e, v.store_table, where, "store_table"), d);
+      break;
+    case TA_STORE_SCATTER:
+      o = o.with_store_scatter(*checked_tensor(e, v.store_dst, where, "store_dst"), d);
+      break;
+    case TA_STORE_ROPE_SCATTER:
+      o = o.with_store_rope_scatter(*checked_tensor(e, v.store_table, where, "store_table"),
+                                    *checked_tensor(e, v.store_dst, where, "store_dst"), d);
+      break;
+    default:
+      fail(where + ": store_kind " + std::to_string(v.store_kind) +
+           " is invalid (0=none 1=rope 2=scatter 3=rope_scatter)");
+    }
+    out.push_back(o);
+  }
+  return out;
+}
+
 // capi/src/api/matmul.rs:86-103.
 void write_stats(ta_run_stats *out, const RunStats &s) {
   if (!out)
@@ -265,6 +310,9 @@ uint64_t ta_tensor_size_bytes(const ta_tensor *t) { return t ? t->tensor.size_by
 uint32_t ta_tensor_is_f16(const ta_tensor *t) {
   return t && t->tensor.dtype() == DType::F16 ? 1u : 0u;
 }
+uint64_t ta_tensor_device_address(const ta_tensor *t) {
+  return t ? (uint64_t)(uintptr_t)t->tensor.device_ptr() : 0;
+}
 
 int ta_upload(const ta_executor *exec, const ta_tensor *dst, const float *src, size_t len) {
   return ffi_status([&] {
@@ -342,6 +390,23 @@ int ta_run_ops_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops, size_t n_
   });
 }
 
+int ta_run_ops_v3(const ta_executor *exec, const ta_matmul_op_v3 *ops, size_t n_ops,
+                  ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_ops_v3: exec is null");
+    write_stats(stats, e.exec->run_ops(checked_ops_v3(e, ops, n_ops, "ta_run_ops_v3")));
+  });
+}
+
+int ta_run_op_graph_v3(const ta_executor *exec, const ta_matmul_op_v3 *ops, size_t n_ops,
+                       ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_op_graph_v3: exec is null");
+    write_stats(stats,
+                e.exec->run_op_graph(checked_ops_v3(e, ops, n_ops, "ta_run_op_graph_v3")));
+  });
+}
+
 int ta_run_op_graph_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops, size_t n_ops,
                        ta_run_stats *stats) {
   return ffi_status([&] {
@@ -413,6 +478,16 @@ ta_prepared *ta_prepared_create_v2(const ta_executor *exec, const ta_matmul_op_v
         return checked_ops_v2(e, static_cast<const ta_matmul_op_v2 *>(o), n, fn);
       },
       ops, n_ops, as_graph, "ta_prepared_create_v2");
+}
+
+ta_prepared *ta_prepared_create_v3(const ta_executor *exec, const ta_matmul_op_v3 *ops,
+                                   size_t n_ops, uint32_t as_graph) {
+  return make_prepared(
+      exec,
+      [](const ta_executor &e, const void *o, size_t n, const std::string &fn) {
+        return checked_ops_v3(e, static_cast<const ta_matmul_op_v3 *>(o), n, fn);
+      },
+      ops, n_ops, as_graph, "ta_prepared_create_v3");
 }
 
 int ta_prepared_run(ta_prepared *prepared, ta_run_stats *stats) {

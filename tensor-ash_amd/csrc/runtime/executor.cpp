@@ -203,6 +203,12 @@ struct ExecutorImpl {
       validate_tensor(op.epilogue.bias, "bias");
     if (op.epilogue.binary.kind != EpilogueBinary::Kind::None)
       validate_tensor(op.epilogue.binary.d, "D");
+    if (op.normed_a)
+      validate_tensor(op.normed_a->weight, "normed-A weight");
+    if (op.store.table)
+      validate_tensor(op.store.table, "store rope table");
+    if (op.store.dst)
+      validate_tensor(op.store.dst, "store destination");
   }
 
   // ---- routing (src/pipeline/mod.rs:259-288, executor/mod.rs:179-315) ----
@@ -235,6 +241,27 @@ struct ExecutorImpl {
     return plan;
   }
 
+  // Auto routes whose kernel cannot honour an op's decode fusions fall
+  // back onto the heuristic pick when that one can (src/executor/mod.rs:
+  // 259-315, demote_for_op); explicit selections keep their loud failure
+  // at record time.
+  OpPlan plan_op(const MatmulOp &op, const ResolvedMatmul &d, bool splitk_eligible) const {
+    OpPlan plan = plan_matmul(d, splitk_eligible && !op.has_decode_fusion());
+    if (op.has_decode_fusion() && selection.is_auto() && !fusions_fit(op, plan.kernel)) {
+      const size_t h = heuristic_kernel_index(ctx->cu_count(), d.batch, d.m, d.n, d.k, d.b_f16,
+                                              d.packed_b, d.a_f16);
+      if (fusions_fit(op, h)) {
+        plan.kernel = h;
+        plan.splitk2.reset();
+      }
+    }
+    return plan;
+  }
+  static bool fusions_fit(const MatmulOp &op, size_t kernel) {
+    const KernelSpec &s = KERNEL_SPECS[kernel];
+    return (!op.normed_a || s.supports_normed_a()) && (op.store.is_none() || s.supports_store());
+  }
+
   OpPlan plan_matmul(const ResolvedMatmul &d, bool splitk_eligible) const {
     if (d.packed_b) {
       OpPlan p;
@@ -255,9 +282,9 @@ struct ExecutorImpl {
 
   // ---- launches ----
   void launch(const std::string &symbol, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t threads,
-              void *args, hipStream_t stream) const {
+              void *args, hipStream_t stream, void *args2 = nullptr) const {
     hipFunction_t f = static_cast<hipFunction_t>(ctx->function(symbol));
-    void *params[] = {args};
+    void *params[] = {args, args2};
     hip_check(hipModuleLaunchKernel(f, gx, gy, gz, threads, 1, 1, 0, stream, params, nullptr),
               ("launch " + symbol).c_str());
   }
@@ -397,8 +424,31 @@ struct ExecutorImpl {
       a.partial = static_cast<float *>(scratch.partial);
       a.counters = scratch.counters;
     }
+    GemvFusion fu{};
+    if (op.normed_a) {
+      fu.norm_w = static_cast<const float *>(op.normed_a->weight->device_ptr());
+      fu.norm_eps = op.normed_a->eps;
+    }
+    if (!op.store.is_none()) {
+      if (dual)
+        fail("internal: store epilogue on a dual GEMV launch");
+      const MatmulStoreDesc &sd = op.store.desc;
+      fu.store_mode = op.store.mode();
+      fu.head_dim = sd.head_dim;
+      fu.pos_base = sd.pos_base;
+      fu.pos_scale = sd.pos_scale;
+      fu.stride_head = sd.stride_head;
+      fu.stride_dim = sd.stride_dim;
+      fu.pos_addr = reinterpret_cast<const uint32_t *>(sd.pos_addr);
+      if (op.store.table)
+        fu.rope_table = static_cast<const float *>(op.store.table->device_ptr());
+      if (op.store.dst) {
+        fu.store_dst = op.store.dst->device_ptr();
+        fu.store_dst_f16 = op.store.dst->dtype() == DType::F16 ? 1u : 0u;
+      }
+    }
     std::string sym = std::string(s.symbol) + (dual ? "_dual" : "") + "_m" + std::to_string(g.mr);
-    launch(sym, g.tiles * g.kchunks, 1, 1, 256, &a, stream);
+    launch(sym, g.tiles * g.kchunks, 1, 1, 256, &a, stream, &fu);
   }
 
   // Dual SwiGLU fusion in a dependent graph: op i = x @ Wu (plain) and op
@@ -409,7 +459,8 @@ struct ExecutorImpl {
     if (pu.kernel != pg.kernel || !KERNEL_SPECS[pu.kernel].weights_f16() ||
         !KERNEL_SPECS[pu.kernel].is_gemv() || pu.splitk2 || pg.splitk2)
       return false;
-    if (!up.epilogue.is_none() || up.call.accumulate || gate.call.accumulate)
+    if (!up.epilogue.is_none() || up.call.accumulate || gate.call.accumulate ||
+        up.has_decode_fusion() || gate.has_decode_fusion())
       return false;
     if (gate.epilogue.binary.kind != EpilogueBinary::Kind::Mul ||
         gate.epilogue.binary.d->buffer_id() != up.call.c->buffer_id())
@@ -505,6 +556,21 @@ struct ExecutorImpl {
     return true;
   }
 
+  // src/executor/recording.rs:204-235: a route without the fused
+  // normed-A / store body fails instead of silently skipping it.
+  static void check_fusions(const KernelSpec &s, const MatmulOp &op, const ResolvedMatmul &d) {
+    if (op.normed_a && !s.supports_normed_a())
+      fail(std::string("kernel '") + s.name +
+           "' does not implement the fused normed-A GEMV (decode GEMV kernels only; normed-A "
+           "requires a decode GEMV route with M <= 8 and batch 1, got M=" +
+           std::to_string(d.m) + ")");
+    if (!op.store.is_none() && !s.supports_store())
+      fail(std::string("kernel '") + s.name +
+           "' does not implement the fused store epilogue (f16-weight decode GEMV kernels "
+           "only; store requires an M=1 f16-weights GEMV route, got M=" +
+           std::to_string(d.m) + ")");
+  }
+
   void check_supported(const KernelSpec &s, const ResolvedMatmul &d) const {
     if (!kernel_supports(s, d)) {
       std::ostringstream o;
@@ -572,6 +638,8 @@ struct ExecutorImpl {
       return false;
     // Whole K windows in both phases (the kernel does not mask rows).
     if (gate.call.a->shape().back() % kMlpRowsA != 0 || down.call.a->shape().back() % kMlpRowsB != 0)
+      return false;
+    if (down.has_decode_fusion())
       return false;
     if (!down.packed_b || down.call.a->buffer_id() != gate.call.c->buffer_id() ||
         down.call.a->shape() != gate.call.c->shape())
@@ -681,6 +749,7 @@ struct ExecutorImpl {
       }
       const KernelSpec &s = KERNEL_SPECS[p.kernel];
       check_supported(s, res[i]);
+      check_fusions(s, ops[i], res[i]);
       if (s.is_gemv())
         launch_gemv(s, res[i], ops[i], p.role == 2 ? &ops[i - 1] : nullptr, scratch, stream);
       else
@@ -853,7 +922,7 @@ struct ExecutorImpl {
     const uint64_t flops = total_flops(res);
 
     if (config.tune && ops.size() == 1 && !ops[0].call.accumulate && ops[0].epilogue.is_none() &&
-        !res[0].a_f16 && !res[0].packed_b) {
+        !ops[0].has_decode_fusion() && !res[0].a_f16 && !res[0].packed_b) {
       const ResolvedMatmul &d = res[0];
       const TuneKey key{d.batch, d.m, d.n, d.k, d.b_f16};
       if (!is_tuned(key)) {
@@ -870,7 +939,7 @@ struct ExecutorImpl {
     for (size_t i = 0; i < ops.size(); ++i) {
       const bool eligible = !ops[i].call.accumulate && ops[i].epilogue.is_none() &&
                             (graph || ops.size() == 1);
-      plans.push_back(plan_matmul(res[i], eligible));
+      plans.push_back(plan_op(ops[i], res[i], eligible));
     }
     if (graph)
       mark_fusions(ops, res, plans);
@@ -932,8 +1001,8 @@ struct ExecutorImpl {
     // Data-parallel routes only, like the reference: split-K would need
     // its scratch baked into the graph for the handle's lifetime.
     std::vector<OpPlan> plans;
-    for (const auto &d : res)
-      plans.push_back(plan_matmul(d, false));
+    for (size_t i = 0; i < res.size(); ++i)
+      plans.push_back(plan_op(ops[i], res[i], false));
     if (graph)
       mark_fusions(ops, res, plans);
     for (size_t i = 0; i < ops.size(); ++i)

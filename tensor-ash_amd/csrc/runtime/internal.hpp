@@ -47,6 +47,8 @@ struct ResolvedMatmul {
   static ResolvedMatmul from_op(const MatmulOp &op);
   void validate_bias_shape(const std::vector<uint32_t> &shape) const;
   void validate_epilogue(const MatmulOp &op) const;
+  void validate_normed_a(const MatmulOp &op) const;
+  void validate_store(const MatmulOp &op) const;
   bool operator==(const ResolvedMatmul &o) const;
 };
 uint64_t total_flops(const std::vector<ResolvedMatmul> &resolved);

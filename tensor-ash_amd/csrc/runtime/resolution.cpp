@@ -164,11 +164,80 @@ ResolvedMatmul ResolvedMatmul::from_op(const MatmulOp &op) {
     if (r.n % 32 != 0)
       fail("packed-B GEMV requires N to be a multiple of 32 (got " + std::to_string(r.n) + ")");
   }
-  if (r.a_f16 && !op.epilogue.is_none())
+  if (r.a_f16 && (!op.epilogue.is_none() || op.has_decode_fusion()))
     fail("matmul with f16 A storage cannot fuse epilogues, normed-A, or store ops "
          "(the coopmat route has no fused specializations)");
   r.validate_epilogue(op);
+  r.validate_normed_a(op);
+  r.validate_store(op);
   return r;
+}
+
+// resolution.rs:214-241: the normed-A weight rides the bias slot and eps
+// the beta slot of the reference's push constants, hence the exclusions
+// (kept: they are the op's contract).
+void ResolvedMatmul::validate_normed_a(const MatmulOp &op) const {
+  if (!op.normed_a)
+    return;
+  const Tensor *w = op.normed_a->weight;
+  if (!w)
+    fail("normed-A weight tensor is null");
+  if (w->dtype() != DType::F32)
+    fail("normed-A weight must be f32 storage");
+  if (w->len() != k)
+    fail("normed-A weight length " + std::to_string(w->len()) + " must equal K = " +
+         std::to_string(k));
+  if (op.epilogue.bias)
+    fail("normed-A cannot combine with an epilogue bias (both use the bias slot)");
+  if (op.epilogue.binary.kind == EpilogueBinary::Kind::AddScaled)
+    fail("normed-A cannot combine with the AddScaled epilogue (both use beta)");
+}
+
+// resolution.rs:243-316.
+void ResolvedMatmul::validate_store(const MatmulOp &op) const {
+  if (op.store.is_none())
+    return;
+  if (m != 1 || batch != 1)
+    fail("fused store epilogue requires M == 1 and batch == 1 (got M=" + std::to_string(m) +
+         ", batch=" + std::to_string(batch) + ")");
+  if (!b_f16)
+    fail("fused store epilogue requires f16 weights (f16w row-GEMV routes only)");
+  if (op.call.accumulate)
+    fail("fused store epilogue cannot combine with accumulate");
+  if (!op.epilogue.is_none())
+    fail("fused store epilogue cannot combine with a fused epilogue");
+  const MatmulStoreDesc &d = op.store.desc;
+  if (d.head_dim == 0 || d.head_dim % 2 != 0 || n % d.head_dim != 0)
+    fail("store head_dim " + std::to_string(d.head_dim) + " must be even and divide N = " +
+         std::to_string(n));
+  const bool rope = op.store.kind == MatmulStore::Kind::Rope ||
+                    op.store.kind == MatmulStore::Kind::RopeScatter;
+  const bool scatter = op.store.kind == MatmulStore::Kind::Scatter ||
+                       op.store.kind == MatmulStore::Kind::RopeScatter;
+  if (rope) {
+    const Tensor *t = op.store.table;
+    if (!t)
+      fail("store rope table tensor is null");
+    if (t->dtype() != DType::F32)
+      fail("store rope table must be f32 storage");
+    const uint64_t needed = ((uint64_t)d.pos_base + 1) * d.head_dim;
+    if (t->len() < needed)
+      fail("store rope table len " + std::to_string(t->len()) + " does not cover pos_base " +
+           std::to_string(d.pos_base) + " (needs " + std::to_string(needed) + ")");
+  }
+  if (scatter) {
+    const Tensor *dst = op.store.dst;
+    if (!dst)
+      fail("store destination tensor is null");
+    const uint64_t heads = n / d.head_dim;
+    const uint64_t last = (uint64_t)d.pos_base * d.pos_scale +
+                          (heads - 1) * (uint64_t)d.stride_head +
+                          (uint64_t)(d.head_dim - 1) * d.stride_dim;
+    if (last >= dst->len())
+      fail("store destination access " + std::to_string(last) + " out of bounds for len " +
+           std::to_string(dst->len()) + " (pos_base " + std::to_string(d.pos_base) + ", N " +
+           std::to_string(n) + ", head_dim " + std::to_string(d.head_dim) + ")");
+  }
 }
 
 // resolution.rs:318-351.

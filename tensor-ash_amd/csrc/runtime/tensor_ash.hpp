@@ -98,10 +98,46 @@ struct Epilogue {
   }
 };
 
-// src/matmul/api.rs:213-299 (normed_a / store are not on this path).
+// src/matmul/api.rs:107-133: geometry of the fused store epilogue.  The
+// position is P = pos_base + *pos_addr (pos_addr: device address of a u32
+// cell, 0 = none); output column c scatters to element
+// P * pos_scale + (c / head_dim) * stride_head + (c % head_dim) * stride_dim;
+// RoPE rotates the interleaved (even, odd) pairs of each head by the
+// (cos, sin) at row P * head_dim/2 + (c % head_dim)/2 of a
+// [T_max, head_dim/2, 2] f32 table.
+struct MatmulStoreDesc {
+  uint32_t head_dim = 0;
+  uint32_t pos_base = 0;
+  uint32_t pos_scale = 0;
+  uint32_t stride_head = 0;
+  uint32_t stride_dim = 0;
+  uint64_t pos_addr = 0;
+};
+
+// src/matmul/api.rs:135-206: fused store-time destination of an M = 1
+// f16-weights decode GEMV (codes are the reference's STORE_MODE values).
+struct MatmulStore {
+  enum class Kind : uint32_t { None = 0, Rope = 1, Scatter = 2, RopeScatter = 3 };
+  Kind kind = Kind::None;
+  const Tensor *table = nullptr; // Rope, RopeScatter
+  const Tensor *dst = nullptr;   // Scatter, RopeScatter (f32 or f16)
+  MatmulStoreDesc desc;
+  bool is_none() const { return kind == Kind::None; }
+  uint32_t mode() const { return (uint32_t)kind; }
+};
+
+// src/matmul/api.rs:213-299.  normed_a = (weight, eps): C = rms_norm(A,
+// weight, eps) @ B, on the decode GEMV routes only.
+struct NormedA {
+  const Tensor *weight = nullptr;
+  float eps = 0.0f;
+};
+
 struct MatmulOp {
   MatmulCall call;
   Epilogue epilogue;
+  std::optional<NormedA> normed_a;
+  MatmulStore store;
   bool packed_b = false;
   MatmulOp() = default;
   explicit MatmulOp(const MatmulCall &c) : call(c) {}
@@ -114,6 +150,28 @@ struct MatmulOp {
     o.packed_b = true;
     return o;
   }
+  MatmulOp with_normed_a(const Tensor &weight, float eps) const {
+    MatmulOp o = *this;
+    o.normed_a = NormedA{&weight, eps};
+    return o;
+  }
+  MatmulOp with_store_rope(const Tensor &table, const MatmulStoreDesc &desc) const {
+    MatmulOp o = *this;
+    o.store = MatmulStore{MatmulStore::Kind::Rope, &table, nullptr, desc};
+    return o;
+  }
+  MatmulOp with_store_scatter(const Tensor &dst, const MatmulStoreDesc &desc) const {
+    MatmulOp o = *this;
+    o.store = MatmulStore{MatmulStore::Kind::Scatter, nullptr, &dst, desc};
+    return o;
+  }
+  MatmulOp with_store_rope_scatter(const Tensor &table, const Tensor &dst,
+                                   const MatmulStoreDesc &desc) const {
+    MatmulOp o = *this;
+    o.store = MatmulStore{MatmulStore::Kind::RopeScatter, &table, &dst, desc};
+    return o;
+  }
+  bool has_decode_fusion() const { return normed_a.has_value() || !store.is_none(); }
 };
 
 // src/matmul/api.rs:311-353.
@@ -172,6 +230,10 @@ struct KernelSpec {
            kind == KernelKind::GemvF32Row;
   }
   bool packed() const { return kind == KernelKind::GemvF16Packed; }
+  // src/pipeline/runtime.rs:62-76: the decode GEMVs implement the fused
+  // normed-A preamble; the f16-weight ones also the store epilogue.
+  bool supports_normed_a() const { return is_gemv(); }
+  bool supports_store() const { return is_gemv() && weights_f16(); }
 };
 extern const KernelSpec KERNEL_SPECS[];
 extern const size_t KERNEL_SPECS_LEN;

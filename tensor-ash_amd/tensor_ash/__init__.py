@@ -58,6 +58,18 @@ class _OpV2(C.Structure):
     _fields_ = [("base", _Op), ("packed_b", C.c_uint32), ("reserved", C.c_uint32 * 3)]
 
 
+class _StoreDesc(C.Structure):
+    _fields_ = [("head_dim", C.c_uint32), ("pos_base", C.c_uint32), ("pos_scale", C.c_uint32),
+                ("stride_head", C.c_uint32), ("stride_dim", C.c_uint32), ("reserved", C.c_uint32),
+                ("pos_addr", C.c_uint64)]
+
+
+class _OpV3(C.Structure):
+    _fields_ = [("v2", _OpV2), ("norm_weight", C.c_void_p), ("norm_eps", C.c_float),
+                ("store_kind", C.c_uint32), ("store_table", C.c_void_p), ("store_dst", C.c_void_p),
+                ("store", _StoreDesc)]
+
+
 class _DispatchInfo(C.Structure):
     _fields_ = [("kernel", C.c_char_p), ("tile", C.c_uint32 * 3), ("has_split_k2", C.c_uint32),
                 ("split_k2_splits", C.c_uint32)]
@@ -101,6 +113,10 @@ _sig("ta_run_op_graph_v2", C.c_int, P, C.POINTER(_OpV2), sz, C.POINTER(RunStats)
 _sig("ta_matmul_split_k2", C.c_int, P, P, P, P, f32, u32, C.POINTER(RunStats))
 _sig("ta_prepared_create", P, P, C.POINTER(_Op), sz, u32)
 _sig("ta_prepared_create_v2", P, P, C.POINTER(_OpV2), sz, u32)
+_sig("ta_run_ops_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
+_sig("ta_run_op_graph_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
+_sig("ta_prepared_create_v3", P, P, C.POINTER(_OpV3), sz, u32)
+_sig("ta_tensor_device_address", u64, P)
 _sig("ta_prepared_run", C.c_int, P, C.POINTER(RunStats))
 _sig("ta_prepared_submit", C.c_int, P)
 _sig("ta_prepared_wait", C.c_int, P, C.POINTER(RunStats))
@@ -196,6 +212,11 @@ class Tensor:
     def size_bytes(self) -> int:
         return int(_lib.ta_tensor_size_bytes(self._h))
 
+    @property
+    def device_address(self) -> int:
+        """Device address of the allocation (for MatmulStoreDesc.pos_addr)."""
+        return int(_lib.ta_tensor_device_address(self._h))
+
     def close(self):
         if self._h:
             _lib.ta_tensor_destroy(self._h)
@@ -218,9 +239,35 @@ class Epilogue:
     beta: float = 0.0
 
 
+STORE_NONE, STORE_ROPE, STORE_SCATTER, STORE_ROPE_SCATTER = 0, 1, 2, 3
+
+
+@dataclass
+class MatmulStoreDesc:
+    """src/matmul/api.rs:117-133.  pos_addr: device address of a u32 cell
+    (Tensor.device_address), 0 = none."""
+    head_dim: int
+    pos_base: int = 0
+    pos_scale: int = 0
+    stride_head: int = 0
+    stride_dim: int = 0
+    pos_addr: int = 0
+
+
+@dataclass
+class MatmulStore:
+    """src/matmul/api.rs:135-206: kind STORE_ROPE (table), STORE_SCATTER
+    (dst) or STORE_ROPE_SCATTER (table, dst)."""
+    kind: int
+    desc: MatmulStoreDesc
+    table: Optional[Tensor] = None
+    dst: Optional[Tensor] = None
+
+
 @dataclass
 class MatmulOp:
-    """src/matmul/api.rs:213-299 (with_packed_b -> packed_b=True)."""
+    """src/matmul/api.rs:213-299: with_packed_b -> packed_b=True,
+    with_normed_a(w, eps) -> normed_a=(w, eps), with_store_* -> store."""
     a: Tensor
     b: Tensor
     c: Tensor
@@ -228,6 +275,8 @@ class MatmulOp:
     accumulate: bool = False
     epilogue: Epilogue = field(default_factory=Epilogue)
     packed_b: bool = False
+    normed_a: Optional[tuple] = None
+    store: Optional[MatmulStore] = None
 
     def _raw(self) -> _Op:
         e = self.epilogue
@@ -235,18 +284,35 @@ class MatmulOp:
                    _Epilogue(e.bias.handle if e.bias else None, e.activation, e.binary,
                              e.d.handle if e.d else None, e.beta))
 
+    def _raw_v3(self) -> _OpV3:
+        op = _OpV3(_OpV2(self._raw(), int(self.packed_b)))
+        if self.normed_a is not None:
+            op.norm_weight = self.normed_a[0].handle
+            op.norm_eps = float(self.normed_a[1])
+        if self.store is not None:
+            st, d = self.store, self.store.desc
+            op.store_kind = st.kind
+            op.store_table = st.table.handle if st.table else None
+            op.store_dst = st.dst.handle if st.dst else None
+            op.store = _StoreDesc(d.head_dim, d.pos_base, d.pos_scale, d.stride_head, d.stride_dim, 0,
+                                  d.pos_addr)
+        return op
+
 
 def _ops_array(ops: Sequence[MatmulOp]):
+    """(array, version): the narrowest C struct that carries every op."""
+    if any(o.normed_a is not None or o.store is not None for o in ops):
+        return (_OpV3 * len(ops))(*[o._raw_v3() for o in ops]), 3
     if any(o.packed_b for o in ops):
         arr = (_OpV2 * len(ops))(*[_OpV2(o._raw(), int(o.packed_b)) for o in ops])
-        return arr, True
-    return (_Op * len(ops))(*[o._raw() for o in ops]), False
+        return arr, 2
+    return (_Op * len(ops))(*[o._raw() for o in ops]), 1
 
 
 class Prepared:
     def __init__(self, exec_: "Executor", ops: Sequence[MatmulOp], as_graph: bool):
-        arr, v2 = _ops_array(ops)
-        fn = _lib.ta_prepared_create_v2 if v2 else _lib.ta_prepared_create
+        arr, ver = _ops_array(ops)
+        fn = {1: _lib.ta_prepared_create, 2: _lib.ta_prepared_create_v2, 3: _lib.ta_prepared_create_v3}[ver]
         self._h = _checkp(fn(exec_.handle, arr, len(ops), int(as_graph)))
         self._keep = (exec_, list(ops))
 
@@ -325,16 +391,16 @@ class Executor:
         return st
 
     def run_ops(self, ops: Sequence[MatmulOp]) -> RunStats:
-        arr, v2 = _ops_array(ops)
+        arr, ver = _ops_array(ops)
         st = RunStats()
-        fn = _lib.ta_run_ops_v2 if v2 else _lib.ta_run_ops
+        fn = {1: _lib.ta_run_ops, 2: _lib.ta_run_ops_v2, 3: _lib.ta_run_ops_v3}[ver]
         _check(fn(self._h, arr, len(ops), C.byref(st)))
         return st
 
     def run_op_graph(self, ops: Sequence[MatmulOp]) -> RunStats:
-        arr, v2 = _ops_array(ops)
+        arr, ver = _ops_array(ops)
         st = RunStats()
-        fn = _lib.ta_run_op_graph_v2 if v2 else _lib.ta_run_op_graph
+        fn = {1: _lib.ta_run_op_graph, 2: _lib.ta_run_op_graph_v2, 3: _lib.ta_run_op_graph_v3}[ver]
         _check(fn(self._h, arr, len(ops), C.byref(st)))
         return st
 

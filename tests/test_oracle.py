@@ -259,3 +259,65 @@ def test_fill_normal_distribution(oracle):
     assert abs(v.mean()) < 2e-4 and abs(v.std() - 0.02) < 2e-4
     assert scipy.stats.kstest(v / 0.02, "norm").pvalue > 1e-3
     assert np.array_equal(oracle.fill_normal(9, 5, 1.0), oracle.fill_normal(9, 5, 1.0))
+
+
+# ---------------------------------------------------------------- decode fusions
+
+def test_rms_norm_matches_torch_and_closed_form(oracle):
+    """rms_norm_rows pinned against torch's rms_norm in float64 (same
+    formula, independent implementation) and against the closed form of a
+    constant row: x = c gives w * c / sqrt(c^2 + eps)."""
+    import torch
+    m, k, eps = 3, 203, 1e-5
+    x = oracle.fill_det(m * k, 70)
+    w = oracle.fill_det(k, 71)
+    got = oracle.rms_norm_rows(x, w, m, k, eps).reshape(m, k)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x.reshape(m, k)).double(), (k,),
+                                       torch.from_numpy(w).double(), eps=float(np.float32(eps)))
+    assert np.allclose(got, ref.numpy(), rtol=2e-7, atol=1e-7)
+    c = np.float32(0.75)
+    got = oracle.rms_norm_rows(np.full(k, c, np.float32), w, 1, k, eps)
+    want = (w.astype(np.float64) * c / math.sqrt(float(c) ** 2 + float(np.float32(eps)))).astype(np.float32)
+    assert np.array_equal(got, want)
+    # A scaled row normalizes to the same values (up to eps).
+    big = oracle.rms_norm_rows(x[:k] * 1000.0, w, 1, k, 0.0)
+    assert np.allclose(big, oracle.rms_norm_rows(x[:k], w, 1, k, 0.0), rtol=1e-6, atol=1e-7)
+
+
+def test_rope_pairs_is_a_rotation(oracle):
+    """rope_pairs pinned against complex multiplication: each (even, odd)
+    pair of head h at position p is multiplied by cos + i sin of its own
+    angle; the identity angle leaves the row bit-exact and a quarter turn
+    maps (a, b) to (-b, a) exactly."""
+    hd, t_max, pos, n = 8, 6, 4, 32
+    y = oracle.fill_det(n, 72)
+    theta = np.linspace(0.1, 2.9, t_max * hd // 2).reshape(t_max, hd // 2)
+    table = np.stack([np.cos(theta), np.sin(theta)], axis=-1).astype(np.float32)
+    got = oracle.rope_pairs(y, table, pos, hd)
+    z = y[0::2].astype(np.float64) + 1j * y[1::2].astype(np.float64)
+    ang = table[pos, (np.arange(n // 2) % (hd // 2))].astype(np.float64)
+    rot = z * (ang[:, 0] + 1j * ang[:, 1])
+    assert np.allclose(got[0::2], rot.real, atol=1e-6) and np.allclose(got[1::2], rot.imag, atol=1e-6)
+    ident = np.tile(np.array([1.0, 0.0], np.float32), t_max * hd // 2)
+    assert np.array_equal(oracle.rope_pairs(y, ident, pos, hd), y)
+    quarter = np.tile(np.array([0.0, 1.0], np.float32), t_max * hd // 2)
+    q = oracle.rope_pairs(y, quarter, pos, hd)
+    assert np.array_equal(q[0::2], -y[1::2]) and np.array_equal(q[1::2], y[0::2])
+
+
+def test_scatter_index_matches_cache_layouts(oracle):
+    """scatter_index pinned by the two KV layouts the reference scatters
+    into (src/matmul/api.rs:160-168): V cache [H, T_max, dh] (pos_scale dh,
+    stride_head T_max*dh, stride_dim 1) and Kt cache [H, dh, T_max]
+    (pos_scale 1, stride_head dh*T_max, stride_dim T_max); placing the row
+    and reading the cache back through numpy indexing recovers it."""
+    h, dh, t_max, pos = 4, 8, 10, 7
+    y = oracle.fill_det(h * dh, 73)
+    v_cache = oracle.store_scatter(np.zeros(h * t_max * dh), y, pos, dh, dh, t_max * dh, 1)
+    assert np.array_equal(v_cache.reshape(h, t_max, dh)[:, pos, :].reshape(-1), y)
+    assert np.count_nonzero(v_cache) == np.count_nonzero(y)
+    kt_cache = oracle.store_scatter(np.zeros(h * dh * t_max), y, pos, dh, 1, dh * t_max, t_max)
+    assert np.array_equal(kt_cache.reshape(h, dh, t_max)[:, :, pos].reshape(-1), y)
+    f16 = oracle.store_scatter(np.zeros(h * t_max * dh), y, pos, dh, dh, t_max * dh, 1, f16=True)
+    assert np.array_equal(f16.reshape(h, t_max, dh)[:, pos, :].reshape(-1),
+                          y.astype(np.float16).astype(np.float32))
