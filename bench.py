@@ -6,7 +6,9 @@ HBM).  One step = one `ta_run_ops` call of that fused op.  The same JSON
 line carries, under "secondary", the decode SwiGLU MLP GEMVs (config 3,
 HBM GB/s with weight copies rotated past the 256 MB last-level cache),
 the batched GELU GEMM (config 2a), the deterministic split-K shapes
-(config 4) and the TinyLlama-shaped prefill GEMMs (config 5).
+(config 4), the TinyLlama-shaped prefill GEMMs (config 5) and, for
+reference only, the vendor library (hipBLASLt through torch.matmul) on the
+headline and prefill shapes.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 
@@ -204,6 +206,47 @@ def prefill_layer(ta, ex, iters=10):
     return out
 
 
+def vendor_reference(hl_inputs, iters=20):
+    """The vendor library on the same shapes, for reference only (not part
+    of the product path; the role of the reference's
+    benchmarks/cublas_bench/cublas_bench.cu):
+    torch's matmul, which is hipBLASLt on ROCm, timed with torch events on
+    torch's stream.  fp32 runs full-precision FP32 (no TF32 on this path);
+    the f16 rows are f16 x f16 -> f16, the semantics of this build's a16
+    route, not of its f16w route (f32 activations)."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        return statistics.median(ts)
+
+    out = {"library": "hipBLASLt via torch.matmul " + torch.__version__}
+    ha, hb = hl_inputs
+    a, b = torch.from_numpy(ha).cuda(), torch.from_numpy(hb).cuda()
+    us = timed(lambda: a @ b)
+    out["sgemm_4096^3_f32"] = dict(us=us, tflops=2.0 * 4096 ** 3 / us / 1e6)
+    g = torch.Generator(device="cuda").manual_seed(61)
+    for (m, n, k) in ((512, 2560, 2048), (512, 2048, 2048), (512, 5632, 2048), (512, 2048, 5632)):
+        x = torch.rand(m, k, device="cuda", generator=g, dtype=torch.float16) * 2 - 1
+        w = torch.randn(k, n, device="cuda", generator=g, dtype=torch.float16) * 0.02
+        us = timed(lambda: x @ w)
+        out[f"hgemm_{m}x{n}x{k}_f16"] = dict(us=us, tflops=2.0 * m * n * k / us / 1e6)
+    del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(inputs, target_s: float = 12.0):
     """The oracle's cpu_bmm (restatement of tools/test-support cpu_bmm:
     naive i-j-k, f64 accumulate) on host cores, over a bounded sample of
@@ -256,13 +299,19 @@ def main() -> int:
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (rocprof counter calibration)")
-    ap.add_argument("--sections", default="decode,gelu,splitk,prefill",
+    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,vendor",
                     help="comma list of secondary sections to run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md but not built", file=sys.stderr)
+              "multi-GPU sharding is not built", file=sys.stderr)
         return 2
+    sections = set() if args.only_headline else set(args.sections.split(","))
+    if args.calibrate_copy or "vendor" in sections:
+        # torch's ROCm wheel carries its own HIP runtime; the runtime loaded
+        # first serves the process, and torch only works on its own, so
+        # torch is imported before libtensor_ash loads.
+        import torch  # noqa: F401
     if args.calibrate_copy:
         # A plain copy kernel of known size: FETCH_SIZE / WRITE_SIZE of this
         # dispatch calibrate the counters used for the headline's traffic.
@@ -281,7 +330,6 @@ def main() -> int:
     log("headline 4096^3 f32 fused GEMM ...")
     hl = headline(ta, ex, args.steps, args.warmup)
     secondary = {}
-    sections = set() if args.only_headline else set(args.sections.split(","))
     if "decode" in sections:
         log("decode SwiGLU MLP ...")
         secondary["decode_swiglu_mlp_f16w"] = decode_mlp(ta, ex)
@@ -294,6 +342,9 @@ def main() -> int:
     if "prefill" in sections:
         log("prefill layer GEMMs ...")
         secondary["prefill_tinyllama_m512_f16w"] = prefill_layer(ta, ex)
+    if "vendor" in sections:
+        log("vendor library reference ...")
+        secondary["vendor_reference"] = vendor_reference(hl["inputs"])
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
