@@ -234,3 +234,63 @@ def store_scatter(dst, y, pos: int, head_dim: int, pos_scale: int, stride_head: 
         v = round_via_f16(v)
     out[scatter_index(pos, v.size, head_dim, pos_scale, stride_head, stride_dim)] = v
     return out
+
+
+# ---- model ops (numpy restatements; pinned in tests/test_oracle.py) ----
+
+def softmax_rows(x, rows: int, cols: int, scale: float, valid) -> np.ndarray:
+    """Row softmax of shaders/op_softmax_f32_row.comp semantics in f64:
+    row r uses its first valid(r) columns of x * scale; masked columns and
+    all-masked rows are 0.  `valid` is an int or a per-row callable."""
+    x = np.asarray(x, dtype=np.float32).reshape(rows, cols)
+    out = np.zeros((rows, cols), dtype=np.float64)
+    for r in range(rows):
+        v = min(cols, valid(r) if callable(valid) else valid)
+        if v == 0:
+            continue
+        z = (x[r, :v] * np.float32(scale)).astype(np.float64)
+        e = np.exp(z - z.max())
+        out[r, :v] = e / e.sum()
+    return out.astype(np.float32).reshape(-1)
+
+
+def layer_norm_rows(x, w, b, rows: int, cols: int, eps: float) -> np.ndarray:
+    """LayerNorm of tests/correctness/elementwise.rs:99-142: (x - mean) /
+    sqrt(var + eps) in f64 (population variance), rounded to f32, then
+    * w + b in f32."""
+    x64 = np.asarray(x, dtype=np.float32).reshape(rows, cols).astype(np.float64)
+    mean = x64.mean(axis=1, keepdims=True)
+    var = ((x64 - mean) ** 2).mean(axis=1, keepdims=True)
+    y = ((x64 - mean) / np.sqrt(var + float(np.float32(eps)))).astype(np.float32)
+    return (y * np.asarray(w, np.float32) + np.asarray(b, np.float32)).reshape(-1)
+
+
+def rope_tokens(x, table, tokens: int, heads: int, head_dim: int, rot_dim: int, pos_base: int) -> np.ndarray:
+    """RoPE of shaders/op_rope_body.glsl: pair i < rot_dim/2 of (token, head)
+    rotates by table[(pos_base + token) * rot_dim/2 + i] = (c, s):
+    r0 = fma(x0, c, -x1*s), r1 = fma(x0, s, x1*c); lanes >= rot_dim pass."""
+    x = np.asarray(x, dtype=np.float32).reshape(tokens, heads, head_dim)
+    t = np.asarray(table, dtype=np.float32).reshape(-1, rot_dim // 2, 2)
+    out = x.copy()
+    cs = t[pos_base:pos_base + tokens]           # [tokens, half, 2]
+    c, s = cs[:, None, :, 0], cs[:, None, :, 1]  # broadcast over heads
+    x0, x1 = x[:, :, 0:rot_dim:2], x[:, :, 1:rot_dim:2]
+    out[:, :, 0:rot_dim:2] = _fma32(x0, c, (-x1 * s).astype(np.float32))
+    out[:, :, 1:rot_dim:2] = _fma32(x0, s, (x1 * c).astype(np.float32))
+    return out.reshape(-1)
+
+
+def copy_strided(src, dst, extent, src_offset, src_strides, dst_offset, dst_strides,
+                 dst_f16: bool = False) -> np.ndarray:
+    """Strided 3-D copy of shaders/op_copy_strided_body.glsl: element
+    (x, y, z) < extent moves src[src_offset + x*ss0 + y*ss1 + z*ss2] to
+    dst[dst_offset + x*ds0 + y*ds1 + z*ds2]; an f16 destination holds the
+    RNE-rounded value (returned widened)."""
+    out = np.array(dst, dtype=np.float32).reshape(-1).copy()
+    s = np.asarray(src, dtype=np.float32).reshape(-1)
+    xs, ys, zs = np.meshgrid(np.arange(extent[0]), np.arange(extent[1]), np.arange(extent[2]), indexing="ij")
+    si = src_offset + xs * src_strides[0] + ys * src_strides[1] + zs * src_strides[2]
+    di = dst_offset + xs * dst_strides[0] + ys * dst_strides[1] + zs * dst_strides[2]
+    v = s[si.reshape(-1)]
+    out[di.reshape(-1)] = round_via_f16(v) if dst_f16 else v
+    return out

@@ -134,6 +134,58 @@ typedef struct GemvFusion {
   void *store_dst;         // f32 or f16 elements
 } GemvFusion;
 
+// ---- model ops (ta_softmax_rows, ta_rms_norm, ta_layer_norm, ta_rope,
+// ta_copy_strided; src/executor/elementwise/ops.rs semantics) ----
+
+// Row softmax: valid = causal ? min(cols, valid_base + row % rows_per_group
+// + 1) : min(cols, valid_base); columns >= valid store 0.
+typedef struct SoftmaxArgs {
+  const float *in;
+  float *out;
+  uint32_t rows, cols;
+  uint32_t valid_base, rows_per_group, causal;
+  float scale;
+} SoftmaxArgs;
+
+// Row norm: RMSNorm (bias null) or LayerNorm; io_f16: f16 input/output.
+typedef struct NormArgs {
+  const void *in;
+  void *out;
+  const float *weight;
+  const float *bias;
+  uint32_t rows, cols;
+  float eps;
+  uint32_t io_f16;
+} NormArgs;
+
+// RoPE over [tokens, heads, head_dim]: pairs (2i, 2i+1) of the first
+// rot_dim lanes rotate by table[(pos_base + *pos_addr + token) * rot_dim/2
+// + i] (cos, sin); the other lanes pass through.
+typedef struct RopeArgs {
+  const void *in;
+  void *out;
+  const float *table;
+  const uint32_t *pos_addr; // null: none
+  uint32_t tokens, heads, head_dim, rot_dim, pos_base;
+  uint32_t io_f16;
+} RopeArgs;
+
+// Strided 3-D copy: for (x, y, z) < extent, dst[dst_offset + *pos_addr *
+// pos_scale + x*ds0 + y*ds1 + z*ds2] = src[src_offset + x*ss0 + y*ss1 +
+// z*ss2]; f16 sides widen exactly / narrow with RNE.
+typedef struct CopyArgs {
+  const void *src;
+  void *dst;
+  const uint32_t *pos_addr; // null: none
+  uint32_t extent[3];
+  uint32_t src_offset;
+  uint32_t src_strides[3];
+  uint32_t dst_offset;
+  uint32_t dst_strides[3];
+  uint32_t pos_scale;
+  uint32_t src_f16, dst_f16;
+} CopyArgs;
+
 // Persistent decode SwiGLU MLP chain in one launch: `layers` MLPs, layer
 // l+1 reading layer l's output y as its x.  In a layer, `a` is the dual
 // gate/up GEMV (producer of h = act(x Wg) * (x Wu)) and `b` the down-proj

@@ -213,14 +213,6 @@ template <typename T> void destroy_handle(T *p) {
   }
 }
 
-int unsupported(const ta_executor *exec, const char *fn) {
-  return ffi_status([&] {
-    checked_ref(exec, std::string(fn) + ": exec is null");
-    fail(std::string(fn) +
-         ": unsupported: model ops are outside this build's fused-epilogue GEMM path");
-  });
-}
-
 } // namespace
 
 extern "C" {
@@ -426,25 +418,89 @@ int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a, const ta_ten
   });
 }
 
-int ta_softmax_rows(const ta_executor *exec, const ta_tensor *, const ta_tensor *, float, uint32_t,
-                    uint32_t, uint32_t, ta_run_stats *) {
-  return unsupported(exec, "ta_softmax_rows");
+// capi/src/api/elementwise.rs: the model ops.
+int ta_softmax_rows(const ta_executor *exec, const ta_tensor *input, const ta_tensor *output,
+                    float scale, uint32_t mask_kind, uint32_t valid_or_prefix,
+                    uint32_t rows_per_group, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_softmax_rows: exec is null");
+    const Tensor *in = checked_tensor(e, input, "ta_softmax_rows", "input");
+    const Tensor *out = checked_tensor(e, output, "ta_softmax_rows", "output");
+    SoftmaxMask mask;
+    switch (mask_kind) {
+    case TA_SOFTMAX_MASK_FULL:
+      break;
+    case TA_SOFTMAX_MASK_PREFIX:
+      mask = SoftmaxMask::prefix_of(valid_or_prefix);
+      break;
+    case TA_SOFTMAX_MASK_CAUSAL:
+      mask = SoftmaxMask::causal(valid_or_prefix, rows_per_group);
+      break;
+    default:
+      fail("ta_softmax_rows: mask_kind " + std::to_string(mask_kind) +
+           " is invalid (0=full 1=prefix 2=causal)");
+    }
+    write_stats(stats, e.exec->run_softmax_rows(*in, *out, scale, mask));
+  });
 }
-int ta_rms_norm(const ta_executor *exec, const ta_tensor *, const ta_tensor *, const ta_tensor *,
-                float, ta_run_stats *) {
-  return unsupported(exec, "ta_rms_norm");
+
+int ta_rms_norm(const ta_executor *exec, const ta_tensor *input, const ta_tensor *weight,
+                const ta_tensor *output, float eps, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_rms_norm: exec is null");
+    const Tensor *in = checked_tensor(e, input, "ta_rms_norm", "input");
+    const Tensor *w = checked_tensor(e, weight, "ta_rms_norm", "weight");
+    const Tensor *out = checked_tensor(e, output, "ta_rms_norm", "output");
+    write_stats(stats, e.exec->run_rms_norm(*in, *w, *out, eps));
+  });
 }
-int ta_layer_norm(const ta_executor *exec, const ta_tensor *, const ta_tensor *, const ta_tensor *,
-                  const ta_tensor *, float, ta_run_stats *) {
-  return unsupported(exec, "ta_layer_norm");
+
+int ta_layer_norm(const ta_executor *exec, const ta_tensor *input, const ta_tensor *weight,
+                  const ta_tensor *bias, const ta_tensor *output, float eps, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_layer_norm: exec is null");
+    const Tensor *in = checked_tensor(e, input, "ta_layer_norm", "input");
+    const Tensor *w = checked_tensor(e, weight, "ta_layer_norm", "weight");
+    const Tensor *b = checked_tensor(e, bias, "ta_layer_norm", "bias");
+    const Tensor *out = checked_tensor(e, output, "ta_layer_norm", "output");
+    write_stats(stats, e.exec->run_layer_norm(*in, *w, *b, *out, eps));
+  });
 }
-int ta_rope(const ta_executor *exec, const ta_tensor *, const ta_tensor *, const ta_tensor *,
-            const ta_rope_desc *, ta_run_stats *) {
-  return unsupported(exec, "ta_rope");
+
+int ta_rope(const ta_executor *exec, const ta_tensor *input, const ta_tensor *table,
+            const ta_tensor *output, const ta_rope_desc *desc, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_rope: exec is null");
+    const Tensor *in = checked_tensor(e, input, "ta_rope", "input");
+    const Tensor *t = checked_tensor(e, table, "ta_rope", "table");
+    const Tensor *out = checked_tensor(e, output, "ta_rope", "output");
+    const ta_rope_desc &d = checked_ref(desc, "ta_rope: desc is null");
+    RopeDesc rd;
+    rd.heads = d.heads;
+    rd.head_dim = d.head_dim;
+    rd.rot_dim = d.rot_dim;
+    rd.pos_base = d.pos_base;
+    write_stats(stats, e.exec->run_rope(*in, *t, *out, rd));
+  });
 }
-int ta_copy_strided(const ta_executor *exec, const ta_tensor *, const ta_tensor *,
-                    const ta_copy_desc *, ta_run_stats *) {
-  return unsupported(exec, "ta_copy_strided");
+
+int ta_copy_strided(const ta_executor *exec, const ta_tensor *src, const ta_tensor *dst,
+                    const ta_copy_desc *desc, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_copy_strided: exec is null");
+    const Tensor *s_ = checked_tensor(e, src, "ta_copy_strided", "src");
+    const Tensor *d_ = checked_tensor(e, dst, "ta_copy_strided", "dst");
+    const ta_copy_desc &d = checked_ref(desc, "ta_copy_strided: desc is null");
+    CopyDesc cd;
+    for (int i = 0; i < 3; ++i) {
+      cd.extent[i] = d.extent[i];
+      cd.src_strides[i] = d.src_strides[i];
+      cd.dst_strides[i] = d.dst_strides[i];
+    }
+    cd.src_offset = d.src_offset;
+    cd.dst_offset = d.dst_offset;
+    write_stats(stats, e.exec->run_copy_strided(*s_, *d_, cd));
+  });
 }
 
 static ta_prepared *make_prepared(const ta_executor *exec, std::vector<MatmulOp> (*conv)(

@@ -775,6 +775,21 @@ struct ExecutorImpl {
     return (uint64_t)((double)ms * 1e6);
   }
 
+  // One model-op launch on a slot between its events
+  // (elementwise/mod.rs:498-515: n_calls 1, no flops).
+  RunStats run_single(const char *symbol, uint32_t groups, void *args) {
+    ctx->make_current();
+    Lease lease(this);
+    Slot *slot = lease.s;
+    hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
+    launch(symbol, groups, 1, 1, 256, args, slot->stream);
+    hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
+    hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
+    return RunStats{(uint64_t)((double)ms * 1e6), 1, 0};
+  }
+
   // ---- tuning (src/executor/tuning.rs) ----
   void load_store() {
     header = tune_header_line(*ctx);
@@ -1139,6 +1154,203 @@ RunStats Executor::run_op_graph(const std::vector<MatmulOp> &ops) const {
 }
 RunStats Executor::run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const {
   return impl_->run_split_k2(call, num_k_splits);
+}
+
+// ---- model ops (src/executor/elementwise/ops.rs) ----
+namespace {
+void ensure_f32(const Tensor &t, const std::string &op, const char *role) {
+  if (t.dtype() != DType::F32)
+    fail(op + ": " + role + " must be f32 storage (got " + dtype_name(t.dtype()) + ")");
+}
+void ensure_same_shape(const std::string &op, const Tensor &in, const Tensor &out) {
+  if (in.shape() != out.shape())
+    fail(op + ": output shape " + fmt_shape(out.shape()) + " must equal input shape " +
+         fmt_shape(in.shape()));
+}
+// elementwise/mod.rs:391-398.
+std::pair<uint32_t, uint32_t> rows_cols(const Tensor &t, const std::string &op) {
+  const uint32_t cols = t.shape().back();
+  const uint64_t rows = t.len() / cols;
+  if (rows > UINT32_MAX)
+    fail(op + ": row count " + std::to_string(rows) + " exceeds u32");
+  return {(uint32_t)rows, cols};
+}
+bool io_f16(const std::string &op, const Tensor &in, const Tensor &out) {
+  if (in.dtype() != out.dtype())
+    fail(op + ": input (" + dtype_name(in.dtype()) + ") and output (" + dtype_name(out.dtype()) +
+         ") must share a storage type");
+  return in.dtype() == DType::F16;
+}
+uint32_t grid_for(uint64_t items, uint32_t per_group, uint32_t cus) {
+  return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((items + per_group - 1) / per_group,
+                                                            64ull * cus));
+}
+} // namespace
+
+RunStats Executor::run_softmax_rows(const Tensor &input, const Tensor &output, float scale,
+                                    SoftmaxMask mask) const {
+  const std::string op = "run_softmax_rows";
+  impl_->validate_tensor(&input, "input");
+  impl_->validate_tensor(&output, "output");
+  ensure_f32(input, op, "input");
+  ensure_f32(output, op, "output");
+  ensure_same_shape(op, input, output);
+  auto [rows, cols] = rows_cols(input, op);
+  SoftmaxArgs a{};
+  a.in = static_cast<const float *>(input.device_ptr());
+  a.out = static_cast<float *>(output.device_ptr());
+  a.rows = rows;
+  a.cols = cols;
+  a.scale = scale;
+  a.rows_per_group = 1;
+  switch (mask.kind) {
+  case SoftmaxMask::Kind::Full:
+    a.valid_base = cols;
+    break;
+  case SoftmaxMask::Kind::Prefix:
+    a.valid_base = std::min(mask.valid, cols);
+    break;
+  case SoftmaxMask::Kind::Causal:
+    if (mask.rows_per_group == 0 || rows % mask.rows_per_group != 0)
+      fail(op + ": rows_per_group " + std::to_string(mask.rows_per_group) +
+           " must divide rows " + std::to_string(rows));
+    a.valid_base = mask.prefix;
+    a.rows_per_group = mask.rows_per_group;
+    a.causal = 1;
+    break;
+  }
+  return impl_->run_single("ta_softmax_rows", grid_for(rows, 1, impl_->ctx->cu_count()), &a);
+}
+
+static RunStats run_norm(ExecutorImpl &e, const std::string &op, const Tensor &input,
+                         const Tensor &weight, const Tensor *bias, const Tensor &output,
+                         float eps) {
+  e.validate_tensor(&input, "input");
+  e.validate_tensor(&output, "output");
+  e.validate_tensor(&weight, "weight");
+  const bool f16 = io_f16(op, input, output);
+  ensure_f32(weight, op, "weight");
+  if (bias) {
+    e.validate_tensor(bias, "bias");
+    ensure_f32(*bias, op, "bias");
+    if (f16)
+      fail(op + ": f16 activations are supported for RMSNorm only (no f16 LayerNorm kernel)");
+  }
+  ensure_same_shape(op, input, output);
+  auto [rows, cols] = rows_cols(input, op);
+  if (weight.len() != cols)
+    fail(op + ": weight length " + std::to_string(weight.len()) + " != row length " +
+         std::to_string(cols));
+  if (bias && bias->len() != cols)
+    fail(op + ": bias length " + std::to_string(bias->len()) + " != row length " +
+         std::to_string(cols));
+  NormArgs a{};
+  a.in = input.device_ptr();
+  a.out = output.device_ptr();
+  a.weight = static_cast<const float *>(weight.device_ptr());
+  a.bias = bias ? static_cast<const float *>(bias->device_ptr()) : nullptr;
+  a.rows = rows;
+  a.cols = cols;
+  a.eps = eps;
+  a.io_f16 = f16 ? 1u : 0u;
+  return e.run_single("ta_norm_rows", grid_for(rows, 1, e.ctx->cu_count()), &a);
+}
+
+RunStats Executor::run_rms_norm(const Tensor &input, const Tensor &weight, const Tensor &output,
+                                float eps) const {
+  return run_norm(*impl_, "run_rms_norm", input, weight, nullptr, output, eps);
+}
+
+RunStats Executor::run_layer_norm(const Tensor &input, const Tensor &weight, const Tensor &bias,
+                                  const Tensor &output, float eps) const {
+  return run_norm(*impl_, "run_layer_norm", input, weight, &bias, output, eps);
+}
+
+RunStats Executor::run_rope(const Tensor &input, const Tensor &table, const Tensor &output,
+                            const RopeDesc &desc) const {
+  const std::string op = "run_rope";
+  impl_->validate_tensor(&input, "input");
+  impl_->validate_tensor(&output, "output");
+  impl_->validate_tensor(&table, "table");
+  const bool f16 = io_f16(op, input, output);
+  ensure_f32(table, op, "table");
+  ensure_same_shape(op, input, output);
+  // ops.rs:177-207 (rope_tokens).
+  if (desc.rot_dim < 2 || desc.rot_dim % 2 != 0 || desc.rot_dim > desc.head_dim)
+    fail(op + ": rot_dim " + std::to_string(desc.rot_dim) +
+         " must be even, >= 2, and <= head_dim " + std::to_string(desc.head_dim));
+  const uint64_t vec_elems = (uint64_t)desc.heads * desc.head_dim;
+  if (vec_elems == 0 || input.len() % vec_elems != 0)
+    fail(op + ": input length " + std::to_string(input.len()) +
+         " is not a multiple of heads*head_dim " + std::to_string(vec_elems));
+  const uint64_t tokens = input.len() / vec_elems;
+  if (tokens > UINT32_MAX)
+    fail(op + ": token count exceeds u32");
+  const uint64_t needed = ((uint64_t)desc.pos_base + tokens) * desc.rot_dim;
+  if (table.len() < needed)
+    fail(op + ": table length " + std::to_string(table.len()) + " < required " +
+         std::to_string(needed) + " (pos_base " + std::to_string(desc.pos_base) + " + " +
+         std::to_string(tokens) + " tokens, rot_dim " + std::to_string(desc.rot_dim) + ")");
+  RopeArgs a{};
+  a.in = input.device_ptr();
+  a.out = output.device_ptr();
+  a.table = static_cast<const float *>(table.device_ptr());
+  a.pos_addr = reinterpret_cast<const uint32_t *>(desc.pos_addr);
+  a.tokens = (uint32_t)tokens;
+  a.heads = desc.heads;
+  a.head_dim = desc.head_dim;
+  a.rot_dim = desc.rot_dim;
+  a.pos_base = desc.pos_base;
+  a.io_f16 = f16 ? 1u : 0u;
+  const uint64_t pairs = tokens * desc.heads * (desc.rot_dim / 2);
+  return impl_->run_single("ta_rope", grid_for(pairs, 256, impl_->ctx->cu_count()), &a);
+}
+
+RunStats Executor::run_copy_strided(const Tensor &src, const Tensor &dst,
+                                    const CopyDesc &desc) const {
+  const std::string op = "run_copy_strided";
+  impl_->validate_tensor(&src, "src");
+  impl_->validate_tensor(&dst, "dst");
+  // ops.rs:387-437.
+  if (src.buffer_id() == dst.buffer_id())
+    fail(op + ": src and dst must be different tensors");
+  for (uint32_t e : desc.extent)
+    if (e == 0)
+      fail(op + ": extent [" + std::to_string(desc.extent[0]) + ", " +
+           std::to_string(desc.extent[1]) + ", " + std::to_string(desc.extent[2]) +
+           "] has a zero axis");
+  auto max_index = [&](uint32_t offset, const std::array<uint32_t, 3> &strides) {
+    uint64_t m = offset;
+    for (int i = 0; i < 3; ++i)
+      m += (uint64_t)(desc.extent[i] - 1) * strides[i];
+    return m;
+  };
+  if (max_index(desc.src_offset, desc.src_strides) >= src.len())
+    fail(op + ": source access reaches element " +
+         std::to_string(max_index(desc.src_offset, desc.src_strides)) + " but src has " +
+         std::to_string(src.len()));
+  if (max_index(desc.dst_offset, desc.dst_strides) >= dst.len())
+    fail(op + ": destination access reaches element " +
+         std::to_string(max_index(desc.dst_offset, desc.dst_strides)) + " but dst has " +
+         std::to_string(dst.len()));
+  const uint64_t total = (uint64_t)desc.extent[0] * desc.extent[1] * desc.extent[2];
+  if (total > UINT32_MAX)
+    fail(op + ": extent product exceeds u32");
+  CopyArgs a{};
+  a.src = src.device_ptr();
+  a.dst = dst.device_ptr();
+  a.pos_addr = reinterpret_cast<const uint32_t *>(desc.pos_addr);
+  for (int i = 0; i < 3; ++i) {
+    a.extent[i] = desc.extent[i];
+    a.src_strides[i] = desc.src_strides[i];
+    a.dst_strides[i] = desc.dst_strides[i];
+  }
+  a.src_offset = desc.src_offset;
+  a.dst_offset = desc.dst_offset;
+  a.pos_scale = desc.pos_scale;
+  a.src_f16 = src.dtype() == DType::F16 ? 1u : 0u;
+  a.dst_f16 = dst.dtype() == DType::F16 ? 1u : 0u;
+  return impl_->run_single("ta_copy_strided", grid_for(total, 256, impl_->ctx->cu_count()), &a);
 }
 
 std::unique_ptr<PreparedOps> Executor::prepare_matmuls(const std::vector<MatmulCall> &calls) const {

@@ -15,6 +15,7 @@
 namespace tensor_ash {
 
 [[noreturn]] void fail(const std::string &msg);
+std::string fmt_shape(const std::vector<uint32_t> &shape); // "[a, b, c]"
 void hip_check(hipError_t err, const char *what);
 
 struct DeviceBuffer {

@@ -19,6 +19,8 @@ std::optional<uint64_t> checked_product(std::initializer_list<uint64_t> values) 
   return acc;
 }
 
+} // namespace
+
 std::string fmt_shape(const std::vector<uint32_t> &s) {
   std::ostringstream o;
   o << "[";
@@ -27,6 +29,8 @@ std::string fmt_shape(const std::vector<uint32_t> &s) {
   o << "]";
   return o.str();
 }
+
+namespace {
 
 void ensure_dim_eq(const char *ll, uint32_t l, const char *rl, uint32_t r) {
   if (l != r) {

@@ -174,6 +174,33 @@ struct MatmulOp {
   bool has_decode_fusion() const { return normed_a.has_value() || !store.is_none(); }
 };
 
+// Model-op descriptors (src/executor/elementwise/mod.rs:112-270).
+struct SoftmaxMask {
+  enum class Kind { Full, Prefix, Causal };
+  Kind kind = Kind::Full;
+  uint32_t valid = 0;          // Prefix
+  uint32_t prefix = 0;         // Causal
+  uint32_t rows_per_group = 0; // Causal
+  static SoftmaxMask full() { return {}; }
+  static SoftmaxMask prefix_of(uint32_t valid) { return {Kind::Prefix, valid, 0, 0}; }
+  static SoftmaxMask causal(uint32_t prefix, uint32_t rows_per_group) {
+    return {Kind::Causal, 0, prefix, rows_per_group};
+  }
+};
+struct RopeDesc {
+  uint32_t heads = 0, head_dim = 0, rot_dim = 0, pos_base = 0;
+  uint64_t pos_addr = 0; // device address of a u32 position, 0 = none
+};
+struct CopyDesc {
+  std::array<uint32_t, 3> extent{};
+  uint32_t src_offset = 0;
+  std::array<uint32_t, 3> src_strides{};
+  uint32_t dst_offset = 0;
+  std::array<uint32_t, 3> dst_strides{};
+  uint64_t pos_addr = 0; // device address of a u32 position, 0 = none
+  uint32_t pos_scale = 0;
+};
+
 // src/matmul/api.rs:311-353.
 struct RunStats {
   std::optional<uint64_t> gpu_time_ns;
@@ -329,6 +356,18 @@ public:
   RunStats run_ops(const std::vector<MatmulOp> &ops) const;
   RunStats run_op_graph(const std::vector<MatmulOp> &ops) const;
   RunStats run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const;
+
+  // Model ops (src/executor/elementwise/ops.rs); in-place (input ==
+  // output) is allowed except for the copy.
+  RunStats run_softmax_rows(const Tensor &input, const Tensor &output, float scale,
+                            SoftmaxMask mask) const;
+  RunStats run_rms_norm(const Tensor &input, const Tensor &weight, const Tensor &output,
+                        float eps) const;
+  RunStats run_layer_norm(const Tensor &input, const Tensor &weight, const Tensor &bias,
+                          const Tensor &output, float eps) const;
+  RunStats run_rope(const Tensor &input, const Tensor &table, const Tensor &output,
+                    const RopeDesc &desc) const;
+  RunStats run_copy_strided(const Tensor &src, const Tensor &dst, const CopyDesc &desc) const;
 
   std::unique_ptr<PreparedOps> prepare_matmuls(const std::vector<MatmulCall> &calls) const;
   std::unique_ptr<PreparedOps> prepare_ops(const std::vector<MatmulOp> &ops) const;

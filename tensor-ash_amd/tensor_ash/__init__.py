@@ -70,6 +70,15 @@ class _OpV3(C.Structure):
                 ("store", _StoreDesc)]
 
 
+class _RopeDesc(C.Structure):
+    _fields_ = [("heads", C.c_uint32), ("head_dim", C.c_uint32), ("rot_dim", C.c_uint32), ("pos_base", C.c_uint32)]
+
+
+class _CopyDesc(C.Structure):
+    _fields_ = [("extent", C.c_uint32 * 3), ("src_offset", C.c_uint32), ("src_strides", C.c_uint32 * 3),
+                ("dst_offset", C.c_uint32), ("dst_strides", C.c_uint32 * 3)]
+
+
 class _DispatchInfo(C.Structure):
     _fields_ = [("kernel", C.c_char_p), ("tile", C.c_uint32 * 3), ("has_split_k2", C.c_uint32),
                 ("split_k2_splits", C.c_uint32)]
@@ -117,6 +126,11 @@ _sig("ta_run_ops_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
 _sig("ta_run_op_graph_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
 _sig("ta_prepared_create_v3", P, P, C.POINTER(_OpV3), sz, u32)
 _sig("ta_tensor_device_address", u64, P)
+_sig("ta_softmax_rows", C.c_int, P, P, P, f32, u32, u32, u32, C.POINTER(RunStats))
+_sig("ta_rms_norm", C.c_int, P, P, P, P, f32, C.POINTER(RunStats))
+_sig("ta_layer_norm", C.c_int, P, P, P, P, P, f32, C.POINTER(RunStats))
+_sig("ta_rope", C.c_int, P, P, P, P, C.POINTER(_RopeDesc), C.POINTER(RunStats))
+_sig("ta_copy_strided", C.c_int, P, P, P, C.POINTER(_CopyDesc), C.POINTER(RunStats))
 _sig("ta_prepared_run", C.c_int, P, C.POINTER(RunStats))
 _sig("ta_prepared_submit", C.c_int, P)
 _sig("ta_prepared_wait", C.c_int, P, C.POINTER(RunStats))
@@ -402,6 +416,40 @@ class Executor:
         st = RunStats()
         fn = {1: _lib.ta_run_op_graph, 2: _lib.ta_run_op_graph_v2, 3: _lib.ta_run_op_graph_v3}[ver]
         _check(fn(self._h, arr, len(ops), C.byref(st)))
+        return st
+
+    # ---- model ops (include/tensor_ash.h ta_softmax_rows ... ta_copy_strided) ----
+    def softmax_rows(self, input: Tensor, output: Tensor, scale: float = 1.0, mask_kind: int = 0,
+                     valid_or_prefix: int = 0, rows_per_group: int = 0) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_softmax_rows(self._h, input.handle, output.handle, scale, mask_kind, valid_or_prefix,
+                                    rows_per_group, C.byref(st)))
+        return st
+
+    def rms_norm(self, input: Tensor, weight: Tensor, output: Tensor, eps: float) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_rms_norm(self._h, input.handle, weight.handle, output.handle, eps, C.byref(st)))
+        return st
+
+    def layer_norm(self, input: Tensor, weight: Tensor, bias: Tensor, output: Tensor, eps: float) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_layer_norm(self._h, input.handle, weight.handle, bias.handle, output.handle, eps,
+                                  C.byref(st)))
+        return st
+
+    def rope(self, input: Tensor, table: Tensor, output: Tensor, heads: int, head_dim: int, rot_dim: int,
+             pos_base: int = 0) -> RunStats:
+        st = RunStats()
+        d = _RopeDesc(heads, head_dim, rot_dim, pos_base)
+        _check(_lib.ta_rope(self._h, input.handle, table.handle, output.handle, C.byref(d), C.byref(st)))
+        return st
+
+    def copy_strided(self, src: Tensor, dst: Tensor, extent, src_strides, dst_strides, src_offset: int = 0,
+                     dst_offset: int = 0) -> RunStats:
+        st = RunStats()
+        d = _CopyDesc((C.c_uint32 * 3)(*extent), src_offset, (C.c_uint32 * 3)(*src_strides), dst_offset,
+                      (C.c_uint32 * 3)(*dst_strides))
+        _check(_lib.ta_copy_strided(self._h, src.handle, dst.handle, C.byref(d), C.byref(st)))
         return st
 
     def run_matmuls_split_k2(self, a: Tensor, b: Tensor, c: Tensor, splits: int, alpha: float = 1.0) -> RunStats:

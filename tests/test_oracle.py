@@ -321,3 +321,75 @@ def test_scatter_index_matches_cache_layouts(oracle):
     f16 = oracle.store_scatter(np.zeros(h * t_max * dh), y, pos, dh, dh, t_max * dh, 1, f16=True)
     assert np.array_equal(f16.reshape(h, t_max, dh)[:, pos, :].reshape(-1),
                           y.astype(np.float16).astype(np.float32))
+
+
+# ---------------------------------------------------------------- model ops
+
+def test_softmax_rows_pinned(oracle):
+    """softmax_rows pinned against scipy's softmax (f64) on every valid
+    prefix; masked tails are exactly 0, rows sum to 1, an all-masked row
+    is all zeros."""
+    import scipy.special
+    rows, cols, scale = 6, 517, 0.125
+    x = oracle.fill_det(rows * cols, 2100)
+    full = oracle.softmax_rows(x, rows, cols, scale, cols).reshape(rows, cols)
+    want = scipy.special.softmax(x.reshape(rows, cols).astype(np.float64) * np.float32(scale), axis=1)
+    assert np.allclose(full, want, rtol=1e-6, atol=1e-9)
+    causal = oracle.softmax_rows(x, rows, cols, scale, lambda r: 100 + r % 3 + 1).reshape(rows, cols)
+    for r in range(rows):
+        v = 100 + r % 3 + 1
+        assert np.all(causal[r, v:] == 0) and abs(causal[r].sum() - 1) < 1e-6
+        ref = scipy.special.softmax(x.reshape(rows, cols)[r, :v].astype(np.float64) * np.float32(scale))
+        assert np.allclose(causal[r, :v], ref, rtol=1e-6, atol=1e-9)
+    assert np.all(oracle.softmax_rows(x, rows, cols, scale, 0) == 0)
+
+
+def test_layer_norm_pinned(oracle):
+    """layer_norm_rows pinned against torch's layer_norm in f64 and the
+    invariant that a normalized row (w = 1, b = 0) has mean 0 and
+    variance var / (var + eps)."""
+    import torch
+    rows, cols, eps = 5, 771, 1e-5
+    x, w, b = oracle.fill_det(rows * cols, 2200), oracle.fill_det(cols, 2201), oracle.fill_det(cols, 2202)
+    got = oracle.layer_norm_rows(x, w, b, rows, cols, eps).reshape(rows, cols)
+    ref = torch.nn.functional.layer_norm(torch.from_numpy(x.reshape(rows, cols)).double(), (cols,),
+                                         torch.from_numpy(w).double(), torch.from_numpy(b).double(),
+                                         eps=float(np.float32(eps)))
+    assert np.allclose(got, ref.numpy(), rtol=1e-6, atol=1e-6)
+    y = oracle.layer_norm_rows(x, np.ones(cols), np.zeros(cols), rows, cols, 0.0).reshape(rows, cols)
+    assert np.allclose(y.mean(axis=1), 0, atol=1e-6) and np.allclose((y.astype(np.float64) ** 2).mean(axis=1), 1, atol=1e-5)
+
+
+def test_rope_tokens_pinned(oracle):
+    """rope_tokens pinned against complex multiplication with the Llama
+    table theta = pos / 10000^(2i/rot_dim) (tests/correctness/
+    elementwise.rs:146-222), and lanes past rot_dim passing through."""
+    tokens, heads, hd, rot, t_max, pos_base = 3, 4, 16, 12, 32, 7
+    x = oracle.fill_det(tokens * heads * hd, 2300)
+    half = rot // 2
+    theta = np.array([[p / 10000.0 ** (2.0 * i / rot) for i in range(half)] for p in range(t_max)])
+    table = np.stack([np.cos(theta), np.sin(theta)], axis=-1).astype(np.float32)
+    got = oracle.rope_tokens(x, table, tokens, heads, hd, rot, pos_base).reshape(tokens, heads, hd)
+    xv = x.reshape(tokens, heads, hd).astype(np.float64)
+    z = xv[:, :, 0:rot:2] + 1j * xv[:, :, 1:rot:2]
+    ang = table[pos_base:pos_base + tokens].astype(np.float64)
+    rot_z = z * (ang[:, None, :, 0] + 1j * ang[:, None, :, 1])
+    assert np.allclose(got[:, :, 0:rot:2], rot_z.real, atol=1e-6)
+    assert np.allclose(got[:, :, 1:rot:2], rot_z.imag, atol=1e-6)
+    assert np.array_equal(got[:, :, rot:], x.reshape(tokens, heads, hd)[:, :, rot:])
+
+
+def test_copy_strided_pinned(oracle):
+    """copy_strided pinned by numpy transposes: a stride swap transposes a
+    37x53 matrix, and the Kt-cache append of elementwise.rs:275-300
+    lands the vector in column t of [heads, dh, t_max]."""
+    r, c = 37, 53
+    src = oracle.fill_det(r * c, 2400)
+    t = oracle.copy_strided(src, np.zeros(r * c), (c, r, 1), 0, (1, c, 0), 0, (r, 1, 0))
+    assert np.array_equal(t.reshape(c, r), src.reshape(r, c).T)
+    heads, dh, t_max, step = 4, 8, 16, 5
+    k = oracle.fill_det(heads * dh, 2401)
+    cache = oracle.copy_strided(k, np.zeros(heads * dh * t_max), (dh, heads, 1), 0, (1, dh, 0), step,
+                                (t_max, dh * t_max, 0)).reshape(heads, dh, t_max)
+    assert np.array_equal(cache[:, :, step], k.reshape(heads, dh))
+    assert np.count_nonzero(cache) == np.count_nonzero(k)
