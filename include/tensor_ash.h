@@ -279,6 +279,75 @@ ta_prepared *ta_prepared_create_v3(const ta_executor *exec,
  * (0 for NULL), e.g. for ta_store_desc.pos_addr. */
 uint64_t ta_tensor_device_address(const ta_tensor *tensor);
 
+/* Causal prefill attention, Executor::run_flash_attention
+ * (src/executor/elementwise/flash.rs:13-250; FlashAttentionDesc,
+ * src/executor/elementwise/mod.rs:160-184), which the reference exposes
+ * in its Rust API only.  out = softmax_causal(q Kt * scale) V in one
+ * launch: query row i attends to cache positions < min(kv_len, pos_base
+ * + i + 1).  kt is [H_kv, dh, T_max], v is [H_kv, T_max, dh] (f32 or
+ * f16, alike), dh 64 or 128, H a multiple of H_kv.  q/out are f32, or
+ * f16 with f16 caches; head-major [H, T, dh] unless token_major_heads
+ * (q, and out unless out_token_major_heads) is nonzero: token-major
+ * [T, H*dh]. */
+typedef struct ta_flash_desc {
+  uint32_t kv_len;
+  uint32_t pos_base;
+  float scale;                    /* 1/sqrt(dh) for standard attention */
+  uint32_t token_major_heads;     /* 0: q is head-major */
+  uint32_t out_token_major_heads; /* 0: out follows q */
+  uint32_t reserved;              /* must be zero */
+} ta_flash_desc;
+int ta_flash_attention(const ta_executor *exec, const ta_tensor *q,
+                       const ta_tensor *kt, const ta_tensor *v,
+                       const ta_tensor *out, const ta_flash_desc *desc,
+                       ta_run_stats *stats);
+
+/* Mixed-op graphs, Executor::run_exec_ops / prepare_exec_ops with ExecOp
+ * (src/executor/graph_ops.rs:23-336), Rust-API-only in the reference: a
+ * dependent chain of matmuls and model ops run (or recorded once as a
+ * hipGraph) in list order, every op seeing all earlier writes; every op
+ * is validated before anything is launched.  Operand roles by kind:
+ *   MATMUL          matmul (in/out unused)
+ *   RMS_NORM        in[0] input, in[1] weight, out; scalar = eps
+ *   LAYER_NORM      in[0] input, in[1] weight, in[2] bias, out; scalar = eps
+ *   SOFTMAX_ROWS    in[0] input, out; scalar = scale; mask_kind,
+ *                   valid_or_prefix, rows_per_group as ta_softmax_rows
+ *   ROPE            in[0] input, in[1] table, out; rope
+ *   COPY_STRIDED    in[0] src, out dst; copy
+ *   FLASH_ATTENTION in[0] q, in[1] kt, in[2] v, out; flash
+ * pos_addr (ROPE, COPY_STRIDED): device address of a u32 position cell
+ * read when the op runs (added to rope.pos_base; times pos_scale added to
+ * copy.dst_offset), so a prepared graph replays at a new position after
+ * the cell is rewritten; 0 = none. */
+enum {
+  TA_EXEC_MATMUL = 0,
+  TA_EXEC_RMS_NORM = 1,
+  TA_EXEC_LAYER_NORM = 2,
+  TA_EXEC_SOFTMAX_ROWS = 3,
+  TA_EXEC_ROPE = 4,
+  TA_EXEC_COPY_STRIDED = 5,
+  TA_EXEC_FLASH_ATTENTION = 6,
+};
+typedef struct ta_exec_op {
+  uint32_t kind; /* TA_EXEC_* */
+  uint32_t mask_kind;
+  uint32_t valid_or_prefix;
+  uint32_t rows_per_group;
+  float scalar;
+  uint32_t pos_scale;
+  uint64_t pos_addr;
+  const ta_tensor *in[3];
+  const ta_tensor *out;
+  const ta_matmul_op_v3 *matmul;
+  ta_rope_desc rope;
+  ta_copy_desc copy;
+  ta_flash_desc flash;
+} ta_exec_op;
+int ta_run_exec_ops(const ta_executor *exec, const ta_exec_op *ops,
+                    size_t n_ops, ta_run_stats *stats);
+ta_prepared *ta_prepared_create_exec(const ta_executor *exec,
+                                     const ta_exec_op *ops, size_t n_ops);
+
 /* pack_f16w_row_tiles (src/matmul/api.rs:324-344): row-major [K, N] ->
  * [N/tile_n][K][tile_n]; dst holds K*N floats. */
 int ta_pack_f16w_row_tiles(const float *src, size_t k, size_t n,

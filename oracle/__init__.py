@@ -294,3 +294,31 @@ def copy_strided(src, dst, extent, src_offset, src_strides, dst_offset, dst_stri
     v = s[si.reshape(-1)]
     out[di.reshape(-1)] = round_via_f16(v) if dst_f16 else v
     return out
+
+
+def flash_attention(q, kt, v, heads: int, kv_heads: int, t_q: int, t_max: int, dh: int, kv_len: int,
+                    pos_base: int, scale: float) -> np.ndarray:
+    """Causal prefill attention of tests/correctness/flash.rs:10-61
+    (cpu_flash) in f64: head h reads kv head h / (heads / kv_heads); query
+    row i attends to cache positions < min(kv_len, pos_base + i + 1) with
+    softmax(q . k * scale); q/out are head-major [H, T_q, dh], kt is
+    [H_kv, dh, T_max], v is [H_kv, T_max, dh].  A row with no valid
+    position is all zeros."""
+    q64 = np.asarray(q, np.float32).reshape(heads, t_q, dh).astype(np.float64)
+    kt64 = np.asarray(kt, np.float32).reshape(kv_heads, dh, t_max).astype(np.float64)
+    v64 = np.asarray(v, np.float32).reshape(kv_heads, t_max, dh).astype(np.float64)
+    out = np.zeros((heads, t_q, dh))
+    group = heads // kv_heads
+    valid = np.minimum(kv_len, pos_base + np.arange(t_q) + 1)
+    span = int(valid.max()) if t_q else 0
+    if span == 0:
+        return out.astype(np.float32).reshape(-1)
+    mask = np.arange(span)[None, :] < valid[:, None]
+    for h in range(heads):
+        kh = h // group
+        s = (q64[h] @ kt64[kh, :, :span]) * float(np.float32(scale))
+        s = np.where(mask, s, -np.inf)
+        m = s.max(axis=1, keepdims=True)
+        p = np.where(mask, np.exp(s - m), 0.0)
+        out[h] = (p / p.sum(axis=1, keepdims=True)) @ v64[kh, :span]
+    return out.astype(np.float32).reshape(-1)

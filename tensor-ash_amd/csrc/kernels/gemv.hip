@@ -537,7 +537,9 @@ struct Gemv {
         continue;
       if (f.store_mode != 2) {
         const uint32_t dim = c % f.head_dim;
-        const uint32_t angle = (pos * (f.head_dim / 2) + dim / 2) * 2;
+        const uint64_t angle = ((uint64_t)pos * (f.head_dim / 2) + dim / 2) * 2;
+        if (angle + 1 >= f.table_len)
+          continue;
         const float cos_t = f.rope_table[angle], sin_t = f.rope_table[angle + 1];
         v = (dim & 1u) == 0 ? fmaf(v, cos_t, -partner * sin_t) : fmaf(partner, sin_t, v * cos_t);
       }
@@ -547,6 +549,8 @@ struct Gemv {
         const uint64_t idx = (uint64_t)pos * f.pos_scale +
                              (uint64_t)(c / f.head_dim) * f.stride_head +
                              (uint64_t)(c % f.head_dim) * f.stride_dim;
+        if (idx >= f.dst_len)
+          continue;
         if (f.store_dst_f16)
           static_cast<_Float16 *>(f.store_dst)[idx] = (_Float16)v;
         else

@@ -132,6 +132,10 @@ typedef struct GemvFusion {
   const uint32_t *pos_addr;
   const float *rope_table; // [T_max, head_dim / 2, 2] (cos, sin)
   void *store_dst;         // f32 or f16 elements
+  // Element counts of rope_table / store_dst: a device position that
+  // reaches past them skips the element instead of reading or writing
+  // out of bounds.
+  uint64_t table_len, dst_len;
 } GemvFusion;
 
 // ---- model ops (ta_softmax_rows, ta_rms_norm, ta_layer_norm, ta_rope,
@@ -168,6 +172,7 @@ typedef struct RopeArgs {
   const uint32_t *pos_addr; // null: none
   uint32_t tokens, heads, head_dim, rot_dim, pos_base;
   uint32_t io_f16;
+  uint64_t table_len; // elements; pairs whose angle lies past it are skipped
 } RopeArgs;
 
 // Strided 3-D copy: for (x, y, z) < extent, dst[dst_offset + *pos_addr *
@@ -184,7 +189,24 @@ typedef struct CopyArgs {
   uint32_t dst_strides[3];
   uint32_t pos_scale;
   uint32_t src_f16, dst_f16;
+  uint64_t dst_len; // elements; destinations past it are skipped
 } CopyArgs;
+
+// Causal prefill attention (one launch): query row i of head h attends to
+// cache positions < min(kv_len, pos_base + i + 1) of kv head h /
+// group_size.  q/out element (h, i, d) sits at h * head_stride + i *
+// row_stride + d; kt is [H_kv, dh, t_max], v is [H_kv, t_max, dh].  The
+// grid is q_tiles * heads workgroups of 64 query rows.
+typedef struct FlashArgs {
+  const void *q;
+  const void *kt;
+  const void *v;
+  void *out;
+  uint32_t t_q, t_max, kv_len, pos_base, group_size;
+  float scale;
+  uint32_t q_head_stride, q_row_stride, o_head_stride, o_row_stride;
+  uint32_t heads, q_tiles;
+} FlashArgs;
 
 // Persistent decode SwiGLU MLP chain in one launch: `layers` MLPs, layer
 // l+1 reading layer l's output y as its x.  In a layer, `a` is the dual

@@ -151,7 +151,7 @@ extern "C" __global__ __launch_bounds__(kOpThreads) void ta_norm_rows(NormArgs p
 
 // One thread per rotated pair (grid-strided): r0 = fma(x0, c, -x1 s),
 // r1 = fma(x0, s, x1 c); lanes past rot_dim are copied by the pairs of
-// their head vector.  Each element is read and written by one thread, so
+// their head vector.  A device position past the table skips the pair.  Each element is read and written by one thread, so
 // in-place is safe.
 extern "C" __global__ __launch_bounds__(kOpThreads) void ta_rope(RopeArgs p) {
   const uint32_t half = p.rot_dim / 2;
@@ -167,6 +167,8 @@ extern "C" __global__ __launch_bounds__(kOpThreads) void ta_rope(RopeArgs p) {
     const uint64_t i0 = vbase + 2 * pair;
     const float x0 = load_io(p.in, i0, f16), x1 = load_io(p.in, i0 + 1, f16);
     const uint64_t angle = ((uint64_t)(pos0 + token) * half + pair) * 2;
+    if (angle + 1 >= p.table_len)
+      continue;
     const float c = p.table[angle], s = p.table[angle + 1];
     store_io(p.out, i0, fmaf(x0, c, -x1 * s), f16);
     store_io(p.out, i0 + 1, fmaf(x0, s, x1 * c), f16);
@@ -188,6 +190,7 @@ extern "C" __global__ __launch_bounds__(kOpThreads) void ta_copy_strided(CopyArg
                        z * p.src_strides[2];
     const uint64_t d = p.dst_offset + shift + x * p.dst_strides[0] + y * p.dst_strides[1] +
                        z * p.dst_strides[2];
-    store_io(p.dst, d, load_io(p.src, s, p.src_f16 != 0), p.dst_f16 != 0);
+    if (d < p.dst_len)
+      store_io(p.dst, d, load_io(p.src, s, p.src_f16 != 0), p.dst_f16 != 0);
   }
 }

@@ -418,6 +418,109 @@ int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a, const ta_ten
   });
 }
 
+namespace {
+FlashAttentionDesc flash_desc(const ta_flash_desc &d, const std::string &fn) {
+  if (d.reserved)
+    fail(fn + ": flash.reserved must be zero");
+  FlashAttentionDesc f;
+  f.kv_len = d.kv_len;
+  f.pos_base = d.pos_base;
+  f.scale = d.scale;
+  if (d.token_major_heads)
+    f.token_major_heads = d.token_major_heads;
+  if (d.out_token_major_heads)
+    f.out_token_major_heads = d.out_token_major_heads;
+  return f;
+}
+SoftmaxMask softmax_mask(uint32_t kind, uint32_t valid_or_prefix, uint32_t rows_per_group,
+                         const std::string &fn) {
+  switch (kind) {
+  case TA_SOFTMAX_MASK_FULL:
+    return SoftmaxMask::full();
+  case TA_SOFTMAX_MASK_PREFIX:
+    return SoftmaxMask::prefix_of(valid_or_prefix);
+  case TA_SOFTMAX_MASK_CAUSAL:
+    return SoftmaxMask::causal(valid_or_prefix, rows_per_group);
+  default:
+    fail(fn + ": mask_kind " + std::to_string(kind) + " is invalid (0=full 1=prefix 2=causal)");
+  }
+}
+CopyDesc copy_desc(const ta_copy_desc &d) {
+  CopyDesc cd;
+  for (int i = 0; i < 3; ++i) {
+    cd.extent[i] = d.extent[i];
+    cd.src_strides[i] = d.src_strides[i];
+    cd.dst_strides[i] = d.dst_strides[i];
+  }
+  cd.src_offset = d.src_offset;
+  cd.dst_offset = d.dst_offset;
+  return cd;
+}
+RopeDesc rope_desc(const ta_rope_desc &d) {
+  RopeDesc rd;
+  rd.heads = d.heads;
+  rd.head_dim = d.head_dim;
+  rd.rot_dim = d.rot_dim;
+  rd.pos_base = d.pos_base;
+  return rd;
+}
+
+std::vector<ExecOp> checked_exec_ops(const ta_executor &e, const ta_exec_op *ops, size_t n,
+                                     const std::string &fn) {
+  if (n > 0 && !ops)
+    fail(fn + ": ops is null");
+  std::vector<ExecOp> out;
+  for (size_t i = 0; i < n; ++i) {
+    const std::string where = fn + ": op " + std::to_string(i);
+    const ta_exec_op &o = ops[i];
+    auto t = [&](const ta_tensor *x, const char *role) -> const Tensor & {
+      return *checked_tensor(e, x, where, role);
+    };
+    switch (o.kind) {
+    case TA_EXEC_MATMUL:
+      if (!o.matmul)
+        fail(where + ": matmul is null");
+      out.push_back(ExecOp::from_matmul(checked_ops_v3(e, o.matmul, 1, where)[0]));
+      break;
+    case TA_EXEC_RMS_NORM:
+      out.push_back(ExecOp::rms_norm(t(o.in[0], "input"), t(o.in[1], "weight"),
+                                     t(o.out, "output"), o.scalar));
+      break;
+    case TA_EXEC_LAYER_NORM:
+      out.push_back(ExecOp::layer_norm(t(o.in[0], "input"), t(o.in[1], "weight"),
+                                       t(o.in[2], "bias"), t(o.out, "output"), o.scalar));
+      break;
+    case TA_EXEC_SOFTMAX_ROWS:
+      out.push_back(ExecOp::softmax_rows(
+          t(o.in[0], "input"), t(o.out, "output"), o.scalar,
+          softmax_mask(o.mask_kind, o.valid_or_prefix, o.rows_per_group, where)));
+      break;
+    case TA_EXEC_ROPE: {
+      RopeDesc rd = rope_desc(o.rope);
+      rd.pos_addr = o.pos_addr;
+      out.push_back(ExecOp::rope_op(t(o.in[0], "input"), t(o.in[1], "table"), t(o.out, "output"),
+                                    rd));
+      break;
+    }
+    case TA_EXEC_COPY_STRIDED: {
+      CopyDesc cd = copy_desc(o.copy);
+      cd.pos_addr = o.pos_addr;
+      cd.pos_scale = o.pos_scale;
+      out.push_back(ExecOp::copy_strided(t(o.in[0], "src"), t(o.out, "dst"), cd));
+      break;
+    }
+    case TA_EXEC_FLASH_ATTENTION:
+      out.push_back(ExecOp::flash_attn(t(o.in[0], "q"), t(o.in[1], "kt"), t(o.in[2], "v"),
+                                       t(o.out, "out"), flash_desc(o.flash, where)));
+      break;
+    default:
+      fail(where + ": kind " + std::to_string(o.kind) + " is invalid");
+    }
+  }
+  return out;
+}
+} // namespace
+
 // capi/src/api/elementwise.rs: the model ops.
 int ta_softmax_rows(const ta_executor *exec, const ta_tensor *input, const ta_tensor *output,
                     float scale, uint32_t mask_kind, uint32_t valid_or_prefix,
@@ -426,20 +529,8 @@ int ta_softmax_rows(const ta_executor *exec, const ta_tensor *input, const ta_te
     const ta_executor &e = checked_ref(exec, "ta_softmax_rows: exec is null");
     const Tensor *in = checked_tensor(e, input, "ta_softmax_rows", "input");
     const Tensor *out = checked_tensor(e, output, "ta_softmax_rows", "output");
-    SoftmaxMask mask;
-    switch (mask_kind) {
-    case TA_SOFTMAX_MASK_FULL:
-      break;
-    case TA_SOFTMAX_MASK_PREFIX:
-      mask = SoftmaxMask::prefix_of(valid_or_prefix);
-      break;
-    case TA_SOFTMAX_MASK_CAUSAL:
-      mask = SoftmaxMask::causal(valid_or_prefix, rows_per_group);
-      break;
-    default:
-      fail("ta_softmax_rows: mask_kind " + std::to_string(mask_kind) +
-           " is invalid (0=full 1=prefix 2=causal)");
-    }
+    const SoftmaxMask mask =
+        softmax_mask(mask_kind, valid_or_prefix, rows_per_group, "ta_softmax_rows");
     write_stats(stats, e.exec->run_softmax_rows(*in, *out, scale, mask));
   });
 }
@@ -500,6 +591,39 @@ int ta_copy_strided(const ta_executor *exec, const ta_tensor *src, const ta_tens
     cd.src_offset = d.src_offset;
     cd.dst_offset = d.dst_offset;
     write_stats(stats, e.exec->run_copy_strided(*s_, *d_, cd));
+  });
+}
+
+
+int ta_flash_attention(const ta_executor *exec, const ta_tensor *q, const ta_tensor *kt,
+                       const ta_tensor *v, const ta_tensor *out, const ta_flash_desc *desc,
+                       ta_run_stats *stats) {
+  return ffi_status([&] {
+    const char *fn = "ta_flash_attention";
+    const ta_executor &e = checked_ref(exec, "ta_flash_attention: exec is null");
+    const Tensor *tq = checked_tensor(e, q, fn, "q");
+    const Tensor *tk = checked_tensor(e, kt, fn, "kt");
+    const Tensor *tv = checked_tensor(e, v, fn, "v");
+    const Tensor *to = checked_tensor(e, out, fn, "out");
+    const ta_flash_desc &d = checked_ref(desc, "ta_flash_attention: desc is null");
+    write_stats(stats, e.exec->run_flash_attention(*tq, *tk, *tv, *to, flash_desc(d, fn)));
+  });
+}
+
+int ta_run_exec_ops(const ta_executor *exec, const ta_exec_op *ops, size_t n_ops,
+                    ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_exec_ops: exec is null");
+    write_stats(stats, e.exec->run_exec_ops(checked_exec_ops(e, ops, n_ops, "ta_run_exec_ops")));
+  });
+}
+
+ta_prepared *ta_prepared_create_exec(const ta_executor *exec, const ta_exec_op *ops,
+                                     size_t n_ops) {
+  return ffi_create<ta_prepared>([&] {
+    const ta_executor &e = checked_ref(exec, "ta_prepared_create_exec: exec is null");
+    auto p = e.exec->prepare_exec_ops(checked_exec_ops(e, ops, n_ops, "ta_prepared_create_exec"));
+    return new ta_prepared{std::move(p), e.ctx};
   });
 }
 

@@ -14,7 +14,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <deque>
+#include <cstring>
 #include <fstream>
+#include <functional>
 #include <sstream>
 #include <sys/stat.h>
 #include <unistd.h>
@@ -146,7 +148,18 @@ struct ScratchNeed {
   }
 };
 
+// One model-op launch, planned (validated, arguments packed) before
+// anything is recorded.
+struct ElemLaunch {
+  std::string symbol;
+  uint32_t groups = 0;
+  std::vector<uint8_t> args;
+};
+
 } // namespace
+
+struct ExecutorImpl;
+ElemLaunch plan_exec_elem(ExecutorImpl &e, const ExecOp &op);
 
 struct ExecutorImpl {
   std::shared_ptr<Context> ctx;
@@ -440,11 +453,14 @@ struct ExecutorImpl {
       fu.stride_head = sd.stride_head;
       fu.stride_dim = sd.stride_dim;
       fu.pos_addr = reinterpret_cast<const uint32_t *>(sd.pos_addr);
-      if (op.store.table)
+      if (op.store.table) {
         fu.rope_table = static_cast<const float *>(op.store.table->device_ptr());
+        fu.table_len = op.store.table->len();
+      }
       if (op.store.dst) {
         fu.store_dst = op.store.dst->device_ptr();
         fu.store_dst_f16 = op.store.dst->dtype() == DType::F16 ? 1u : 0u;
+        fu.dst_len = op.store.dst->len();
       }
     }
     std::string sym = std::string(s.symbol) + (dual ? "_dual" : "") + "_m" + std::to_string(g.mr);
@@ -777,17 +793,117 @@ struct ExecutorImpl {
 
   // One model-op launch on a slot between its events
   // (elementwise/mod.rs:498-515: n_calls 1, no flops).
-  RunStats run_single(const char *symbol, uint32_t groups, void *args) {
+  RunStats run_elem(const ElemLaunch &l) {
     ctx->make_current();
     Lease lease(this);
     Slot *slot = lease.s;
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
-    launch(symbol, groups, 1, 1, 256, args, slot->stream);
+    launch(l.symbol, l.groups, 1, 1, 256, const_cast<uint8_t *>(l.args.data()), slot->stream);
     hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
     hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
     float ms = 0.f;
     hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
     return RunStats{(uint64_t)((double)ms * 1e6), 1, 0};
+  }
+
+  // ---- mixed-op graphs (src/executor/graph_ops.rs:244-620) ----
+  // Consecutive matmuls form one segment, routed like run_op_graph (pair
+  // and decode-MLP fusion stay inside a segment); each model op is one
+  // launch.  Stream order provides every op's dependency on earlier ones.
+  struct ExecStep {
+    bool matmul = false;
+    std::vector<MatmulOp> ops;
+    std::vector<ResolvedMatmul> res;
+    std::vector<OpPlan> plans;
+    ElemLaunch elem;
+  };
+  std::vector<ExecStep> plan_exec(const std::vector<ExecOp> &ops, uint64_t &flops) {
+    std::vector<ExecStep> steps;
+    for (const ExecOp &op : ops) {
+      if (op.kind == ExecOp::Kind::Matmul) {
+        validate_op(op.matmul);
+        if (steps.empty() || !steps.back().matmul) {
+          steps.emplace_back();
+          steps.back().matmul = true;
+        }
+        steps.back().ops.push_back(op.matmul);
+        steps.back().res.push_back(ResolvedMatmul::from_op(op.matmul));
+      } else {
+        steps.emplace_back();
+        steps.back().elem = plan_exec_elem(*this, op);
+      }
+    }
+    flops = 0;
+    for (ExecStep &st : steps) {
+      if (!st.matmul)
+        continue;
+      for (size_t i = 0; i < st.ops.size(); ++i)
+        st.plans.push_back(plan_op(st.ops[i], st.res[i], false));
+      mark_fusions(st.ops, st.res, st.plans);
+      for (size_t i = 0; i < st.ops.size(); ++i) {
+        check_supported(KERNEL_SPECS[st.plans[i].kernel], st.res[i]);
+        if (st.plans[i].role != 3 && st.plans[i].role != 4)
+          check_fusions(KERNEL_SPECS[st.plans[i].kernel], st.ops[i], st.res[i]);
+      }
+      flops += total_flops(st.res);
+    }
+    return steps;
+  }
+  ScratchNeed exec_need(const std::vector<ExecStep> &steps) const {
+    ScratchNeed need;
+    for (const ExecStep &st : steps)
+      if (st.matmul)
+        need.merge(total_need(st.res, st.plans));
+    return need;
+  }
+  static bool exec_has_mlp(const std::vector<ExecStep> &steps) {
+    for (const ExecStep &st : steps)
+      if (st.matmul && has_mlp(st.plans))
+        return true;
+    return false;
+  }
+  void record_exec(const std::vector<ExecStep> &steps, Scratch &scratch, uint32_t *status,
+                   hipStream_t stream) const {
+    for (const ExecStep &st : steps) {
+      if (st.matmul)
+        record(st.ops, st.res, st.plans, scratch, status, stream);
+      else
+        launch(st.elem.symbol, st.elem.groups, 1, 1, 256,
+               const_cast<uint8_t *>(st.elem.args.data()), stream);
+    }
+  }
+  RunStats run_exec_impl(const std::vector<ExecOp> &ops) {
+    if (ops.empty())
+      fail("run_exec_ops: empty op list");
+    ctx->make_current();
+    uint64_t flops = 0;
+    const std::vector<ExecStep> steps = plan_exec(ops, flops);
+    Lease lease(this);
+    Slot *slot = lease.s;
+    const ScratchNeed need = exec_need(steps);
+    slot->scratch.ensure(need.splitk, need.partial, need.counters);
+    slot->scratch.ensure_mlp(need.mlp);
+    hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
+    record_exec(steps, slot->scratch, slot->host_status, slot->stream);
+    hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
+    hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
+    if (exec_has_mlp(steps))
+      check_host_status(slot->host_status, slot->scratch.mlp, slot->scratch.mlp_bytes);
+    return RunStats{(uint64_t)((double)ms * 1e6), ops.size(), flops};
+  }
+  std::unique_ptr<PreparedOps> prepare_exec_impl(const Executor *owner,
+                                                 const std::vector<ExecOp> &ops) {
+    if (ops.empty())
+      fail("prepare_exec_ops: empty op list");
+    ctx->make_current();
+    uint64_t flops = 0;
+    auto steps = std::make_shared<std::vector<ExecStep>>(plan_exec(ops, flops));
+    return capture(owner, ops.size(), flops, exec_need(*steps), exec_has_mlp(*steps),
+                   [this, steps](Scratch &scratch, uint32_t *status, hipStream_t stream) {
+                     record_exec(*steps, scratch, status, stream);
+                   });
   }
 
   // ---- tuning (src/executor/tuning.rs) ----
@@ -1023,9 +1139,20 @@ struct ExecutorImpl {
     for (size_t i = 0; i < ops.size(); ++i)
       check_supported(KERNEL_SPECS[plans[i].kernel], res[i]);
 
+    return capture(owner, ops.size(), flops, total_need(res, plans), has_mlp(plans),
+                   [&](Scratch &scratch, uint32_t *status, hipStream_t stream) {
+                     record(ops, res, plans, scratch, status, stream);
+                   });
+  }
+
+  // Record once into a hipGraph on a private stream, with graph-owned
+  // scratch zeroed outside the capture (no memset nodes).
+  std::unique_ptr<PreparedOps>
+  capture(const Executor *owner, size_t n_calls, uint64_t flops, const ScratchNeed &need,
+          bool mlp, const std::function<void(Scratch &, uint32_t *, hipStream_t)> &rec) {
     std::unique_ptr<PreparedOps> p(new PreparedOps());
     p->exec_ = owner;
-    p->n_calls_ = ops.size();
+    p->n_calls_ = n_calls;
     p->flops_ = flops;
     hipStream_t stream = nullptr;
     hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
@@ -1035,22 +1162,20 @@ struct ExecutorImpl {
     p->ev_start_ = e0;
     hip_check(hipEventCreate(&e1), "hipEventCreate");
     p->ev_end_ = e1;
-    // Graph-owned scratch, zeroed outside the capture (no memset nodes).
     Scratch scratch;
-    ScratchNeed need = total_need(res, plans);
     scratch.ensure(need.splitk, need.partial, need.counters);
     scratch.ensure_mlp(need.mlp);
     p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters, scratch.mlp};
     p->mlp_scratch_ = scratch.mlp;
     p->mlp_bytes_ = scratch.mlp_bytes;
-    if (has_mlp(plans))
+    if (mlp)
       p->status_ = alloc_host_status();
 
     hipGraph_t g = nullptr;
     hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal),
               "hipStreamBeginCapture");
     try {
-      record(ops, res, plans, scratch, static_cast<uint32_t *>(p->status_), stream);
+      rec(scratch, static_cast<uint32_t *>(p->status_), stream);
     } catch (...) {
       (void)hipStreamEndCapture(stream, &g);
       if (g)
@@ -1185,13 +1310,20 @@ uint32_t grid_for(uint64_t items, uint32_t per_group, uint32_t cus) {
   return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((items + per_group - 1) / per_group,
                                                             64ull * cus));
 }
-} // namespace
+template <class T> ElemLaunch elem(const char *symbol, uint32_t groups, const T &args) {
+  ElemLaunch l;
+  l.symbol = symbol;
+  l.groups = groups;
+  l.args.resize(sizeof(T));
+  std::memcpy(l.args.data(), &args, sizeof(T));
+  return l;
+}
 
-RunStats Executor::run_softmax_rows(const Tensor &input, const Tensor &output, float scale,
-                                    SoftmaxMask mask) const {
+ElemLaunch plan_softmax(ExecutorImpl &e, const Tensor &input, const Tensor &output, float scale,
+                        SoftmaxMask mask) {
   const std::string op = "run_softmax_rows";
-  impl_->validate_tensor(&input, "input");
-  impl_->validate_tensor(&output, "output");
+  e.validate_tensor(&input, "input");
+  e.validate_tensor(&output, "output");
   ensure_f32(input, op, "input");
   ensure_f32(output, op, "output");
   ensure_same_shape(op, input, output);
@@ -1219,12 +1351,11 @@ RunStats Executor::run_softmax_rows(const Tensor &input, const Tensor &output, f
     a.causal = 1;
     break;
   }
-  return impl_->run_single("ta_softmax_rows", grid_for(rows, 1, impl_->ctx->cu_count()), &a);
+  return elem("ta_softmax_rows", grid_for(rows, 1, e.ctx->cu_count()), a);
 }
 
-static RunStats run_norm(ExecutorImpl &e, const std::string &op, const Tensor &input,
-                         const Tensor &weight, const Tensor *bias, const Tensor &output,
-                         float eps) {
+ElemLaunch plan_norm(ExecutorImpl &e, const std::string &op, const Tensor &input,
+                     const Tensor &weight, const Tensor *bias, const Tensor &output, float eps) {
   e.validate_tensor(&input, "input");
   e.validate_tensor(&output, "output");
   e.validate_tensor(&weight, "weight");
@@ -1253,25 +1384,15 @@ static RunStats run_norm(ExecutorImpl &e, const std::string &op, const Tensor &i
   a.cols = cols;
   a.eps = eps;
   a.io_f16 = f16 ? 1u : 0u;
-  return e.run_single("ta_norm_rows", grid_for(rows, 1, e.ctx->cu_count()), &a);
+  return elem("ta_norm_rows", grid_for(rows, 1, e.ctx->cu_count()), a);
 }
 
-RunStats Executor::run_rms_norm(const Tensor &input, const Tensor &weight, const Tensor &output,
-                                float eps) const {
-  return run_norm(*impl_, "run_rms_norm", input, weight, nullptr, output, eps);
-}
-
-RunStats Executor::run_layer_norm(const Tensor &input, const Tensor &weight, const Tensor &bias,
-                                  const Tensor &output, float eps) const {
-  return run_norm(*impl_, "run_layer_norm", input, weight, &bias, output, eps);
-}
-
-RunStats Executor::run_rope(const Tensor &input, const Tensor &table, const Tensor &output,
-                            const RopeDesc &desc) const {
+ElemLaunch plan_rope(ExecutorImpl &e, const Tensor &input, const Tensor &table,
+                     const Tensor &output, const RopeDesc &desc) {
   const std::string op = "run_rope";
-  impl_->validate_tensor(&input, "input");
-  impl_->validate_tensor(&output, "output");
-  impl_->validate_tensor(&table, "table");
+  e.validate_tensor(&input, "input");
+  e.validate_tensor(&output, "output");
+  e.validate_tensor(&table, "table");
   const bool f16 = io_f16(op, input, output);
   ensure_f32(table, op, "table");
   ensure_same_shape(op, input, output);
@@ -1302,20 +1423,20 @@ RunStats Executor::run_rope(const Tensor &input, const Tensor &table, const Tens
   a.rot_dim = desc.rot_dim;
   a.pos_base = desc.pos_base;
   a.io_f16 = f16 ? 1u : 0u;
+  a.table_len = table.len();
   const uint64_t pairs = tokens * desc.heads * (desc.rot_dim / 2);
-  return impl_->run_single("ta_rope", grid_for(pairs, 256, impl_->ctx->cu_count()), &a);
+  return elem("ta_rope", grid_for(pairs, 256, e.ctx->cu_count()), a);
 }
 
-RunStats Executor::run_copy_strided(const Tensor &src, const Tensor &dst,
-                                    const CopyDesc &desc) const {
+ElemLaunch plan_copy(ExecutorImpl &e, const Tensor &src, const Tensor &dst, const CopyDesc &desc) {
   const std::string op = "run_copy_strided";
-  impl_->validate_tensor(&src, "src");
-  impl_->validate_tensor(&dst, "dst");
+  e.validate_tensor(&src, "src");
+  e.validate_tensor(&dst, "dst");
   // ops.rs:387-437.
   if (src.buffer_id() == dst.buffer_id())
     fail(op + ": src and dst must be different tensors");
-  for (uint32_t e : desc.extent)
-    if (e == 0)
+  for (uint32_t x : desc.extent)
+    if (x == 0)
       fail(op + ": extent [" + std::to_string(desc.extent[0]) + ", " +
            std::to_string(desc.extent[1]) + ", " + std::to_string(desc.extent[2]) +
            "] has a zero axis");
@@ -1350,7 +1471,178 @@ RunStats Executor::run_copy_strided(const Tensor &src, const Tensor &dst,
   a.pos_scale = desc.pos_scale;
   a.src_f16 = src.dtype() == DType::F16 ? 1u : 0u;
   a.dst_f16 = dst.dtype() == DType::F16 ? 1u : 0u;
-  return impl_->run_single("ta_copy_strided", grid_for(total, 256, impl_->ctx->cu_count()), &a);
+  a.dst_len = dst.len();
+  return elem("ta_copy_strided", grid_for(total, 256, e.ctx->cu_count()), a);
+}
+
+// flash.rs:66-250 (plan_flash_attention): the same checks in the same
+// order, then the head-dimension / storage variant.
+ElemLaunch plan_flash(ExecutorImpl &e, const Tensor &q, const Tensor &kt, const Tensor &v,
+                      const Tensor &out, const FlashAttentionDesc &desc) {
+  const std::string op = "run_flash_attention";
+  e.validate_tensor(&q, "q");
+  e.validate_tensor(&out, "out");
+  const bool io16 = io_f16(op, q, out);
+  e.validate_tensor(&kt, "kt");
+  e.validate_tensor(&v, "v");
+  if (kt.dtype() != v.dtype())
+    fail(op + ": kt (" + dtype_name(kt.dtype()) + ") and v (" + dtype_name(v.dtype()) +
+         ") must share a storage type");
+  const bool kv16 = kt.dtype() == DType::F16;
+  if (kt.shape().size() != 3)
+    fail(op + ": kt must be [H_kv, dh, T_max], got " + fmt_shape(kt.shape()));
+  if (v.shape().size() != 3)
+    fail(op + ": v must be [H_kv, T_max, dh], got " + fmt_shape(v.shape()));
+  const uint32_t kv_heads = kt.shape()[0], dh = kt.shape()[1], t_max = kt.shape()[2];
+  if (v.shape()[1] != t_max || v.shape()[0] != kv_heads || v.shape()[2] != dh)
+    fail(op + ": inconsistent cache shapes kt " + fmt_shape(kt.shape()) + ", v " +
+         fmt_shape(v.shape()));
+  uint32_t heads = 0, t_q = 0, q_hs = 0, q_rs = 0;
+  if (desc.token_major_heads) {
+    heads = *desc.token_major_heads;
+    if (heads == 0)
+      fail(op + ": token_major_heads must be nonzero");
+    t_q = q.shape().empty() ? 0 : q.shape()[0];
+    const uint64_t want = (uint64_t)t_q * heads * dh;
+    if (t_q == 0 || q.len() != want)
+      fail(op + ": token-major q " + fmt_shape(q.shape()) + " does not hold [T=" +
+           std::to_string(t_q) + ", H=" + std::to_string(heads) + ", dh=" + std::to_string(dh) +
+           "]");
+    q_hs = dh;
+    q_rs = heads * dh;
+  } else {
+    if (q.shape().size() != 3)
+      fail(op + ": q must be [H, T_q, dh], got " + fmt_shape(q.shape()));
+    heads = q.shape()[0];
+    t_q = q.shape()[1];
+    if (q.shape()[2] != dh)
+      fail(op + ": q dh " + std::to_string(q.shape()[2]) + " != cache dh " + std::to_string(dh) +
+           " (q " + fmt_shape(q.shape()) + ", kt " + fmt_shape(kt.shape()) + ")");
+    q_hs = t_q * dh;
+    q_rs = dh;
+  }
+  uint32_t o_hs = q_hs, o_rs = q_rs;
+  if (desc.out_token_major_heads) {
+    const uint32_t oh = *desc.out_token_major_heads;
+    if (oh == 0)
+      fail(op + ": out_token_major_heads must be nonzero");
+    if (oh != heads)
+      fail(op + ": out_token_major_heads " + std::to_string(oh) + " != q heads " +
+           std::to_string(heads));
+    if (out.len() != (uint64_t)t_q * oh * dh)
+      fail(op + ": token-major out " + fmt_shape(out.shape()) + " does not hold [T=" +
+           std::to_string(t_q) + ", H=" + std::to_string(oh) + ", dh=" + std::to_string(dh) +
+           "]");
+    o_hs = dh;
+    o_rs = oh * dh;
+  } else if (desc.token_major_heads) {
+    if (out.len() != q.len())
+      fail(op + ": out shape " + fmt_shape(out.shape()) + " must match token-major q " +
+           fmt_shape(q.shape()));
+  } else if (out.shape() != q.shape()) {
+    fail(op + ": out shape " + fmt_shape(out.shape()) + " must equal q shape " +
+         fmt_shape(q.shape()));
+  }
+  if (kv_heads == 0 || heads % kv_heads != 0)
+    fail(op + ": H=" + std::to_string(heads) + " must be a multiple of H_kv=" +
+         std::to_string(kv_heads));
+  if (desc.kv_len > t_max)
+    fail(op + ": kv_len " + std::to_string(desc.kv_len) + " exceeds cache T_max " +
+         std::to_string(t_max));
+  if (dh != 64 && dh != 128)
+    fail(op + ": head dimension " + std::to_string(dh) +
+         " unsupported (compiled variants: 64, 128)");
+  if (io16 && !kv16)
+    fail(op + ": f16 q/out are compiled for f16 KV caches only (kv " + dtype_name(kt.dtype()) +
+         ", dh " + std::to_string(dh) + ")");
+  FlashArgs a{};
+  a.q = q.device_ptr();
+  a.kt = kt.device_ptr();
+  a.v = v.device_ptr();
+  a.out = out.device_ptr();
+  a.t_q = t_q;
+  a.t_max = t_max;
+  a.kv_len = desc.kv_len;
+  a.pos_base = desc.pos_base;
+  a.group_size = heads / kv_heads;
+  a.scale = desc.scale;
+  a.q_head_stride = q_hs;
+  a.q_row_stride = q_rs;
+  a.o_head_stride = o_hs;
+  a.o_row_stride = o_rs;
+  a.heads = heads;
+  a.q_tiles = (t_q + 63) / 64;
+  const uint64_t groups = (uint64_t)a.q_tiles * heads;
+  if (groups == 0 || groups > UINT32_MAX)
+    fail(op + ": empty or oversized launch (T_q " + std::to_string(t_q) + ", H " +
+         std::to_string(heads) + ")");
+  const char *sym = io16 ? (dh == 64 ? "ta_flash_attention_io16_dh64"
+                                     : "ta_flash_attention_io16_dh128")
+                   : kv16 ? (dh == 64 ? "ta_flash_attention_kv16_dh64"
+                                      : "ta_flash_attention_kv16_dh128")
+                          : (dh == 64 ? "ta_flash_attention_dh64" : "ta_flash_attention_dh128");
+  return elem(sym, (uint32_t)groups, a);
+}
+} // namespace
+
+ElemLaunch plan_exec_elem(ExecutorImpl &e, const ExecOp &op) {
+  auto need = [&](const Tensor *t, const char *role) -> const Tensor & {
+    if (!t)
+      fail(std::string("run_exec_ops: ") + role + " tensor is null");
+    return *t;
+  };
+  switch (op.kind) {
+  case ExecOp::Kind::RmsNorm:
+    return plan_norm(e, "run_rms_norm", need(op.in[0], "input"), need(op.in[1], "weight"),
+                     nullptr, need(op.out, "output"), op.scalar);
+  case ExecOp::Kind::LayerNorm:
+    return plan_norm(e, "run_layer_norm", need(op.in[0], "input"), need(op.in[1], "weight"),
+                     &need(op.in[2], "bias"), need(op.out, "output"), op.scalar);
+  case ExecOp::Kind::SoftmaxRows:
+    return plan_softmax(e, need(op.in[0], "input"), need(op.out, "output"), op.scalar, op.mask);
+  case ExecOp::Kind::Rope:
+    return plan_rope(e, need(op.in[0], "input"), need(op.in[1], "table"), need(op.out, "output"),
+                     op.rope);
+  case ExecOp::Kind::CopyStrided:
+    return plan_copy(e, need(op.in[0], "src"), need(op.out, "dst"), op.copy);
+  case ExecOp::Kind::FlashAttn:
+    return plan_flash(e, need(op.in[0], "q"), need(op.in[1], "kt"), need(op.in[2], "v"),
+                      need(op.out, "out"), op.flash);
+  case ExecOp::Kind::Matmul:
+    break;
+  }
+  fail("internal: plan_exec_elem on a matmul step");
+}
+
+RunStats Executor::run_softmax_rows(const Tensor &input, const Tensor &output, float scale,
+                                    SoftmaxMask mask) const {
+  return impl_->run_elem(plan_softmax(*impl_, input, output, scale, mask));
+}
+RunStats Executor::run_rms_norm(const Tensor &input, const Tensor &weight, const Tensor &output,
+                                float eps) const {
+  return impl_->run_elem(plan_norm(*impl_, "run_rms_norm", input, weight, nullptr, output, eps));
+}
+RunStats Executor::run_layer_norm(const Tensor &input, const Tensor &weight, const Tensor &bias,
+                                  const Tensor &output, float eps) const {
+  return impl_->run_elem(plan_norm(*impl_, "run_layer_norm", input, weight, &bias, output, eps));
+}
+RunStats Executor::run_rope(const Tensor &input, const Tensor &table, const Tensor &output,
+                            const RopeDesc &desc) const {
+  return impl_->run_elem(plan_rope(*impl_, input, table, output, desc));
+}
+RunStats Executor::run_copy_strided(const Tensor &src, const Tensor &dst,
+                                    const CopyDesc &desc) const {
+  return impl_->run_elem(plan_copy(*impl_, src, dst, desc));
+}
+RunStats Executor::run_flash_attention(const Tensor &q, const Tensor &kt, const Tensor &v,
+                                       const Tensor &out, const FlashAttentionDesc &desc) const {
+  return impl_->run_elem(plan_flash(*impl_, q, kt, v, out, desc));
+}
+RunStats Executor::run_exec_ops(const std::vector<ExecOp> &ops) const {
+  return impl_->run_exec_impl(ops);
+}
+std::unique_ptr<PreparedOps> Executor::prepare_exec_ops(const std::vector<ExecOp> &ops) const {
+  return impl_->prepare_exec_impl(this, ops);
 }
 
 std::unique_ptr<PreparedOps> Executor::prepare_matmuls(const std::vector<MatmulCall> &calls) const {

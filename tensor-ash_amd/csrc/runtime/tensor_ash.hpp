@@ -201,6 +201,87 @@ struct CopyDesc {
   uint32_t pos_scale = 0;
 };
 
+// Causal prefill attention geometry (src/executor/elementwise/mod.rs:
+// 160-184).  q/out default to head-major [H, T_q, dh]; token_major_heads
+// = H reads q (and, unless out_token_major_heads says otherwise, writes
+// out) as token-major [T, H*dh] / [T, H, dh].
+struct FlashAttentionDesc {
+  uint32_t kv_len = 0;   // valid cache positions
+  uint32_t pos_base = 0; // absolute position of query row 0
+  float scale = 1.0f;    // 1/sqrt(dh) for standard attention
+  std::optional<uint32_t> token_major_heads;
+  std::optional<uint32_t> out_token_major_heads;
+};
+
+// One step of a mixed-op graph (src/executor/graph_ops.rs:23-171): ops run
+// in list order and each sees every earlier op's writes.  Operand roles:
+//   Matmul      `matmul`
+//   RmsNorm     in[0] input, in[1] weight, out output, scalar eps
+//   LayerNorm   in[0] input, in[1] weight, in[2] bias, out, scalar eps
+//   SoftmaxRows in[0] input, out, scalar scale, mask
+//   Rope        in[0] input, in[1] table, out, rope
+//   CopyStrided in[0] src, out dst, copy
+//   FlashAttn   in[0] q, in[1] kt, in[2] v, out, flash
+struct ExecOp {
+  enum class Kind { Matmul, RmsNorm, LayerNorm, SoftmaxRows, Rope, CopyStrided, FlashAttn };
+  Kind kind = Kind::Matmul;
+  MatmulOp matmul;
+  std::array<const Tensor *, 3> in{};
+  const Tensor *out = nullptr;
+  float scalar = 0.0f;
+  SoftmaxMask mask;
+  RopeDesc rope;
+  CopyDesc copy;
+  FlashAttentionDesc flash;
+
+  static ExecOp from_matmul(const MatmulOp &op) {
+    ExecOp e;
+    e.matmul = op;
+    return e;
+  }
+  static ExecOp rms_norm(const Tensor &input, const Tensor &weight, const Tensor &output,
+                         float eps) {
+    return make(Kind::RmsNorm, {&input, &weight, nullptr}, &output, eps);
+  }
+  static ExecOp layer_norm(const Tensor &input, const Tensor &weight, const Tensor &bias,
+                           const Tensor &output, float eps) {
+    return make(Kind::LayerNorm, {&input, &weight, &bias}, &output, eps);
+  }
+  static ExecOp softmax_rows(const Tensor &input, const Tensor &output, float scale,
+                             SoftmaxMask mask) {
+    ExecOp e = make(Kind::SoftmaxRows, {&input, nullptr, nullptr}, &output, scale);
+    e.mask = mask;
+    return e;
+  }
+  static ExecOp rope_op(const Tensor &input, const Tensor &table, const Tensor &output,
+                        const RopeDesc &desc) {
+    ExecOp e = make(Kind::Rope, {&input, &table, nullptr}, &output, 0.0f);
+    e.rope = desc;
+    return e;
+  }
+  static ExecOp copy_strided(const Tensor &src, const Tensor &dst, const CopyDesc &desc) {
+    ExecOp e = make(Kind::CopyStrided, {&src, nullptr, nullptr}, &dst, 0.0f);
+    e.copy = desc;
+    return e;
+  }
+  static ExecOp flash_attn(const Tensor &q, const Tensor &kt, const Tensor &v, const Tensor &out,
+                           const FlashAttentionDesc &desc) {
+    ExecOp e = make(Kind::FlashAttn, {&q, &kt, &v}, &out, 0.0f);
+    e.flash = desc;
+    return e;
+  }
+
+private:
+  static ExecOp make(Kind k, std::array<const Tensor *, 3> in, const Tensor *out, float scalar) {
+    ExecOp e;
+    e.kind = k;
+    e.in = in;
+    e.out = out;
+    e.scalar = scalar;
+    return e;
+  }
+};
+
 // src/matmul/api.rs:311-353.
 struct RunStats {
   std::optional<uint64_t> gpu_time_ns;
@@ -368,6 +449,15 @@ public:
   RunStats run_rope(const Tensor &input, const Tensor &table, const Tensor &output,
                     const RopeDesc &desc) const;
   RunStats run_copy_strided(const Tensor &src, const Tensor &dst, const CopyDesc &desc) const;
+  // src/executor/elementwise/flash.rs:13-250: kt [H_kv, dh, T_max],
+  // v [H_kv, T_max, dh], dh 64 or 128, H a multiple of H_kv.
+  RunStats run_flash_attention(const Tensor &q, const Tensor &kt, const Tensor &v,
+                               const Tensor &out, const FlashAttentionDesc &desc) const;
+
+  // Mixed-op graphs (src/executor/graph_ops.rs:244-336): every op is
+  // validated and planned before anything is launched.
+  RunStats run_exec_ops(const std::vector<ExecOp> &ops) const;
+  std::unique_ptr<PreparedOps> prepare_exec_ops(const std::vector<ExecOp> &ops) const;
 
   std::unique_ptr<PreparedOps> prepare_matmuls(const std::vector<MatmulCall> &calls) const;
   std::unique_ptr<PreparedOps> prepare_ops(const std::vector<MatmulOp> &ops) const;

@@ -79,6 +79,20 @@ class _CopyDesc(C.Structure):
                 ("dst_offset", C.c_uint32), ("dst_strides", C.c_uint32 * 3)]
 
 
+class _FlashDesc(C.Structure):
+    _fields_ = [("kv_len", C.c_uint32), ("pos_base", C.c_uint32), ("scale", C.c_float),
+                ("token_major_heads", C.c_uint32), ("out_token_major_heads", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+class _ExecOp(C.Structure):
+    _fields_ = [("kind", C.c_uint32), ("mask_kind", C.c_uint32), ("valid_or_prefix", C.c_uint32),
+                ("rows_per_group", C.c_uint32), ("scalar", C.c_float), ("pos_scale", C.c_uint32),
+                ("pos_addr", C.c_uint64), ("inp", C.c_void_p * 3), ("out", C.c_void_p),
+                ("matmul", C.POINTER(_OpV3)), ("rope", _RopeDesc), ("copy", _CopyDesc),
+                ("flash", _FlashDesc)]
+
+
 class _DispatchInfo(C.Structure):
     _fields_ = [("kernel", C.c_char_p), ("tile", C.c_uint32 * 3), ("has_split_k2", C.c_uint32),
                 ("split_k2_splits", C.c_uint32)]
@@ -126,6 +140,9 @@ _sig("ta_run_ops_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
 _sig("ta_run_op_graph_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
 _sig("ta_prepared_create_v3", P, P, C.POINTER(_OpV3), sz, u32)
 _sig("ta_tensor_device_address", u64, P)
+_sig("ta_flash_attention", C.c_int, P, P, P, P, P, C.POINTER(_FlashDesc), C.POINTER(RunStats))
+_sig("ta_run_exec_ops", C.c_int, P, C.POINTER(_ExecOp), sz, C.POINTER(RunStats))
+_sig("ta_prepared_create_exec", P, P, C.POINTER(_ExecOp), sz)
 _sig("ta_softmax_rows", C.c_int, P, P, P, f32, u32, u32, u32, C.POINTER(RunStats))
 _sig("ta_rms_norm", C.c_int, P, P, P, P, f32, C.POINTER(RunStats))
 _sig("ta_layer_norm", C.c_int, P, P, P, P, P, f32, C.POINTER(RunStats))
@@ -323,11 +340,122 @@ def _ops_array(ops: Sequence[MatmulOp]):
     return (_Op * len(ops))(*[o._raw() for o in ops]), 1
 
 
+SOFTMAX_MASK_FULL, SOFTMAX_MASK_PREFIX, SOFTMAX_MASK_CAUSAL = 0, 1, 2
+EXEC_MATMUL, EXEC_RMS_NORM, EXEC_LAYER_NORM, EXEC_SOFTMAX_ROWS, EXEC_ROPE, EXEC_COPY_STRIDED, \
+    EXEC_FLASH_ATTENTION = range(7)
+
+
+@dataclass
+class RopeDesc:
+    """src/executor/elementwise/mod.rs RopeDesc; pos_addr: device address of
+    a u32 position cell added to pos_base when the op runs (graphs only)."""
+    heads: int
+    head_dim: int
+    rot_dim: int
+    pos_base: int = 0
+    pos_addr: int = 0
+
+
+@dataclass
+class CopyDesc:
+    """src/executor/elementwise/mod.rs CopyDesc; pos_addr / pos_scale (graphs
+    only): the cell's value times pos_scale is added to dst_offset."""
+    extent: Sequence[int]
+    src_strides: Sequence[int]
+    dst_strides: Sequence[int]
+    src_offset: int = 0
+    dst_offset: int = 0
+    pos_addr: int = 0
+    pos_scale: int = 0
+
+    def _raw(self) -> _CopyDesc:
+        return _CopyDesc((C.c_uint32 * 3)(*self.extent), self.src_offset, (C.c_uint32 * 3)(*self.src_strides),
+                         self.dst_offset, (C.c_uint32 * 3)(*self.dst_strides))
+
+
+@dataclass
+class FlashAttentionDesc:
+    """src/executor/elementwise/mod.rs:160-184."""
+    kv_len: int
+    pos_base: int = 0
+    scale: float = 1.0
+    token_major_heads: Optional[int] = None
+    out_token_major_heads: Optional[int] = None
+
+    def _raw(self) -> _FlashDesc:
+        return _FlashDesc(self.kv_len, self.pos_base, self.scale, self.token_major_heads or 0,
+                          self.out_token_major_heads or 0, 0)
+
+
+class ExecOp:
+    """One step of a mixed-op graph (src/executor/graph_ops.rs:23-171)."""
+
+    def __init__(self, kind: int, keep=(), **fields):
+        self.kind = kind
+        self._fields = fields
+        self._keep = list(keep)
+
+    def _raw(self) -> _ExecOp:
+        r = _ExecOp(kind=self.kind)
+        for k, v in self._fields.items():
+            if k == "inp":
+                for i, t in enumerate(v):
+                    r.inp[i] = t.handle if t is not None else None
+            elif k == "out":
+                r.out = v.handle
+            else:
+                setattr(r, k, v)
+        return r
+
+    @staticmethod
+    def matmul(op: "MatmulOp") -> "ExecOp":
+        raw = op._raw_v3()
+        return ExecOp(EXEC_MATMUL, keep=[op, raw], matmul=C.pointer(raw))
+
+    @staticmethod
+    def rms_norm(input, weight, output, eps) -> "ExecOp":
+        return ExecOp(EXEC_RMS_NORM, keep=[input, weight, output], inp=[input, weight], out=output, scalar=eps)
+
+    @staticmethod
+    def layer_norm(input, weight, bias, output, eps) -> "ExecOp":
+        return ExecOp(EXEC_LAYER_NORM, keep=[input, weight, bias, output], inp=[input, weight, bias], out=output,
+                      scalar=eps)
+
+    @staticmethod
+    def softmax_rows(input, output, scale, mask_kind=SOFTMAX_MASK_FULL, valid_or_prefix=0,
+                     rows_per_group=0) -> "ExecOp":
+        return ExecOp(EXEC_SOFTMAX_ROWS, keep=[input, output], inp=[input], out=output, scalar=scale,
+                      mask_kind=mask_kind, valid_or_prefix=valid_or_prefix, rows_per_group=rows_per_group)
+
+    @staticmethod
+    def rope(input, table, output, desc: RopeDesc) -> "ExecOp":
+        return ExecOp(EXEC_ROPE, keep=[input, table, output], inp=[input, table], out=output,
+                      rope=_RopeDesc(desc.heads, desc.head_dim, desc.rot_dim, desc.pos_base),
+                      pos_addr=desc.pos_addr)
+
+    @staticmethod
+    def copy_strided(src, dst, desc: CopyDesc) -> "ExecOp":
+        return ExecOp(EXEC_COPY_STRIDED, keep=[src, dst], inp=[src], out=dst, copy=desc._raw(),
+                      pos_addr=desc.pos_addr, pos_scale=desc.pos_scale)
+
+    @staticmethod
+    def flash_attn(q, kt, v, out, desc: FlashAttentionDesc) -> "ExecOp":
+        return ExecOp(EXEC_FLASH_ATTENTION, keep=[q, kt, v, out], inp=[q, kt, v], out=out, flash=desc._raw())
+
+
+def _exec_array(ops: Sequence[ExecOp]):
+    return (_ExecOp * len(ops))(*[o._raw() for o in ops])
+
+
 class Prepared:
-    def __init__(self, exec_: "Executor", ops: Sequence[MatmulOp], as_graph: bool):
-        arr, ver = _ops_array(ops)
-        fn = {1: _lib.ta_prepared_create, 2: _lib.ta_prepared_create_v2, 3: _lib.ta_prepared_create_v3}[ver]
-        self._h = _checkp(fn(exec_.handle, arr, len(ops), int(as_graph)))
+    def __init__(self, exec_: "Executor", ops: Sequence, as_graph: bool, exec_ops: bool = False):
+        if exec_ops:
+            arr = _exec_array(ops)
+            self._h = _checkp(_lib.ta_prepared_create_exec(exec_.handle, arr, len(ops)))
+        else:
+            arr, ver = _ops_array(ops)
+            fn = {1: _lib.ta_prepared_create, 2: _lib.ta_prepared_create_v2, 3: _lib.ta_prepared_create_v3}[ver]
+            self._h = _checkp(fn(exec_.handle, arr, len(ops), int(as_graph)))
         self._keep = (exec_, list(ops))
 
     def run(self) -> RunStats:
@@ -462,6 +590,22 @@ class Executor:
 
     def prepare_op_graph(self, ops: Sequence[MatmulOp]) -> Prepared:
         return Prepared(self, ops, True)
+
+    # ---- causal prefill attention and mixed-op graphs ----
+    def flash_attention(self, q: Tensor, kt: Tensor, v: Tensor, out: Tensor, desc: FlashAttentionDesc) -> RunStats:
+        st = RunStats()
+        d = desc._raw()
+        _check(_lib.ta_flash_attention(self._h, q.handle, kt.handle, v.handle, out.handle, C.byref(d), C.byref(st)))
+        return st
+
+    def run_exec_ops(self, ops: Sequence[ExecOp]) -> RunStats:
+        arr = _exec_array(ops)
+        st = RunStats()
+        _check(_lib.ta_run_exec_ops(self._h, arr, len(ops), C.byref(st)))
+        return st
+
+    def prepare_exec_ops(self, ops: Sequence[ExecOp]) -> Prepared:
+        return Prepared(self, ops, True, exec_ops=True)
 
     def dispatch_info_for(self, batch: int, m: int, n: int, k: int, b_f16: bool = False) -> dict:
         info = _DispatchInfo()

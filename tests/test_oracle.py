@@ -393,3 +393,53 @@ def test_copy_strided_pinned(oracle):
                                 (t_max, dh * t_max, 0)).reshape(heads, dh, t_max)
     assert np.array_equal(cache[:, :, step], k.reshape(heads, dh))
     assert np.count_nonzero(cache) == np.count_nonzero(k)
+
+
+def test_flash_attention_pinned(oracle):
+    """flash_attention pinned three ways: a scalar triple loop restating
+    cpu_flash (flash.rs:10-61) on a tiny GQA case with an offset; torch's
+    scaled_dot_product_attention in f64 with an explicit boolean mask on a
+    larger case; and closed forms (kv_len 1 returns V[0]; scale 0 returns
+    the mean of the valid V rows)."""
+    import math
+    import torch
+    heads, kv_heads, t_q, t_max, dh, kv_len, pos_base = 4, 2, 5, 12, 8, 9, 4
+    q = oracle.fill_det(heads * t_q * dh, 2500)
+    kt = oracle.fill_det(kv_heads * dh * t_max, 2501)
+    v = oracle.fill_det(kv_heads * t_max * dh, 2502)
+    got = oracle.flash_attention(q, kt, v, heads, kv_heads, t_q, t_max, dh, kv_len, pos_base, 0.35)
+    want = np.zeros(heads * t_q * dh)
+    for h in range(heads):
+        kh = h // (heads // kv_heads)
+        for i in range(t_q):
+            valid = min(kv_len, pos_base + i + 1)
+            sc = [sum(float(q[(h * t_q + i) * dh + d]) * float(kt[(kh * dh + d) * t_max + p]) for d in range(dh))
+                  * float(np.float32(0.35)) for p in range(valid)]
+            mx = max(sc)
+            e = [math.exp(x - mx) for x in sc]
+            tot = sum(e)
+            for d in range(dh):
+                want[(h * t_q + i) * dh + d] = sum(e[p] / tot * float(v[(kh * t_max + p) * dh + d])
+                                                   for p in range(valid))
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
+
+    heads, kv_heads, t_q, t_max, dh, kv_len, pos_base = 8, 2, 70, 128, 64, 100, 30
+    q = oracle.fill_det(heads * t_q * dh, 2510)
+    kt = oracle.fill_det(kv_heads * dh * t_max, 2511)
+    v = oracle.fill_det(kv_heads * t_max * dh, 2512)
+    got = oracle.flash_attention(q, kt, v, heads, kv_heads, t_q, t_max, dh, kv_len, pos_base, 0.125)
+    tq = torch.from_numpy(q.reshape(heads, t_q, dh)).double()
+    tk = torch.from_numpy(kt.reshape(kv_heads, dh, t_max)).double().transpose(1, 2).repeat_interleave(4, 0)
+    tv = torch.from_numpy(v.reshape(kv_heads, t_max, dh)).double().repeat_interleave(4, 0)
+    mask = torch.arange(t_max)[None, :] < torch.clamp(torch.arange(t_q) + pos_base + 1, max=kv_len)[:, None]
+    ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=mask,
+                                                           scale=float(np.float32(0.125)))
+    assert np.allclose(got, ref.numpy().reshape(-1), rtol=1e-6, atol=1e-7)
+
+    one = oracle.flash_attention(q, kt, v, heads, kv_heads, t_q, t_max, dh, 1, 0, 0.125).reshape(heads, t_q, dh)
+    vv = v.reshape(kv_heads, t_max, dh)
+    assert np.array_equal(one[5, 17], vv[1, 0])
+    flat = oracle.flash_attention(q, kt, v, heads, kv_heads, t_q, t_max, dh, kv_len, pos_base, 0.0)
+    flat = flat.reshape(heads, t_q, dh)
+    assert np.allclose(flat[3, 10], vv[0, :41].astype(np.float64).mean(axis=0), atol=1e-7)
+    assert not np.any(oracle.flash_attention(q, kt, v, heads, kv_heads, t_q, t_max, dh, 0, 0, 0.125))
