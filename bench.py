@@ -206,6 +206,38 @@ def prefill_layer(ta, ex, iters=10):
     return out
 
 
+ATTN_CASES = (  # name, H, H_kv, T, dh
+    ("tinyllama_prefill_t512_dh64", 32, 4, 512, 64),
+    ("llama_prefill_t2048_dh128", 32, 8, 2048, 128),
+)
+
+
+def causal_attn_flops(heads, t, dh):
+    """Score and PV products over the causal triangle: 4 * dh flops per
+    (query, attended key) pair, sum_i (i + 1) pairs per head."""
+    return 4.0 * heads * dh * (t * (t + 1) / 2)
+
+
+def attention(ta, ex, iters=10):
+    """Causal prefill attention (run_flash_attention), f32 q/out, f32 and
+    f16 caches, fresh prefill (kv_len = T)."""
+    rng = np.random.default_rng(71)
+    out = {}
+    for name, heads, kvh, t, dh in ATTN_CASES:
+        q = ex.tensor_from(rng.uniform(-1, 1, (heads, t, dh)).astype(np.float32))
+        for kv16 in (False, True):
+            kt = ex.tensor_from(rng.uniform(-1, 1, (kvh, dh, t)).astype(np.float32), f16=kv16)
+            v = ex.tensor_from(rng.uniform(-1, 1, (kvh, t, dh)).astype(np.float32), f16=kv16)
+            o = ex.tensor([heads, t, dh])
+            desc = ta.FlashAttentionDesc(t, 0, float(1.0 / np.sqrt(dh)))
+            for _ in range(3):
+                ex.flash_attention(q, kt, v, o, desc)
+            ns = median_ns([ex.flash_attention(q, kt, v, o, desc) for _ in range(iters)])
+            out[name + ("_kv16" if kv16 else "_f32")] = dict(
+                us=ns / 1e3, tflops=causal_attn_flops(heads, t, dh) / ns / 1e3)
+    return out
+
+
 def vendor_reference(hl_inputs, iters=20):
     """The vendor library on the same shapes, for reference only (not part
     of the product path; the role of the reference's
@@ -231,7 +263,7 @@ def vendor_reference(hl_inputs, iters=20):
             ts.append(e0.elapsed_time(e1) * 1e3)
         return statistics.median(ts)
 
-    out = {"library": "hipBLASLt via torch.matmul " + torch.__version__}
+    out = {"library": "hipBLASLt via torch.matmul, torch SDPA (causal, f32) " + torch.__version__}
     ha, hb = hl_inputs
     a, b = torch.from_numpy(ha).cuda(), torch.from_numpy(hb).cuda()
     us = timed(lambda: a @ b)
@@ -242,6 +274,12 @@ def vendor_reference(hl_inputs, iters=20):
         w = torch.randn(k, n, device="cuda", generator=g, dtype=torch.float16) * 0.02
         us = timed(lambda: x @ w)
         out[f"hgemm_{m}x{n}x{k}_f16"] = dict(us=us, tflops=2.0 * m * n * k / us / 1e6)
+    for name, heads, kvh, t, dh in ATTN_CASES:
+        q = torch.rand(1, heads, t, dh, device="cuda", generator=g) * 2 - 1
+        k = (torch.rand(1, kvh, t, dh, device="cuda", generator=g) * 2 - 1).repeat_interleave(heads // kvh, 1)
+        v = (torch.rand(1, kvh, t, dh, device="cuda", generator=g) * 2 - 1).repeat_interleave(heads // kvh, 1)
+        us = timed(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True))
+        out[f"sdpa_causal_{name}_f32"] = dict(us=us, tflops=causal_attn_flops(heads, t, dh) / us / 1e6)
     del a, b
     torch.cuda.empty_cache()
     return out
@@ -299,7 +337,7 @@ def main() -> int:
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (rocprof counter calibration)")
-    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,vendor",
+    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,attention,vendor",
                     help="comma list of secondary sections to run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -342,6 +380,9 @@ def main() -> int:
     if "prefill" in sections:
         log("prefill layer GEMMs ...")
         secondary["prefill_tinyllama_m512_f16w"] = prefill_layer(ta, ex)
+    if "attention" in sections:
+        log("causal prefill attention ...")
+        secondary["causal_prefill_attention"] = attention(ta, ex)
     if "vendor" in sections:
         log("vendor library reference ...")
         secondary["vendor_reference"] = vendor_reference(hl["inputs"])

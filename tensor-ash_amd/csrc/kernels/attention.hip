@@ -28,6 +28,8 @@
 // staged as zeros, so unwritten cache memory never reaches the sums.
 #include "common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kFlashThreads = 256;
@@ -43,12 +45,23 @@ template <bool F16> TA_DEVICE f32x4 load4(const void *base, uint64_t i) {
     return *reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + i);
   }
 }
-template <bool F16> TA_DEVICE float load1(const void *base, uint64_t i) {
+// Cache loads in storage type; widened to f32 only when written to LDS,
+// so a prefetch does not wait for its data at the load.
+template <bool F16> TA_DEVICE auto load_raw(const void *base, uint64_t i) {
   if constexpr (F16)
-    return (float)static_cast<const _Float16 *>(base)[i];
+    return *reinterpret_cast<const f16x4 *>(static_cast<const _Float16 *>(base) + i);
+  else
+    return *reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + i);
+}
+template <bool F16> TA_DEVICE auto load_raw1(const void *base, uint64_t i) {
+  if constexpr (F16)
+    return static_cast<const _Float16 *>(base)[i];
   else
     return static_cast<const float *>(base)[i];
 }
+TA_DEVICE f32x4 widen(f32x4 v) { return v; }
+TA_DEVICE f32x4 widen(f16x4 h) { return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]}; }
+
 template <bool F16> TA_DEVICE void store4(void *base, uint64_t i, f32x4 v) {
   if constexpr (F16) {
     *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(base) + i) =
@@ -113,38 +126,52 @@ template <int DH, bool KV16, bool IO16> TA_DEVICE void flash_body(const FlashArg
   const uint64_t v_base = (uint64_t)kv_head * p.t_max * DH;
   const bool kt_vec = (p.t_max & 3u) == 0u;
 
-  for (uint32_t t = 0; t < n_tiles; ++t) {
-    const uint32_t k0 = t * kBK;
-    __syncthreads(); // the previous tile's LDS reads are done
-    // K tile: ksh[d][c] = Kt[d][k0 + c] (16 four-key chunks per row).
+  // K/V of the next tile are loaded into registers while the current one
+  // is computed: ksh[d][c] = Kt[d][k0 + c] in 16 four-key chunks per row,
+  // vsh[r][d] = V[k0 + r][d].
+  constexpr int NCH = DH * kBK / 4 / kFlashThreads;
+  using Raw = typename std::conditional<KV16, f16x4, f32x4>::type; // widened at the LDS store
+  Raw kreg[NCH], vreg[NCH];
+  auto load_tile = [&](uint32_t k0) {
 #pragma unroll
-    for (int i = 0; i < DH * kBK / 4 / kFlashThreads; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const uint32_t c = tid + i * kFlashThreads;
-      const uint32_t d = c >> 4, kc = (c & 15u) * 4u;
-      const uint32_t key = k0 + kc;
+      const uint32_t d = c >> 4, key = k0 + (c & 15u) * 4u;
       const uint64_t src = kt_base + (uint64_t)d * p.t_max + key;
-      f32x4 v;
       if (kt_vec && key + 3u < stage_end) {
-        v = load4<KV16>(p.kt, src);
+        kreg[i] = load_raw<KV16>(p.kt, src);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          v[e] = key + e < stage_end ? load1<KV16>(p.kt, src + e) : 0.0f;
+          kreg[i][e] = key + e < stage_end ? load_raw1<KV16>(p.kt, src + e) : 0;
       }
-      *reinterpret_cast<f32x4 *>(ksh + d * kBK + kc) = v;
     }
-    // V tile: vsh[r][d] = V[k0 + r][d].
 #pragma unroll
-    for (int i = 0; i < DH * kBK / 4 / kFlashThreads; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const uint32_t c = tid + i * kFlashThreads;
-      const uint32_t r = c / (DH / 4), dc = (c % (DH / 4)) * 4u;
-      const uint32_t key = k0 + r;
-      f32x4 v = f32x4{};
-      if (key < stage_end)
-        v = load4<KV16>(p.v, v_base + (uint64_t)key * DH + dc);
-      *reinterpret_cast<f32x4 *>(vsh + r * DH + dc) = v;
+      const uint32_t key = k0 + c / (DH / 4), dc = (c % (DH / 4)) * 4u;
+      vreg[i] = key < stage_end ? load_raw<KV16>(p.v, v_base + (uint64_t)key * DH + dc) : Raw{};
+    }
+  };
+  if (n_tiles > 0)
+    load_tile(0);
+
+  // Softmax in base 2: scores are scaled by scale * log2(e) once, so each
+  // probability is one native exp2.
+  const float scale2 = p.scale * 1.44269504088896340736f;
+
+  for (uint32_t t = 0; t < n_tiles; ++t) {
+    const uint32_t k0 = t * kBK;
+    __syncthreads(); // the previous tile's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const uint32_t c = tid + i * kFlashThreads;
+      *reinterpret_cast<f32x4 *>(ksh + (c >> 4) * kBK + (c & 15u) * 4u) = widen(kreg[i]);
+      *reinterpret_cast<f32x4 *>(vsh + (c / (DH / 4)) * DH + (c % (DH / 4)) * 4u) = widen(vreg[i]);
     }
     __syncthreads();
+    if (t + 1 < n_tiles)
+      load_tile(k0 + kBK);
 
     // S^T block: keys kh*32 + m (m < 32) against this wave's 32 queries.
     f32x16 s = f32x16{};
@@ -163,20 +190,20 @@ template <int DH, bool KV16, bool IO16> TA_DEVICE void flash_body(const FlashArg
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t key = kbase + 8u * q + r;
-        const float v = key < valid_row ? s[4 * q + r] * p.scale : kNegMax;
+        const float v = key < valid_row ? s[4 * q + r] * scale2 : kNegMax;
         s[4 * q + r] = v;
         tmax = fmaxf(tmax, v);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float m_new = fmaxf(m_run, tmax);
-    const float corr = expf(m_run - m_new);
+    const float corr = exp2f(m_run - m_new);
     float psum = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t key = kbase + 8u * q + r;
-        const float pv = key < valid_row ? expf(s[4 * q + r] - m_new) : 0.0f;
+        const float pv = key < valid_row ? exp2f(s[4 * q + r] - m_new) : 0.0f;
         s[4 * q + r] = pv;
         psum += pv;
       }
@@ -220,7 +247,7 @@ template <int DH, bool KV16, bool IO16> TA_DEVICE void flash_body(const FlashArg
     const float m1 = mb[(DB * 16) * 64 + lane];
     const float l1 = mb[(DB * 16 + 1) * 64 + lane];
     const float m = fmaxf(m_run, m1);
-    const float a0 = expf(m_run - m), a1 = expf(m1 - m);
+    const float a0 = exp2f(m_run - m), a1 = exp2f(m1 - m);
     float l = l_run * a0 + l1 * a1;
     l += __shfl_xor(l, 32);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
