@@ -238,14 +238,15 @@ def attention(ta, ex, iters=10):
     return out
 
 
-def vendor_reference(hl_inputs, iters=20):
-    """The vendor library on the same shapes, for reference only (not part
+def vendor_reference(iters=20):
+    """The vendor libraries on the same shapes, for reference only (not part
     of the product path; the role of the reference's
-    benchmarks/cublas_bench/cublas_bench.cu):
-    torch's matmul, which is hipBLASLt on ROCm, timed with torch events on
-    torch's stream.  fp32 runs full-precision FP32 (no TF32 on this path);
-    the f16 rows are f16 x f16 -> f16, the semantics of this build's a16
-    route, not of its f16w route (f32 activations)."""
+    benchmarks/cublas_bench/cublas_bench.cu): FP32 SGEMM from the
+    hipBLASLt timing binary (HIP events, full FP32 compute type); f16 GEMM
+    (torch's matmul, hipBLASLt on ROCm) and causal SDPA from torch, timed
+    with torch events on torch's stream.  The f16 rows are f16 x f16 -> f16,
+    the semantics of this build's a16 route, not of its f16w route (f32
+    activations)."""
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False
 
@@ -263,11 +264,9 @@ def vendor_reference(hl_inputs, iters=20):
             ts.append(e0.elapsed_time(e1) * 1e3)
         return statistics.median(ts)
 
-    out = {"library": "hipBLASLt via torch.matmul, torch SDPA (causal, f32) " + torch.__version__}
-    ha, hb = hl_inputs
-    a, b = torch.from_numpy(ha).cuda(), torch.from_numpy(hb).cuda()
-    us = timed(lambda: a @ b)
-    out["sgemm_4096^3_f32"] = dict(us=us, tflops=2.0 * 4096 ** 3 / us / 1e6)
+    out = {"library": "hipBLASLt FP32 via lib/vendor_bench (fastest of 8 heuristic candidates); "
+                      "f16 GEMM and causal SDPA via torch " + torch.__version__}
+    out.update(vendor_sgemm())
     g = torch.Generator(device="cuda").manual_seed(61)
     for (m, n, k) in ((512, 2560, 2048), (512, 2048, 2048), (512, 5632, 2048), (512, 2048, 5632)):
         x = torch.rand(m, k, device="cuda", generator=g, dtype=torch.float16) * 2 - 1
@@ -280,8 +279,28 @@ def vendor_reference(hl_inputs, iters=20):
         v = (torch.rand(1, kvh, t, dh, device="cuda", generator=g) * 2 - 1).repeat_interleave(heads // kvh, 1)
         us = timed(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True))
         out[f"sdpa_causal_{name}_f32"] = dict(us=us, tflops=causal_attn_flops(heads, t, dh) / us / 1e6)
-    del a, b
     torch.cuda.empty_cache()
+    return out
+
+
+def vendor_sgemm():
+    """FP32 SGEMM of hipBLASLt on the BASELINE shapes (vendor_bench/cases.csv),
+    run as a child process; median-based TFLOP/s."""
+    import csv
+    import io
+    import subprocess
+    pkg = Path(__file__).resolve().parent / "tensor-ash_amd"
+    exe = pkg / "lib" / "vendor_bench"
+    if not exe.exists():
+        return {"sgemm_error": f"{exe} not built"}
+    cases = (pkg / "vendor_bench" / "cases.csv").read_text()
+    proc = subprocess.run([str(exe), "--iters", "20", "--warmup", "5"], input=cases, text=True,
+                          capture_output=True, timeout=240)
+    if proc.returncode != 0:
+        return {"sgemm_error": proc.stderr.strip()[-400:]}
+    out = {}
+    for row in csv.DictReader(io.StringIO(proc.stdout)):
+        out["sgemm_" + row["label"] + "_f32"] = dict(us=float(row["median_ms"]) * 1e3, tflops=float(row["tflops"]))
     return out
 
 
@@ -385,7 +404,7 @@ def main() -> int:
         secondary["causal_prefill_attention"] = attention(ta, ex)
     if "vendor" in sections:
         log("vendor library reference ...")
-        secondary["vendor_reference"] = vendor_reference(hl["inputs"])
+        secondary["vendor_reference"] = vendor_reference()
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")

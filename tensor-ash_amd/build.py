@@ -85,9 +85,22 @@ def build_oracle() -> Path:
     return so
 
 
+def build_vendor_bench() -> Path:
+    """lib/vendor_bench: the hipBLASLt FP32 SGEMM timing binary (comparison
+    baseline, not part of the library)."""
+    src = PKG / "vendor_bench" / "vendor_bench.cpp"
+    out = LIB / "vendor_bench"
+    LIB.mkdir(exist_ok=True)
+    cxx = shutil.which("g++") or "g++"
+    _run([cxx, "-O2", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", str(src),
+          "-o", str(out), f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lhipblaslt", "-lamdhip64"])
+    return out
+
+
 def build_all() -> None:
-    with cf.ThreadPoolExecutor(max_workers=3) as pool:
-        futs = [pool.submit(build_kernels), pool.submit(build_host), pool.submit(build_oracle)]
+    with cf.ThreadPoolExecutor(max_workers=4) as pool:
+        futs = [pool.submit(build_kernels), pool.submit(build_host), pool.submit(build_oracle),
+                pool.submit(build_vendor_bench)]
         for f in futs:
             f.result()
 
