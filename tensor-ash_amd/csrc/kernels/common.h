@@ -69,35 +69,28 @@ TA_DEVICE void ta_tile_coords(uint32_t lin, uint32_t tiles_m, uint32_t tiles_n,
 
 // Output stage shared by the MFMA GEMMs.  One 32-row block of each wave's
 // WTM x WTN sub-tile at a time goes through LDS (the K loop's buffers are
-// free after its last barrier); the wave reads its block back row-major,
-// applies the epilogue and stores 128-bit (f32) or 64-bit (f16) vectors.
-// This keeps the accumulators in registers (no dynamic indexing) and makes
-// the C/D traffic coalesced.  Accumulator layout of the 32x32 MFMAs: lane
-// l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// free after its last barrier): `stage(Cs, blk)` writes block blk of the
+// accumulators row-major into the wave's region (row stride WTN + 4), then
+// the wave reads it back row-major, applies the epilogue and stores 128-bit
+// (f32) or 64-bit (f16) vectors.  This keeps the accumulators in registers
+// (no dynamic indexing) and makes the C/D traffic coalesced.
 // Split mode (num_splits > 1): alpha * partial to plane (batch*S + split).
 // C_F16: C is f16 storage (RNE), only alpha / accumulate apply.
 // Waves with `active` false hold no tile and only join the barriers.
-template <int WTM, int WTN, int FM, int FN, int T, bool C_F16>
-TA_DEVICE void ta_store_tile(float *smem, int smem_floats, const f32x16 (&acc)[FM][FN],
-                             const GemmArgs &p, uint32_t lane, uint32_t wave, uint32_t wm,
-                             uint32_t wn, uint32_t m0, uint32_t n0, uint32_t batch,
-                             uint32_t split, bool active = true) {
+template <int WTM, int WTN, int T, bool C_F16, class Stage>
+TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &p, uint32_t lane,
+                                    uint32_t wave, uint32_t wm, uint32_t wn, uint32_t m0,
+                                    uint32_t n0, uint32_t batch, uint32_t split,
+                                    bool active = true) {
   constexpr int LDC = WTN + 4;
-  (void)smem_floats;
   float *Cs = smem + wave * (32 * LDC);
-  const uint32_t lr = lane & 31u, lg = lane >> 5;
   const uint32_t S = p.num_splits;
   const uint64_t mn = (uint64_t)p.m * p.n;
   const bool vec_out = (p.n & 3u) == 0u;
 #pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    if (active) {
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Cs[(8 * (r / 4) + 4 * lg + (r % 4)) * LDC + fn * 32 + lr] = acc[fm][fn][r];
-    }
+  for (int fm = 0; fm < WTM / 32; ++fm) {
+    if (active)
+      stage(Cs, fm);
     __syncthreads();
     const uint32_t row0 = m0 + wm * WTM + fm * 32;
     const uint32_t col0 = n0 + wn * WTN;
@@ -143,4 +136,30 @@ TA_DEVICE void ta_store_tile(float *smem, int smem_floats, const f32x16 (&acc)[F
     }
     __syncthreads();
   }
+}
+
+// ta_store_tile_staged for the 32x32 MFMA accumulator layout: lane l,
+// register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+template <int WTM, int WTN, int FM, int FN, int T, bool C_F16>
+TA_DEVICE void ta_store_tile(float *smem, int smem_floats, const f32x16 (&acc)[FM][FN],
+                             const GemmArgs &p, uint32_t lane, uint32_t wave, uint32_t wm,
+                             uint32_t wn, uint32_t m0, uint32_t n0, uint32_t batch,
+                             uint32_t split, bool active = true) {
+  (void)smem_floats;
+  constexpr int LDC = WTN + 4;
+  const uint32_t lr = lane & 31u, lg = lane >> 5;
+  auto stage = [&](float *Cs, int fm) __attribute__((always_inline)) {
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+      if (f != fm)
+        continue;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          Cs[(8 * (r / 4) + 4 * lg + (r % 4)) * LDC + fn * 32 + lr] = acc[f][fn][r];
+    }
+  };
+  ta_store_tile_staged<WTM, WTN, T, C_F16>(smem, stage, p, lane, wave, wm, wn, m0, n0, batch,
+                                           split, active);
 }

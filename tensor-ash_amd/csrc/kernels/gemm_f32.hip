@@ -27,6 +27,8 @@
 //    (64-bit for f16 B) global loads; the others load scalars.
 #include "common.h"
 
+#include <utility>
+
 namespace {
 
 template <int BM, int BN, int WGM, int WGN, bool VEC, bool HALF_B, int BK_ = 16>
@@ -247,6 +249,210 @@ struct GemmF32 {
 };
 
 
+template <class F, int... I>
+TA_DEVICE void ta_static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
+  ta_static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// FP32 kernel for full 256x256 tiles (M % 256 == 0, N % 256 == 0,
+// K % 32 == 0, f32 A and B, no split-K): the shape of the fastest vendor
+// FP32 kernels on this chip, written out by hand.
+//  * v_mfma_f32_16x16x4_f32; 4 waves (2x2) of 128x128 wave tiles, 8x8
+//    blocks of 16x16 accumulators (256 registers per lane, kept in the
+//    AGPRs; one wave per SIMD).  MFMA step s of a 16-deep stage takes
+//    k = (lane / 16) * 4 + s from both operands.
+//  * NS = 4 stages of 16-deep A [256][16] and B [16][256] slabs in LDS,
+//    filled by direct global -> LDS loads (global_load_lds_dwordx4) with
+//    16-byte chunks XOR-swizzled per row on the global side:
+//      A rows (64 bytes): chunk ^ ((b1 ^ b3) | b2 << 1) of the row index, so
+//        8 consecutive rows of a ds_read_b128 hit distinct chunk slots in
+//        a 128-byte bank window and 16 rows distinct slots in 256 bytes;
+//      B rows (1 KiB): chunk ^ 4 * ((row >> 2) & 3), so the four rows a
+//        wave reads at once (k = group * 4 + s) use four 16-bank quarters.
+//  * One barrier per stage.  The LDS operands of stage k+1 are read into a
+//    second register set while stage k's 256 MFMAs run, and each side
+//    operation of a stage (8 direct loads, 8 ds_read_b128, 16
+//    ds_read2st64_b32) is issued after every 8th MFMA, so the MFMA pipe
+//    never waits on LDS latency or instruction issue.  The MFMAs and side
+//    operations are volatile inline asm so this order is the one executed;
+//    the explicit s_waitcnt at the end of a stage covers the register set
+//    read during it.
+//  * The loop is branch-free: K / 16 stages are walked two at a time (the
+//    register sets alternate), and loads past the last stage re-read the
+//    last stage (clamped source) into buffers nobody reads.
+//  * Output through ta_store_tile_staged (the fused epilogue).
+template <int NS> struct GemmF32Mi16 {
+  static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 2, BK = 16, T = 256;
+  static constexpr int WTM = 128, WTN = 128, FM = 8, FN = 8;
+  static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BK * BN * 4, STAGE = A_BYTES + B_BYTES;
+  static constexpr int CPA = BK / 4, CPR = BN / 4; // 16-byte chunks per A / B row
+  static constexpr int A_LD = A_BYTES / 16 / T, B_LD = B_BYTES / 16 / T, LD = A_LD + B_LD;
+  static constexpr int SMEM_BYTES = NS * STAGE;
+  static constexpr int READS = FM + 2 * FN; // LDS reads per stage
+  static constexpr int MFMAS = 4 * FM * FN; // per stage
+  static_assert(NS >= 3 && (NS - 3) * LD <= 63, "vmcnt range");
+  static_assert(LD + READS == MFMAS / 8, "one side operation per 8 MFMAs");
+  static_assert(4 * 32 * (WTN + 4) * 4 <= SMEM_BYTES, "C staging fits in LDS");
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+  static TA_DEVICE uint32_t swz_a(uint32_t row) {
+    return (((row >> 1) ^ (row >> 3)) & 1u) | (((row >> 2) & 1u) << 1);
+  }
+  static TA_DEVICE uint32_t swz_b(uint32_t row) { return 4u * ((row >> 2) & 3u); }
+
+  static TA_DEVICE void run(const GemmArgs &p) {
+    __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WGN, wn = wave % WGN;
+    uint32_t tm, tn;
+    ta_tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t batch = blockIdx.z;
+    const float *A = static_cast<const float *>(p.a) + (uint64_t)batch * p.stride_a;
+    const float *B = static_cast<const float *>(p.b) + (uint64_t)batch * p.stride_b;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+    const uint32_t kts = p.k / BK;
+
+    const char *asrc[A_LD];
+    const char *bsrc[B_LD];
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const uint32_t q = i * T + tid, row = q / CPA, c = (q % CPA) ^ swz_a(row);
+      asrc[i] = reinterpret_cast<const char *>(A + (uint64_t)(m0 + row) * p.k + 4 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const uint32_t q = i * T + tid, row = q / CPR, c = (q % CPR) ^ swz_b(row);
+      bsrc[i] = reinterpret_cast<const char *>(B + (uint64_t)row * p.n + n0 + 4 * c);
+    }
+    const uint32_t lr = lane & 15u, lg = lane >> 4;
+    uint32_t a_off[FM], b_off[FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const uint32_t row = wm * WTM + fm * 16 + lr;
+      a_off[fm] = lds0 + row * (BK * 4) + 16u * (lg ^ swz_a(row));
+    }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const uint32_t col = wn * WTN + fn * 16 + lr, row = lg * 4u;
+      b_off[fn] = lds0 + A_BYTES + row * (BN * 4) + 16u * ((col >> 2) ^ swz_b(row)) + (col & 3u) * 4;
+    }
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+        acc[fm][fn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 ra[2][FM];
+    f32x2 rb[2][FN][2];
+
+    // i-th direct load of stage j (A chunks first, then B).
+    auto gload = [&](uint32_t j, auto i_c) __attribute__((always_inline)) {
+      constexpr int i = decltype(i_c)::value;
+      const uint32_t jj = min(j, kts - 1u);
+      const uint32_t base = lds0 + (j % NS) * STAGE + wave * 64 * 16;
+      const char *src;
+      uint32_t dst;
+      if constexpr (i < A_LD) {
+        src = asrc[i] + (uint64_t)jj * BK * 4;
+        dst = base + i * T * 16;
+      } else {
+        src = bsrc[i - A_LD] + (uint64_t)jj * BK * p.n * 4;
+        dst = base + A_BYTES + (i - A_LD) * T * 16;
+      }
+      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst)
+                   : "memory", "m0");
+    };
+    // i-th LDS read of a stage into register set `set` (A b128s, then B pairs).
+    auto lread = [&](auto set_c, uint32_t stoff, auto i_c) __attribute__((always_inline)) {
+      constexpr int set = decltype(set_c)::value, i = decltype(i_c)::value;
+      if constexpr (i < FM) {
+        f32x4 v;
+        asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a_off[i] + stoff) : "memory");
+        ra[set][i] = v;
+      } else {
+        constexpr int fn = (i - FM) / 2, h = (i - FM) % 2;
+        f32x2 v;
+        if constexpr (h == 0)
+          asm volatile("ds_read2st64_b32 %0, %1 offset1:4" : "=v"(v) : "v"(b_off[fn] + stoff)
+                       : "memory");
+        else
+          asm volatile("ds_read2st64_b32 %0, %1 offset0:8 offset1:12"
+                       : "=v"(v)
+                       : "v"(b_off[fn] + stoff)
+                       : "memory");
+        rb[set][fn][h] = v;
+      }
+    };
+    auto mfma = [&](auto set_c, auto idx_c) __attribute__((always_inline)) {
+      constexpr int set = decltype(set_c)::value, idx = decltype(idx_c)::value;
+      constexpr int s = idx / (FM * FN), fm = (idx / FN) % FM, fn = idx % FN;
+      f32x4 c = acc[fm][fn];
+      const float av = ra[set][fm][s], bv = rb[set][fn][s / 2][s % 2];
+      asm volatile("v_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+a"(c) : "v"(av), "v"(bv));
+      acc[fm][fn] = c;
+    };
+
+    for (uint32_t j = 0; j < NS - 1; ++j)
+      ta_static_for<LD>([&](auto i_c) __attribute__((always_inline)) { gload(j, i_c); });
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * LD) : "memory");
+    __syncthreads();
+    ta_static_for<READS>([&](auto i_c) __attribute__((always_inline)) {
+      lread(std::integral_constant<int, 0>{}, 0u, i_c);
+    });
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // Stage kt: MFMAs on register set `cur`; loads of stage kt + NS - 1
+    // and LDS reads of stage kt + 1 (into the other set) in between.
+    auto body = [&](auto cur_c, uint32_t kt) __attribute__((always_inline)) {
+      constexpr int cur = decltype(cur_c)::value;
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * LD) : "memory");
+      const uint32_t stoff = ((kt + 1) % NS) * STAGE;
+      ta_static_for<MFMAS>([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        mfma(cur_c, ic);
+        if constexpr (i % 8 == 7) {
+          constexpr int side = i / 8; // loads at even slots below 2*LD, reads elsewhere
+          if constexpr (side < 2 * LD && (side & 1) == 0)
+            gload(kt + NS - 1, std::integral_constant<int, side / 2>{});
+          else
+            lread(std::integral_constant<int, 1 - cur>{}, stoff,
+                  std::integral_constant<int, (side < 2 * LD ? side / 2 : side - LD)>{});
+        }
+      });
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+    for (uint32_t kt = 0; kt < kts; kt += 2) {
+      body(std::integral_constant<int, 0>{}, kt);
+      body(std::integral_constant<int, 1>{}, kt + 1);
+    }
+    // Drain the trailing loads; give the last MFMA results their wait states.
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    __syncthreads();
+
+    // 16x16 blocks: lane l holds rows 4*(l/16) + i, column l%16.
+    constexpr int LDC = WTN + 4;
+    auto stage = [&](float *Cs, int blk) __attribute__((always_inline)) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        if (fm / 2 != blk)
+          continue;
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            Cs[((fm % 2) * 16 + 4 * lg + i) * LDC + fn * 16 + lr] = acc[fm][fn][i];
+      }
+    };
+    ta_store_tile_staged<WTM, WTN, T, false>(reinterpret_cast<float *>(smem), stage, p, lane, wave,
+                                             wm, wn, m0, n0, batch, 0);
+  }
+};
+
 } // namespace
 
 #define TA_GEMM_F32(NAME, BM, BN, WGM, WGN, VEC, HALF_B, BK)                      \
@@ -272,3 +478,7 @@ TA_GEMM_F32_FAMILY(m64n64, 64, 64, 2, 2, 16)
 TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4, 16)
 TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2, 16)
 
+// Full 256x256 tiles of f32 A and B with K % 32 == 0 (see GemmF32Mi16).
+extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m256n256_mi16(GemmArgs p) {
+  GemmF32Mi16<4>::run(p);
+}

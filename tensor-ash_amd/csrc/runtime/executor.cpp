@@ -378,8 +378,10 @@ struct ExecutorImpl {
       a.a = splitk_scratch;
     }
     const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
-    launch(std::string(s.symbol) + (lds ? "_lds" : vec ? "_vec" : "_gen"), (uint32_t)gx, 1,
-           (uint32_t)gz, gemm_threads(s), &a, stream);
+    const bool mi16 = s.kind == KernelKind::GemmF32 && s.tile_m == 256 && s.tile_n == 256 &&
+                      a.num_splits == 1 && f32_mi16_ok(d);
+    launch(std::string(s.symbol) + (mi16 ? "_mi16" : lds ? "_lds" : vec ? "_vec" : "_gen"),
+           (uint32_t)gx, 1, (uint32_t)gz, mi16 ? 256u : gemm_threads(s), &a, stream);
     if (splits > 1) {
       SplitReduceArgs r{};
       r.scratch = static_cast<const float *>(splitk_scratch);

@@ -107,6 +107,11 @@ uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 // Shapes the pipelined f16-MFMA kernels (`_lds` code objects) take: whole
 // 64-deep K stages and 16-byte B rows.
 bool gemm_lds_ok(const ResolvedMatmul &d) { return d.k > 0 && d.k % 64 == 0 && d.n % 8 == 0; }
+// ta_gemm_f32_m256n256_mi16 takes whole 256x256 tiles of f32 A and B and
+// walks K two 16-deep stages at a time.
+bool f32_mi16_ok(const ResolvedMatmul &d) {
+  return !d.a_f16 && !d.b_f16 && d.m % 256 == 0 && d.n % 256 == 0 && d.k > 0 && d.k % 32 == 0;
+}
 
 bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
   // The 256x256 f16-MFMA tiles exist only as pipelined kernels.
