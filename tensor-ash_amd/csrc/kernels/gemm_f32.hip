@@ -258,7 +258,7 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 }
 
 // FP32 kernel for full 256x256 tiles (M % 256 == 0, N % 256 == 0,
-// K % 32 == 0, f32 A and B, no split-K): the shape of the fastest vendor
+// K % 64 == 0, f32 A and B, no split-K): the shape of the fastest vendor
 // FP32 kernels on this chip, written out by hand.
 //  * v_mfma_f32_16x16x4_f32; 4 waves (2x2) of 128x128 wave tiles, 8x8
 //    blocks of 16x16 accumulators (256 registers per lane, kept in the
@@ -280,9 +280,15 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 //    operations are volatile inline asm so this order is the one executed;
 //    the explicit s_waitcnt at the end of a stage covers the register set
 //    read during it.
-//  * The loop is branch-free: K / 16 stages are walked two at a time (the
-//    register sets alternate), and loads past the last stage re-read the
-//    last stage (clamped source) into buffers nobody reads.
+//  * The side operations need no VALU work: direct loads address through a
+//    wave-uniform 64-bit base advanced with scalar adds plus a fixed 32-bit
+//    lane offset, and LDS reads use fixed base registers (one set per
+//    stage pair) with the stage in the immediate offset.  Vector address
+//    arithmetic between MFMAs measurably stalls the MFMA pipe.
+//  * The loop is branch-free: K / 16 stages are walked four at a time (the
+//    stage index, and so every LDS offset, is a compile-time constant in
+//    each copy), and loads past the last stage re-read the last stage
+//    (clamped source) into buffers nobody reads.
 //  * Output through ta_store_tile_staged (the fused epilogue).
 template <int NS> struct GemmF32Mi16 {
   static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 2, BK = 16, T = 256;
@@ -317,29 +323,38 @@ template <int NS> struct GemmF32Mi16 {
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
     const uint32_t kts = p.k / BK;
 
-    const char *asrc[A_LD];
-    const char *bsrc[B_LD];
+    // Direct loads: wave-uniform 64-bit base (per stage) + per-lane 32-bit offset.
+    uint32_t avoff[A_LD], bvoff[B_LD];
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       const uint32_t q = i * T + tid, row = q / CPA, c = (q % CPA) ^ swz_a(row);
-      asrc[i] = reinterpret_cast<const char *>(A + (uint64_t)(m0 + row) * p.k + 4 * c);
+      avoff[i] = row * p.k * 4 + 16 * c;
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
       const uint32_t q = i * T + tid, row = q / CPR, c = (q % CPR) ^ swz_b(row);
-      bsrc[i] = reinterpret_cast<const char *>(B + (uint64_t)row * p.n + n0 + 4 * c);
+      bvoff[i] = row * p.n * 4 + 16 * c;
     }
+    const char *abase0 = reinterpret_cast<const char *>(A + (uint64_t)m0 * p.k);
+    const char *bbase0 = reinterpret_cast<const char *>(B + n0);
+    const uint64_t b_stage = (uint64_t)BK * p.n * 4;
     const uint32_t lr = lane & 15u, lg = lane >> 4;
-    uint32_t a_off[FM], b_off[FN];
+    // LDS read bases for stages {0, 1} (group 0) and {2, 3} (group 1); the
+    // stage within a group is the instruction's immediate offset.
+    uint32_t a_off[2][FM], b_off[2][FN];
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm) {
-      const uint32_t row = wm * WTM + fm * 16 + lr;
-      a_off[fm] = lds0 + row * (BK * 4) + 16u * (lg ^ swz_a(row));
-    }
+    for (int g = 0; g < 2; ++g) {
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-      const uint32_t col = wn * WTN + fn * 16 + lr, row = lg * 4u;
-      b_off[fn] = lds0 + A_BYTES + row * (BN * 4) + 16u * ((col >> 2) ^ swz_b(row)) + (col & 3u) * 4;
+      for (int fm = 0; fm < FM; ++fm) {
+        const uint32_t row = wm * WTM + fm * 16 + lr;
+        a_off[g][fm] = lds0 + g * 2 * STAGE + row * (BK * 4) + 16u * (lg ^ swz_a(row));
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const uint32_t col = wn * WTN + fn * 16 + lr, row = lg * 4u;
+        b_off[g][fn] = lds0 + g * 2 * STAGE + A_BYTES + row * (BN * 4) +
+                       16u * ((col >> 2) ^ swz_b(row)) + (col & 3u) * 4;
+      }
     }
     f32x4 acc[FM][FN];
 #pragma unroll
@@ -350,41 +365,40 @@ template <int NS> struct GemmF32Mi16 {
     f32x4 ra[2][FM];
     f32x2 rb[2][FN][2];
 
-    // i-th direct load of stage j (A chunks first, then B).
+    // i-th direct load of stage j (A chunks first, then B); loads past the
+    // last stage re-read it into a buffer nobody reads.
     auto gload = [&](uint32_t j, auto i_c) __attribute__((always_inline)) {
       constexpr int i = decltype(i_c)::value;
       const uint32_t jj = min(j, kts - 1u);
       const uint32_t base = lds0 + (j % NS) * STAGE + wave * 64 * 16;
-      const char *src;
-      uint32_t dst;
       if constexpr (i < A_LD) {
-        src = asrc[i] + (uint64_t)jj * BK * 4;
-        dst = base + i * T * 16;
+        const char *sb = abase0 + (uint64_t)jj * BK * 4;
+        const uint32_t vo = avoff[i];
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(vo), "s"(sb),
+                     "s"(base + i * T * 16) : "memory", "m0");
       } else {
-        src = bsrc[i - A_LD] + (uint64_t)jj * BK * p.n * 4;
-        dst = base + A_BYTES + (i - A_LD) * T * 16;
+        const char *sb = bbase0 + (uint64_t)jj * b_stage;
+        const uint32_t vo = bvoff[i - A_LD];
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(vo),
+                     "s"(sb), "s"(base + A_BYTES + (i - A_LD) * T * 16) : "memory", "m0");
       }
-      asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst)
-                   : "memory", "m0");
     };
-    // i-th LDS read of a stage into register set `set` (A b128s, then B pairs).
-    auto lread = [&](auto set_c, uint32_t stoff, auto i_c) __attribute__((always_inline)) {
-      constexpr int set = decltype(set_c)::value, i = decltype(i_c)::value;
+    // i-th LDS read of stage `stg` (compile time) into register set `set`.
+    auto lread = [&](auto set_c, auto stg_c, auto i_c) __attribute__((always_inline)) {
+      constexpr int set = decltype(set_c)::value, stg = decltype(stg_c)::value, i = decltype(i_c)::value;
+      constexpr int g = stg / 2, so = (stg % 2) * STAGE;
       if constexpr (i < FM) {
         f32x4 v;
-        asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a_off[i] + stoff) : "memory");
+        const uint32_t ad = a_off[g][i];
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(ad), "n"(so) : "memory");
         ra[set][i] = v;
       } else {
         constexpr int fn = (i - FM) / 2, h = (i - FM) % 2;
+        constexpr int o0 = so / 256 + 8 * h, o1 = o0 + 4;
+        const uint32_t bd = b_off[g][fn];
         f32x2 v;
-        if constexpr (h == 0)
-          asm volatile("ds_read2st64_b32 %0, %1 offset1:4" : "=v"(v) : "v"(b_off[fn] + stoff)
-                       : "memory");
-        else
-          asm volatile("ds_read2st64_b32 %0, %1 offset0:8 offset1:12"
-                       : "=v"(v)
-                       : "v"(b_off[fn] + stoff)
-                       : "memory");
+        asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3"
+                     : "=v"(v) : "v"(bd), "n"(o0), "n"(o1) : "memory");
         rb[set][fn][h] = v;
       }
     };
@@ -402,33 +416,34 @@ template <int NS> struct GemmF32Mi16 {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * LD) : "memory");
     __syncthreads();
     ta_static_for<READS>([&](auto i_c) __attribute__((always_inline)) {
-      lread(std::integral_constant<int, 0>{}, 0u, i_c);
+      lread(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, i_c);
     });
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
     // Stage kt: MFMAs on register set `cur`; loads of stage kt + NS - 1
     // and LDS reads of stage kt + 1 (into the other set) in between.
-    auto body = [&](auto cur_c, uint32_t kt) __attribute__((always_inline)) {
-      constexpr int cur = decltype(cur_c)::value;
+    auto body = [&](auto stg_c, uint32_t kt) __attribute__((always_inline)) {
+      constexpr int stg = decltype(stg_c)::value, cur = stg % 2; // stg = kt % NS
       asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * LD) : "memory");
-      const uint32_t stoff = ((kt + 1) % NS) * STAGE;
       ta_static_for<MFMAS>([&](auto ic) __attribute__((always_inline)) {
         constexpr int i = decltype(ic)::value;
-        mfma(cur_c, ic);
+        mfma(std::integral_constant<int, cur>{}, ic);
         if constexpr (i % 8 == 7) {
           constexpr int side = i / 8; // loads at even slots below 2*LD, reads elsewhere
           if constexpr (side < 2 * LD && (side & 1) == 0)
             gload(kt + NS - 1, std::integral_constant<int, side / 2>{});
           else
-            lread(std::integral_constant<int, 1 - cur>{}, stoff,
+            lread(std::integral_constant<int, 1 - cur>{}, std::integral_constant<int, (stg + 1) % NS>{},
                   std::integral_constant<int, (side < 2 * LD ? side / 2 : side - LD)>{});
         }
       });
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
-    for (uint32_t kt = 0; kt < kts; kt += 2) {
+    for (uint32_t kt = 0; kt < kts; kt += NS) {
       body(std::integral_constant<int, 0>{}, kt);
       body(std::integral_constant<int, 1>{}, kt + 1);
+      body(std::integral_constant<int, 2>{}, kt + 2);
+      body(std::integral_constant<int, 3>{}, kt + 3);
     }
     // Drain the trailing loads; give the last MFMA results their wait states.
     asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
@@ -478,7 +493,7 @@ TA_GEMM_F32_FAMILY(m64n64, 64, 64, 2, 2, 16)
 TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4, 16)
 TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2, 16)
 
-// Full 256x256 tiles of f32 A and B with K % 32 == 0 (see GemmF32Mi16).
+// Full 256x256 tiles of f32 A and B with K % 64 == 0 (see GemmF32Mi16).
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m256n256_mi16(GemmArgs p) {
   GemmF32Mi16<4>::run(p);
 }

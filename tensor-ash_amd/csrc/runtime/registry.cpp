@@ -108,9 +108,11 @@ uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 // 64-deep K stages and 16-byte B rows.
 bool gemm_lds_ok(const ResolvedMatmul &d) { return d.k > 0 && d.k % 64 == 0 && d.n % 8 == 0; }
 // ta_gemm_f32_m256n256_mi16 takes whole 256x256 tiles of f32 A and B and
-// walks K two 16-deep stages at a time.
+// walks K four 16-deep stages at a time; its 32-bit per-lane load offsets
+// span 256 rows of A and 16 rows of B.
 bool f32_mi16_ok(const ResolvedMatmul &d) {
-  return !d.a_f16 && !d.b_f16 && d.m % 256 == 0 && d.n % 256 == 0 && d.k > 0 && d.k % 32 == 0;
+  return !d.a_f16 && !d.b_f16 && d.m % 256 == 0 && d.n % 256 == 0 && d.k > 0 && d.k % 64 == 0 &&
+         256ull * d.k * 4 < (1ull << 32) && 16ull * d.n * 4 < (1ull << 32);
 }
 
 bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {

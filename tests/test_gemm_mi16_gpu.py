@@ -1,6 +1,6 @@
 """GPU parity of the aligned FP32 route (256x256 tiles on
 v_mfma_f32_16x16x4_f32, taken when M and N are multiples of 256 and K of
-32) against the CPU oracle, with every epilogue, alpha / accumulate and
+64) against the CPU oracle, with every epilogue, alpha / accumulate and
 the batch-broadcast forms; shapes just off the alignment take the other
 kernels and must agree too.  Tolerances as in test_gemm_gpu.check_f32.
 """
@@ -23,7 +23,7 @@ EPIS = [dict(), dict(bias=True), dict(act=1), dict(act=2, bias=True), dict(act=3
         dict(binary=2), dict(alpha=0.25, accumulate=True, act=3), dict(bias=True, act=2, binary=2)]
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 32), (512, 768, 96), (768, 512, 1024)])
+@pytest.mark.parametrize("shape", [(256, 256, 64), (512, 768, 192), (768, 512, 1024)])
 @pytest.mark.parametrize("epi", EPIS)
 def test_aligned_epilogues(ta, kex, oracle, shape, epi):
     m, n, k = shape
@@ -38,8 +38,8 @@ def test_aligned_batch_broadcast(ta, kex, oracle, ba, bb, bc):
              kernel_ex=kex)
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 48), (256, 256, 16), (255, 256, 32), (256, 260, 64),
-                                   (512, 512, 4000)])
+@pytest.mark.parametrize("shape", [(256, 256, 48), (256, 256, 16), (256, 256, 32), (256, 256, 96),
+                                   (255, 256, 64), (256, 260, 64), (512, 512, 4000)])
 def test_unaligned_fall_back(ta, kex, oracle, shape):
     run_case(ta, kex, oracle, *shape, bias=[shape[1]], act=3, kernel_ex=kex)
 
