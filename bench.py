@@ -294,7 +294,7 @@ def vendor_sgemm():
     if not exe.exists():
         return {"sgemm_error": f"{exe} not built"}
     cases = (pkg / "vendor_bench" / "cases.csv").read_text()
-    proc = subprocess.run([str(exe), "--iters", "20", "--warmup", "5"], input=cases, text=True,
+    proc = subprocess.run([str(exe), "--iters", "20", "--warmup", "30"], input=cases, text=True,
                           capture_output=True, timeout=240)
     if proc.returncode != 0:
         return {"sgemm_error": proc.stderr.strip()[-400:]}
@@ -350,8 +350,9 @@ def load_traffic():
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=50,
+                    help="untimed steps first; the chip needs ~20 ms of MFMA load to reach its steady clock")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
