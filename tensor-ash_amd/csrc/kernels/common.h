@@ -18,12 +18,17 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 TA_DEVICE float ta_activate(float x, uint32_t act) {
   if (act == TA_ACT_RELU)
     return fmaxf(x, 0.0f);
+  // SiLU and GELU use the HIP fast exp / divide intrinsics (a few ulp):
+  // at one wave per SIMD the precise library calls were the longest part
+  // of a large GEMM's epilogue.
   if (act == TA_ACT_SILU)
-    return x / (1.0f + expf(-x));
+    return __fdividef(x, 1.0f + __expf(-x));
   if (act == TA_ACT_GELU) {
-    // Published tanh form of GELU: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
-    const float k0 = 0.7978845608028654f;
-    return 0.5f * x * (1.0f + tanhf(k0 * fmaf(0.044715f * x * x, x, x)));
+    // Published tanh form of GELU, 0.5 x (1 + tanh(u)) with u = sqrt(2/pi)
+    // (x + 0.044715 x^3), evaluated through the identity 0.5 (1 + tanh(u))
+    // = 1 / (1 + exp(-2u)): one exp and one divide instead of tanh.
+    const float k2 = 2.0f * 0.7978845608028654f;
+    return __fdividef(x, 1.0f + __expf(-k2 * fmaf(0.044715f * x * x, x, x)));
   }
   return x;
 }
@@ -120,13 +125,23 @@ TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &
                 (_Float16)(p.alpha * v[c] + (acc_old ? (float)c16[base + c] : 0.0f));
         }
       } else if (vec_out && col + 4 <= p.n) {
-        f32x4 o;
-        if (S > 1) {
-          o = p.alpha * v;
-        } else {
+        // ta_epilogue on four columns with 128-bit loads of C, bias and D.
+        f32x4 o = p.alpha * v;
+        if (S == 1) {
+          if (p.flags & TA_FLAG_ACCUMULATE)
+            o += *reinterpret_cast<const f32x4 *>(&p.c[base]);
+          if (p.flags & TA_FLAG_BIAS)
+            o += *reinterpret_cast<const f32x4 *>(
+                &p.bias[(uint64_t)batch * p.bias_batch_stride + col]);
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            o[c] = ta_epilogue(v[c], p, base + c, col + c, batch);
+            o[c] = ta_activate(o[c], p.act);
+          if (p.binary != TA_BIN_NONE) {
+            const f32x4 d = *reinterpret_cast<const f32x4 *>(&p.d[base]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              o[c] = p.binary == TA_BIN_ADD_SCALED ? fmaf(p.beta, d[c], o[c]) : o[c] * d[c];
+          }
         }
         *reinterpret_cast<f32x4 *>(&p.c[base]) = o;
       } else {

@@ -444,9 +444,16 @@ template <int NS> struct GemmF32Mi16 {
       body(std::integral_constant<int, 1>{}, kt + 1);
       body(std::integral_constant<int, 2>{}, kt + 2);
       body(std::integral_constant<int, 3>{}, kt + 3);
+      // The MFMAs are inline asm, so the compiler does not know their result
+      // latency: wait states after each iteration's last MFMAs, so copies
+      // the compiler places at the loop exit read settled accumulators.
+      asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
     }
-    // Drain the trailing loads; give the last MFMA results their wait states.
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    // Drain the trailing loads.  Every accumulator then passes through an
+    // empty volatile asm (volatile asm keeps its order), so every read of it
+    // in the epilogue lands after the wait states above.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // CHAIN_PLACEHOLDER
     __syncthreads();
 
     // 16x16 blocks: lane l holds rows 4*(l/16) + i, column l%16.
