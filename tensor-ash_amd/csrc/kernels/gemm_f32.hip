@@ -257,25 +257,28 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
   ta_static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// FP32 kernel for full 256x256 tiles (M % 256 == 0, N % 256 == 0,
-// K % 64 == 0, f32 A and B, no split-K): the shape of the fastest vendor
-// FP32 kernels on this chip, written out by hand.
-//  * v_mfma_f32_16x16x4_f32; 4 waves (2x2) of 128x128 wave tiles, 8x8
-//    blocks of 16x16 accumulators (256 registers per lane, kept in the
-//    AGPRs; one wave per SIMD).  MFMA step s of a 16-deep stage takes
-//    k = (lane / 16) * 4 + s from both operands.
-//  * NS = 4 stages of 16-deep A [256][16] and B [16][256] slabs in LDS,
+// Pipelined FP32 kernel for whole BM x BN tiles of f32 A and B whose
+// K windows hold a multiple of 64 (K % (64 * splits) == 0): the shape of
+// the fastest vendor FP32 kernels on this chip, written out by hand.  The
+// 256x256 instance (2x2 waves of 128x128) serves plain GEMMs; 64x256 (1x4
+// waves of 64x64) and 32x128 (1x2 waves of 32x64) serve split-K stage 1
+// (and plain GEMMs that select those tiles),
+// where grid.z = batch * splits and each split writes its partial tile.
+//  * v_mfma_f32_16x16x4_f32; FM x FN blocks of 16x16 accumulators per wave
+//    (256 registers per lane at 128x128, kept in the AGPRs).  MFMA step s
+//    of a 16-deep stage takes k = (lane / 16) * 4 + s from both operands.
+//  * NS = 4 stages of 16-deep A [BM][16] and B [16][BN] slabs in LDS,
 //    filled by direct global -> LDS loads (global_load_lds_dwordx4) with
 //    16-byte chunks XOR-swizzled per row on the global side:
 //      A rows (64 bytes): chunk ^ ((b1 ^ b3) | b2 << 1) of the row index, so
 //        8 consecutive rows of a ds_read_b128 hit distinct chunk slots in
 //        a 128-byte bank window and 16 rows distinct slots in 256 bytes;
-//      B rows (1 KiB): chunk ^ 4 * ((row >> 2) & 3), so the four rows a
+//      B rows (BN * 4 bytes): chunk ^ 4 * ((row >> 2) & 3), so the four rows a
 //        wave reads at once (k = group * 4 + s) use four 16-bank quarters.
 //  * One barrier per stage.  The LDS operands of stage k+1 are read into a
-//    second register set while stage k's 256 MFMAs run, and each side
-//    operation of a stage (8 direct loads, 8 ds_read_b128, 16
-//    ds_read2st64_b32) is issued after every 8th MFMA, so the MFMA pipe
+//    second register set while stage k's MFMAs run, and the side
+//    operations of a stage (direct loads, ds_read_b128 of A,
+//    ds_read2st64_b32 of B) are spread evenly between them, so the MFMA pipe
 //    never waits on LDS latency or instruction issue.  The MFMAs and side
 //    operations are volatile inline asm so this order is the one executed;
 //    the explicit s_waitcnt at the end of a stage covers the register set
@@ -290,24 +293,37 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 //    each copy), and loads past the last stage re-read the last stage
 //    (clamped source) into buffers nobody reads.
 //  * Output through ta_store_tile_staged (the fused epilogue).
-template <int NS> struct GemmF32Mi16 {
-  static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 2, BK = 16, T = 256;
-  static constexpr int WTM = 128, WTN = 128, FM = 8, FN = 8;
+template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
+  static constexpr int BK = 16, T = 64 * WGM * WGN;
+  static constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 16, FN = WTN / 16;
   static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BK * BN * 4, STAGE = A_BYTES + B_BYTES;
   static constexpr int CPA = BK / 4, CPR = BN / 4; // 16-byte chunks per A / B row
   static constexpr int A_LD = A_BYTES / 16 / T, B_LD = B_BYTES / 16 / T, LD = A_LD + B_LD;
   static constexpr int SMEM_BYTES = NS * STAGE;
   static constexpr int READS = FM + 2 * FN; // LDS reads per stage
   static constexpr int MFMAS = 4 * FM * FN; // per stage
-  static_assert(NS >= 3 && (NS - 3) * LD <= 63, "vmcnt range");
-  static_assert(LD + READS == MFMAS / 8, "one side operation per 8 MFMAs");
-  static_assert(4 * 32 * (WTN + 4) * 4 <= SMEM_BYTES, "C staging fits in LDS");
+  static constexpr int SIDE = LD + READS;   // side operations per stage
+  static constexpr int RU = BN / 64;        // a B row in 256-byte ds_read2st64 units
+  static_assert(NS == 4, "the loop is unrolled by four stages, two LDS base groups");
+  static_assert((NS - 3) * LD <= 63, "vmcnt range");
+  static_assert(A_LD * T * 16 == A_BYTES && B_LD * T * 16 == B_BYTES, "stages split evenly");
+  static_assert(SIDE <= MFMAS && 2 * LD <= SIDE, "side operations fit between the MFMAs");
+  static_assert(CPA == 4 && CPR >= 16, "swizzles assume 64-byte A rows, >= 256-byte B rows");
+  static_assert(WGM * WGN * 32 * (WTN + 4) * 4 <= SMEM_BYTES, "C staging fits in LDS");
+  static_assert(STAGE % 256 == 0 && STAGE / 256 + 3 * RU <= 255, "ds_read2st64 offsets");
   typedef float f32x2 __attribute__((ext_vector_type(2)));
 
   static TA_DEVICE uint32_t swz_a(uint32_t row) {
     return (((row >> 1) ^ (row >> 3)) & 1u) | (((row >> 2) & 1u) << 1);
   }
   static TA_DEVICE uint32_t swz_b(uint32_t row) { return 4u * ((row >> 2) & 3u); }
+  // The side operation issued after MFMA i of a stage, or -1.
+  static constexpr int side_after(int i) {
+    for (int j = 0; j < SIDE; ++j)
+      if ((j + 1) * MFMAS / SIDE - 1 == i)
+        return j;
+    return -1;
+  }
 
   static TA_DEVICE void run(const GemmArgs &p) {
     __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
@@ -317,11 +333,26 @@ template <int NS> struct GemmF32Mi16 {
     uint32_t tm, tn;
     ta_tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const uint32_t batch = blockIdx.z;
-    const float *A = static_cast<const float *>(p.a) + (uint64_t)batch * p.stride_a;
-    const float *B = static_cast<const float *>(p.b) + (uint64_t)batch * p.stride_b;
+    const uint32_t P = p.num_splits;
+    const uint32_t batch = blockIdx.z / P, split = blockIdx.z % P;
+    // Split-K window (the GemmF32 rule; the host sends only shapes whose
+    // windows all hold a multiple of 64 rows of K).
+    uint32_t klo = 0, khi = p.k;
+    if (P > 1) {
+      const uint32_t Tt = max(1u, p.sub_splits), S = P / Tt;
+      const uint32_t sp = split / Tt, t = split % Tt;
+      const uint32_t per = p.k / S, rem = p.k % S;
+      const uint32_t lo = sp * per + min(sp, rem);
+      const uint32_t len = per + (sp < rem ? 1u : 0u);
+      const uint32_t per2 = len / Tt, rem2 = len % Tt;
+      klo = lo + t * per2 + min(t, rem2);
+      khi = klo + per2 + (t < rem2 ? 1u : 0u);
+    }
+    const float *A = static_cast<const float *>(p.a) + (uint64_t)batch * p.stride_a + klo;
+    const float *B = static_cast<const float *>(p.b) + (uint64_t)batch * p.stride_b +
+                     (uint64_t)klo * p.n;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
-    const uint32_t kts = p.k / BK;
+    const uint32_t kts = (khi - klo) / BK;
 
     // Direct loads: wave-uniform 64-bit base (per stage) + per-lane 32-bit offset.
     uint32_t avoff[A_LD], bvoff[B_LD];
@@ -394,7 +425,8 @@ template <int NS> struct GemmF32Mi16 {
         ra[set][i] = v;
       } else {
         constexpr int fn = (i - FM) / 2, h = (i - FM) % 2;
-        constexpr int o0 = so / 256 + 8 * h, o1 = o0 + 4;
+        // rows group * 4 + 2h and + 1 of the B slab
+        constexpr int o0 = so / 256 + 2 * RU * h, o1 = o0 + RU;
         const uint32_t bd = b_off[g][fn];
         f32x2 v;
         asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3"
@@ -425,11 +457,13 @@ template <int NS> struct GemmF32Mi16 {
     auto body = [&](auto stg_c, uint32_t kt) __attribute__((always_inline)) {
       constexpr int stg = decltype(stg_c)::value, cur = stg % 2; // stg = kt % NS
       asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * LD) : "memory");
+      // Side operation j follows MFMA (j + 1) * MFMAS / SIDE - 1: loads at
+      // the even slots below 2 * LD, LDS reads in the others.
       ta_static_for<MFMAS>([&](auto ic) __attribute__((always_inline)) {
         constexpr int i = decltype(ic)::value;
         mfma(std::integral_constant<int, cur>{}, ic);
-        if constexpr (i % 8 == 7) {
-          constexpr int side = i / 8; // loads at even slots below 2*LD, reads elsewhere
+        constexpr int side = side_after(i);
+        if constexpr (side >= 0) {
           if constexpr (side < 2 * LD && (side & 1) == 0)
             gload(kt + NS - 1, std::integral_constant<int, side / 2>{});
           else
@@ -449,11 +483,9 @@ template <int NS> struct GemmF32Mi16 {
       // the compiler places at the loop exit read settled accumulators.
       asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
     }
-    // Drain the trailing loads.  Every accumulator then passes through an
-    // empty volatile asm (volatile asm keeps its order), so every read of it
-    // in the epilogue lands after the wait states above.
+    // Drain the trailing loads (they re-read the last stage into buffers
+    // nobody reads) before the LDS is reused for the write-out.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // CHAIN_PLACEHOLDER
     __syncthreads();
 
     // 16x16 blocks: lane l holds rows 4*(l/16) + i, column l%16.
@@ -471,7 +503,7 @@ template <int NS> struct GemmF32Mi16 {
       }
     };
     ta_store_tile_staged<WTM, WTN, T, false>(reinterpret_cast<float *>(smem), stage, p, lane, wave,
-                                             wm, wn, m0, n0, batch, 0);
+                                             wm, wn, m0, n0, batch, split);
   }
 };
 
@@ -500,7 +532,15 @@ TA_GEMM_F32_FAMILY(m64n64, 64, 64, 2, 2, 16)
 TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4, 16)
 TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2, 16)
 
-// Full 256x256 tiles of f32 A and B with K % 64 == 0 (see GemmF32Mi16).
+// Whole tiles of f32 A and B whose K windows hold multiples of 64 rows
+// (see GemmF32Mi16): the 256x256 data-parallel tile and the two skinny
+// split-K stage-1 tiles.
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m256n256_mi16(GemmArgs p) {
-  GemmF32Mi16<4>::run(p);
+  GemmF32Mi16<256, 256, 2, 2, 4>::run(p);
+}
+extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m64n256_mi16(GemmArgs p) {
+  GemmF32Mi16<64, 256, 1, 4, 4>::run(p);
+}
+extern "C" __global__ __launch_bounds__(128) void ta_gemm_f32_m32n128_mi16(GemmArgs p) {
+  GemmF32Mi16<32, 128, 1, 2, 4>::run(p);
 }

@@ -378,10 +378,12 @@ struct ExecutorImpl {
       a.a = splitk_scratch;
     }
     const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
-    const bool mi16 = s.kind == KernelKind::GemmF32 && s.tile_m == 256 && s.tile_n == 256 &&
-                      a.num_splits == 1 && f32_mi16_ok(d);
+    const bool mi16 = s.kind == KernelKind::GemmF32 && f32_mi16_ok(d, s.tile_m, s.tile_n,
+                                                                   a.num_splits);
+    const uint32_t threads =
+        mi16 ? (s.tile_m == 256 ? 256u : s.tile_m == 64 ? 256u : 128u) : gemm_threads(s);
     launch(std::string(s.symbol) + (mi16 ? "_mi16" : lds ? "_lds" : vec ? "_vec" : "_gen"),
-           (uint32_t)gx, 1, (uint32_t)gz, mi16 ? 256u : gemm_threads(s), &a, stream);
+           (uint32_t)gx, 1, (uint32_t)gz, threads, &a, stream);
     if (splits > 1) {
       SplitReduceArgs r{};
       r.scratch = static_cast<const float *>(splitk_scratch);

@@ -1,6 +1,6 @@
-"""GPU parity of the aligned FP32 route (256x256 tiles on
-v_mfma_f32_16x16x4_f32, taken when M and N are multiples of 256 and K of
-64) against the CPU oracle, with every epilogue, alpha / accumulate and
+"""GPU parity of the aligned FP32 route (256x256, 64x256 and 32x128 tiles
+on v_mfma_f32_16x16x4_f32, taken when M and N are multiples of the tile
+and K of 64) against the CPU oracle, with every epilogue, alpha / accumulate and
 the batch-broadcast forms; shapes just off the alignment take the other
 kernels and must agree too.  Tolerances as in test_gemm_gpu.check_f32.
 """
@@ -12,9 +12,9 @@ from test_gemm_gpu import run_case
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def kex(ta, ctx):
-    e = ta.Executor(ctx, kernel_selection="f32_m256n256", tune=False)
+@pytest.fixture(scope="module", params=["f32_m256n256", "f32_m64n256", "f32_m32n128"])
+def kex(ta, ctx, request):
+    e = ta.Executor(ctx, kernel_selection=request.param, tune=False)
     yield e
     e.close()
 

@@ -305,6 +305,9 @@ def test_config4_splitk_deterministic(ta, ex, oracle, m, n, k, splits):
 @pytest.mark.parametrize("m,n,k,splits,alpha,batch", [
     (64, 64, 8192, 16, 1.0, 1), (256, 256, 4096, 4, 1.0, 1), (101, 103, 999, 7, 1.0, 1),
     (33, 65, 4000, 5, 0.25, 3),
+    # windows of whole 64-deep stages: the pipelined stage-1 kernels
+    (64, 512, 8192, 4, 0.5, 2), (32, 256, 16384, 8, 1.0, 1), (64, 256, 4160, 5, 1.0, 1),
+    (32, 128, 8192, 2, 2.0, 3),
 ])
 def test_splitk_shapes(ta, ex, oracle, m, n, k, splits, alpha, batch):
     """tests/correctness/splitk2.rs:48-122 shapes (odd, batched, alpha)."""
