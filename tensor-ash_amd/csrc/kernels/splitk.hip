@@ -21,11 +21,13 @@
 namespace {
 constexpr int kThreads = 256, kBatch = 8;
 
-TA_DEVICE f32x4 load_quad(const SplitReduceArgs &p, bool vec, uint64_t base, uint32_t plane) {
-  if (vec) {
-    const uint64_t b = base / p.mn, e = base % p.mn;
-    return *reinterpret_cast<const f32x4 *>(p.scratch + (b * p.num_splits + plane) * p.mn + e);
-  }
+// Quad starting at element `base` of plane `plane`; `off0` is its offset
+// in plane 0 of its batch (vector path only: mn % 4 == 0 keeps a quad in
+// one batch).
+TA_DEVICE f32x4 load_quad(const SplitReduceArgs &p, bool vec, uint64_t base, uint64_t off0,
+                          uint32_t plane) {
+  if (vec)
+    return *reinterpret_cast<const f32x4 *>(p.scratch + off0 + (uint64_t)plane * p.mn);
   f32x4 v = {0.f, 0.f, 0.f, 0.f};
   for (uint32_t c = 0; c < 4; ++c) {
     const uint64_t i = base + c;
@@ -53,18 +55,20 @@ extern "C" __global__ __launch_bounds__(kThreads) void ta_splitk_reduce(SplitRed
     const uint64_t q = qb * QW + ql;
     if (q < quads) {
       // Planes lo..hi-1 in order, loaded kBatch at a time ahead of their
-      // adds so the loads overlap; the adds keep the plane order.
+      // adds so the loads overlap (one round trip when hi - lo <= kBatch);
+      // the adds keep the plane order.
       const uint64_t base = q * 4;
-      f32x4 acc = load_quad(p, vec, base, lo);
-      for (uint32_t s0 = lo + 1; s0 < hi; s0 += kBatch) {
+      const uint64_t off0 = vec ? (base / p.mn) * P * p.mn + base % p.mn : 0;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (uint32_t s0 = lo; s0 < hi; s0 += kBatch) {
         f32x4 v[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j)
-          v[j] = s0 + j < hi ? load_quad(p, vec, base, s0 + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+          v[j] = s0 + j < hi ? load_quad(p, vec, base, off0, s0 + j) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < kBatch; ++j)
           if (s0 + j < hi)
-            acc += v[j];
+            acc = s0 + j == lo ? v[j] : acc + v[j];
       }
       part[g * QW + ql] = acc;
     }

@@ -307,7 +307,7 @@ struct ExecutorImpl {
     const KernelSpec &s = KERNEL_SPECS[p.kernel];
     if (p.splitk2) {
       need.splitk = (uint64_t)d.batch * d.m * d.n * *p.splitk2 *
-                    splitk_sub_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, *p.splitk2) * 4;
+                    splitk_sub_splits(ctx->cu_count(), d, *p.splitk2) * 4;
     } else if (s.is_gemv()) {
       GemvPlan g = plan_gemv(ctx->cu_count(), d.m, d.n, d.k, s.tile_n, p.role == 2,
                             gemv_unit(s.tile_n, s.kind == KernelKind::GemvF32Row, p.role == 2, d.m));
@@ -340,7 +340,7 @@ struct ExecutorImpl {
     a.k = d.k;
     a.alpha = op.call.alpha;
     const uint32_t sub =
-        splits > 1 ? splitk_sub_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, splits) : 1;
+        splits > 1 ? splitk_sub_splits(ctx->cu_count(), d, splits) : 1;
     a.num_splits = std::max(1u, splits) * sub;
     a.sub_splits = sub;
     if (splits <= 1) {

@@ -235,35 +235,44 @@ uint32_t gemm_threads(const KernelSpec &s) {
   return s.tile_m == 32 ? 128 : 256;
 }
 
-// Sub-windows per split for stage 1.  A stage-1 workgroup keeps about one
-// 16-deep K slab of A and B in flight, so HBM needs several hundred of
-// them: aim for 4 workgroups per CU (8 for 128-thread tiles), with >= 256
-// K values per window, grid z <= 65535, u32 scratch addressing and at most
-// 256 MiB of partial planes.
-uint32_t splitk_sub_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
-                           uint32_t splits) {
-  if (splits < 2 || batch == 0)
+// Sub-windows per split for stage 1.  A stage-1 workgroup of the plain
+// FP32 kernels keeps about one 16-deep K slab of A and B in flight, so HBM
+// needs several hundred of them: aim for 4 workgroups per CU (8 for
+// 128-thread tiles), with >= 256 K values per window.  The pipelined
+// kernels (f32 operands, whole tiles, 64-aligned windows) keep three
+// slabs in flight and are fastest at one workgroup per CU, which also
+// halves the partial planes the reduce reads.  Always: grid z <= 65535,
+// u32 scratch addressing and at most 256 MiB of partial planes.
+uint32_t splitk_sub_splits(uint32_t cus, const ResolvedMatmul &d, uint32_t splits) {
+  if (splits < 2 || d.batch == 0)
     return 1;
-  const KernelSpec &s = splitk_stage1_spec(m, n);
-  const uint64_t tiles = (uint64_t)batch * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
+  const KernelSpec &s = splitk_stage1_spec(d.m, d.n);
+  const uint64_t tiles = (uint64_t)d.batch * div_ceil(d.m, s.tile_m) * div_ceil(d.n, s.tile_n);
+  const uint64_t plane = (uint64_t)d.batch * d.m * d.n;
+  auto capped = [&](uint64_t t) {
+    t = std::min<uint64_t>(t, 65535 / ((uint64_t)d.batch * splits));
+    t = std::min<uint64_t>(t, std::max<uint64_t>(1, ((uint64_t)UINT32_MAX + 1) / (plane * splits)));
+    t = std::min<uint64_t>(t, std::max<uint64_t>(1, (256ull << 20) / (plane * 4 * splits)));
+    return (uint32_t)std::max<uint64_t>(1, t);
+  };
+  const uint32_t one_per_cu =
+      capped(std::max<uint64_t>(1, (cus + tiles * splits - 1) / (tiles * splits)));
+  if (f32_mi16_ok(d, s.tile_m, s.tile_n, splits * one_per_cu))
+    return one_per_cu;
   const uint64_t target = (uint64_t)cus * (gemm_threads(s) <= 128 ? 8 : 4);
   uint64_t t = std::max<uint64_t>(1, (target + tiles * splits - 1) / (tiles * splits));
-  t = std::min<uint64_t>(t, std::max<uint64_t>(1, k / ((uint64_t)splits * 256)));
-  t = std::min<uint64_t>(t, 65535 / ((uint64_t)batch * splits));
-  const uint64_t plane = (uint64_t)batch * m * n;
-  t = std::min<uint64_t>(t, std::max<uint64_t>(1, ((uint64_t)UINT32_MAX + 1) / (plane * splits)));
-  t = std::min<uint64_t>(t, std::max<uint64_t>(1, (256ull << 20) / (plane * 4 * splits)));
-  return (uint32_t)std::max<uint64_t>(1, t);
+  t = std::min<uint64_t>(t, std::max<uint64_t>(1, d.k / ((uint64_t)splits * 256)));
+  return capped(t);
 }
 
 // Plane groups per element for the split-K reduce: at least 8, then
-// doubled (up to the plane count and 256) until quads * groups threads
-// give every CU about two workgroups' worth of loads, so small outputs
-// with many planes still spread over the chip.  A function of the shape
+// doubled (up to 256, keeping >= 4 planes per group) until quads * groups
+// threads give every CU about two workgroups' worth of loads, so small
+// outputs with many planes still spread over the chip.  A function of the shape
 // only, which keeps the summation order fixed.
 uint32_t splitk_reduce_groups(uint32_t cus, uint64_t quads, uint32_t planes) {
   uint32_t g = 8;
-  while (g < 256 && 2 * g <= planes && quads * g < 512ull * cus)
+  while (g < 256 && 8ull * g <= planes && quads * g < 512ull * cus)
     g *= 2;
   while (g > 1 && g > planes)
     g /= 2;

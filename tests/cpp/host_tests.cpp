@@ -162,7 +162,8 @@ static void test_splitk() {
   // function of the shape (fixed summation order), and more groups for
   // small outputs.
   CHECK(splitk_reduce_groups(256, 4096, 256) == 32);
-  CHECK(splitk_reduce_groups(256, 1024, 256) == 128);
+  CHECK(splitk_reduce_groups(256, 1024, 256) == 64); // >= 4 planes per group
+  CHECK(splitk_reduce_groups(256, 1024, 512) == 128);
   CHECK(splitk_reduce_groups(256, 1u << 20, 64) == 8);
   CHECK(splitk_reduce_groups(256, 16, 3) == 2);
   CHECK(splitk_reduce_groups(256, 16, 2) == 2);
