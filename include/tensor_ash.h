@@ -302,6 +302,56 @@ int ta_flash_attention(const ta_executor *exec, const ta_tensor *q,
                        const ta_tensor *out, const ta_flash_desc *desc,
                        ta_run_stats *stats);
 
+/* Host-visible u32 cells (src/executor/cells.rs:10-205; Rust API only in
+ * the reference): pinned, mapped host memory that kernels read and write
+ * through ta_u32_cell_device_address and the host through
+ * ta_u32_cell_write / ta_u32_cell_read between submissions.  cap 1 plays
+ * PosBuffer (create_pos_buffer) and HostU32Buffer
+ * (create_host_u32_buffer); cap n plays TokenIdBuffer
+ * (create_token_id_buffer).  Cells start zeroed.  ta_u32_cell_write fails
+ * when n exceeds cap; ta_u32_cell_read returns element 0. */
+typedef struct ta_u32_cell ta_u32_cell;
+ta_u32_cell *ta_u32_cell_create(ta_context *ctx, uint32_t cap);
+void ta_u32_cell_destroy(ta_u32_cell *cell);
+int ta_u32_cell_write(ta_u32_cell *cell, const uint32_t *values, size_t n);
+int ta_u32_cell_read(const ta_u32_cell *cell, uint32_t *value);
+uint64_t ta_u32_cell_device_address(const ta_u32_cell *cell);
+uint32_t ta_u32_cell_cap(const ta_u32_cell *cell);
+
+/* The GPU token loop, Executor::run_argmax / run_embed_gather /
+ * run_embed_gather_rows (src/executor/elementwise/ops.rs:456-595; Rust
+ * API only in the reference).  ta_argmax writes to element 0 of `result`
+ * the index of the largest value of `input` (f32, any shape, read flat),
+ * the largest index among equal maxima (the reference's greedy sampler).
+ * ta_embed_gather copies row min(tokens[t], vocab - 1) of `table`
+ * ([vocab, embd], f32 or f16) to row t of `out` ([embd] or [t, embd], f32
+ * or f16), reading the ids when the op runs, so it can follow ta_argmax in
+ * a graph with no host round trip. */
+int ta_argmax(const ta_executor *exec, const ta_tensor *input, ta_u32_cell *result,
+              ta_run_stats *stats);
+int ta_embed_gather(const ta_executor *exec, const ta_u32_cell *tokens,
+                    const ta_tensor *table, const ta_tensor *out, ta_run_stats *stats);
+
+/* Fused split-K decode attention, Executor::run_attn_decode
+ * (src/executor/elementwise/attn.rs:14-185; AttnDecodeDesc,
+ * src/executor/elementwise/mod.rs:200-241; Rust API only in the
+ * reference): out = softmax(q Kt * scale) V for one query row per head
+ * over the kv_len valid cache positions (never reading past them).  q and
+ * out are f32 [kv_heads, group, dh] (group <= 8), kt [kv_heads, dh,
+ * T_max], v [kv_heads, T_max, dh] (f32 or f16, alike), dh 64 or 128.
+ * scratch (f32) holds at least kv_heads * TA_ATTN_DECODE_MAX_CHUNKS *
+ * group * (dh + 2) values.  pos_addr (device address of a u32 cell, 0 =
+ * none) adds the cell's value to kv_len when the op runs. */
+#define TA_ATTN_DECODE_MAX_CHUNKS 32
+typedef struct ta_attn_decode_desc {
+  uint32_t kv_len;
+  float scale; /* 1/sqrt(dh) for standard attention */
+  uint64_t pos_addr;
+} ta_attn_decode_desc;
+int ta_attn_decode(const ta_executor *exec, const ta_tensor *q, const ta_tensor *kt,
+                   const ta_tensor *v, const ta_tensor *scratch, const ta_tensor *out,
+                   const ta_attn_decode_desc *desc, ta_run_stats *stats);
+
 /* Mixed-op graphs, Executor::run_exec_ops / prepare_exec_ops with ExecOp
  * (src/executor/graph_ops.rs:23-336), Rust-API-only in the reference: a
  * dependent chain of matmuls and model ops run (or recorded once as a
@@ -315,6 +365,9 @@ int ta_flash_attention(const ta_executor *exec, const ta_tensor *q,
  *   ROPE            in[0] input, in[1] table, out; rope
  *   COPY_STRIDED    in[0] src, out dst; copy
  *   FLASH_ATTENTION in[0] q, in[1] kt, in[2] v, out; flash
+ *   ARGMAX          in[0] input; cell result
+ *   EMBED_GATHER    cell token ids, in[0] table, out
+ *   ATTN_DECODE     in[0] q, in[1] kt, in[2] v, aux scratch, out; attn
  * pos_addr (ROPE, COPY_STRIDED): device address of a u32 position cell
  * read when the op runs (added to rope.pos_base; times pos_scale added to
  * copy.dst_offset), so a prepared graph replays at a new position after
@@ -327,6 +380,9 @@ enum {
   TA_EXEC_ROPE = 4,
   TA_EXEC_COPY_STRIDED = 5,
   TA_EXEC_FLASH_ATTENTION = 6,
+  TA_EXEC_ARGMAX = 7,
+  TA_EXEC_EMBED_GATHER = 8,
+  TA_EXEC_ATTN_DECODE = 9,
 };
 typedef struct ta_exec_op {
   uint32_t kind; /* TA_EXEC_* */
@@ -342,6 +398,9 @@ typedef struct ta_exec_op {
   ta_rope_desc rope;
   ta_copy_desc copy;
   ta_flash_desc flash;
+  const ta_u32_cell *cell;
+  const ta_tensor *aux;
+  ta_attn_decode_desc attn;
 } ta_exec_op;
 int ta_run_exec_ops(const ta_executor *exec, const ta_exec_op *ops,
                     size_t n_ops, ta_run_stats *stats);

@@ -322,3 +322,47 @@ def flash_attention(q, kt, v, heads: int, kv_heads: int, t_q: int, t_max: int, d
         p = np.where(mask, np.exp(s - m), 0.0)
         out[h] = (p / p.sum(axis=1, keepdims=True)) @ v64[kh, :span]
     return out.astype(np.float32).reshape(-1)
+
+
+def argmax_last(x) -> int:
+    """Greedy-sampling argmax of shaders/op_argmax_f32.comp and
+    tests/correctness/token_loop.rs:14-22 (cpu_argmax, Rust
+    `max_by(total_cmp)`): the index of the largest value, the LARGEST index
+    among equal maxima; NaNs never win (an all-NaN vector gives 0)."""
+    v = np.asarray(x, np.float32).reshape(-1)
+    if v.size == 0:
+        raise ValueError("argmax of an empty vector")
+    finite = ~np.isnan(v)
+    if not finite.any():
+        return 0
+    return int(np.nonzero(v == v[finite].max())[0][-1])
+
+
+def embed_gather(table, vocab: int, embd: int, tokens, out_f16: bool = False) -> np.ndarray:
+    """Embedding rows of shaders/op_embed_gather.comp: row t of the output is
+    row min(tokens[t], vocab - 1) of the [vocab, embd] table (already holding
+    the stored, e.g. f16-rounded, values); an f16 output holds the values
+    rounded to f16 (RNE)."""
+    t = np.asarray(table, np.float32).reshape(vocab, embd)
+    ids = np.minimum(np.asarray(tokens, np.int64).reshape(-1), vocab - 1)
+    rows = t[ids].reshape(-1)
+    return round_via_f16(rows) if out_f16 else rows.copy()
+
+
+def attn_decode(q, kt, v, kv_heads: int, group: int, t_max: int, dh: int, kv_len: int,
+                scale: float) -> np.ndarray:
+    """Decode attention of tests/correctness/attn_decode.rs:14-54
+    (cpu_attn_decode) in f64: each of the `group` query rows of kv head h
+    (q [kv_heads, group, dh]) attends to cache positions < kv_len with
+    softmax(q . k * scale); kt [kv_heads, dh, t_max], v [kv_heads, t_max, dh];
+    out [kv_heads, group, dh]."""
+    q64 = np.asarray(q, np.float32).reshape(kv_heads, group, dh).astype(np.float64)
+    kt64 = np.asarray(kt, np.float32).reshape(kv_heads, dh, t_max)[:, :, :kv_len].astype(np.float64)
+    v64 = np.asarray(v, np.float32).reshape(kv_heads, t_max, dh)[:, :kv_len].astype(np.float64)
+    out = np.zeros((kv_heads, group, dh))
+    for h in range(kv_heads):
+        s = (q64[h] @ kt64[h]) * float(scale)
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        out[h] = (p / p.sum(axis=1, keepdims=True)) @ v64[h]
+    return out.astype(np.float32).reshape(-1)

@@ -208,6 +208,53 @@ typedef struct FlashArgs {
   uint32_t heads, q_tiles;
 } FlashArgs;
 
+// Greedy-sampling argmax over n f32 values (one workgroup): the index of
+// the largest value, the largest index among equal maxima, to *result.
+typedef struct ArgmaxArgs {
+  const float *in;
+  uint32_t *result;
+  uint32_t n;
+  uint32_t pad;
+} ArgmaxArgs;
+
+// Embedding-row gather: out row t = table row min(tokens[t], vocab - 1),
+// t < n_tokens; table [vocab, embd] f32 or f16, out [n_tokens, embd] f32 or
+// f16.  Grid: (ceil(embd / 1024), n_tokens) workgroups of 256 threads.
+typedef struct EmbedArgs {
+  const uint32_t *tokens;
+  const void *table;
+  void *out;
+  uint32_t embd, vocab, n_tokens;
+  uint32_t table_f16, out_f16;
+  uint32_t pad;
+} EmbedArgs;
+
+// Split-K decode attention, stage 1: workgroup (chunk, kv_head) attends
+// the `group` query rows of kv_head to positions [chunk * cs, min((chunk +
+// 1) * cs, L)), cs = ceil(L / num_chunks), L = kv_len (+ *pos when pos is
+// set), and stores per row {acc[dh], m, l} (m in log2 units) to
+// scratch[kv_head][chunk][row].  q/out [kv_heads, group, dh]; kt [kv_heads,
+// dh, t_max]; v [kv_heads, t_max, dh].
+typedef struct AttnDecodeArgs {
+  const float *q;
+  const void *kt;
+  const void *v;
+  float *scratch;
+  const uint32_t *pos;
+  uint32_t kv_len, num_chunks, group, t_max;
+  float scale;
+  uint32_t pad;
+} AttnDecodeArgs;
+
+// Stage 2: one workgroup per (kv_head, row) merges the num_chunks
+// partials of the row exactly into out[kv_head][row][0..dh).
+typedef struct AttnCombineArgs {
+  const float *scratch;
+  float *out;
+  uint32_t num_chunks, group, dh;
+  uint32_t pad;
+} AttnCombineArgs;
+
 // Persistent decode SwiGLU MLP chain in one launch: `layers` MLPs, layer
 // l+1 reading layer l's output y as its x.  In a layer, `a` is the dual
 // gate/up GEMV (producer of h = act(x Wg) * (x Wu)) and `b` the down-proj

@@ -26,6 +26,9 @@ struct ta_prepared {
   std::unique_ptr<PreparedOps> prepared;
   std::shared_ptr<Context> ctx;
 };
+struct ta_u32_cell {
+  std::unique_ptr<U32Cell> cell;
+};
 
 namespace {
 
@@ -465,6 +468,23 @@ RopeDesc rope_desc(const ta_rope_desc &d) {
   return rd;
 }
 
+const U32Cell *checked_cell(const ta_executor &e, const ta_u32_cell *c, const std::string &op,
+                            const char *operand) {
+  if (!c)
+    fail(op + ": " + operand + " is null");
+  if (c->cell->context() != e.ctx.get())
+    fail(op + ": " + operand + " belongs to a different HIP context");
+  return c->cell.get();
+}
+
+AttnDecodeDesc attn_decode_desc(const ta_attn_decode_desc &d) {
+  AttnDecodeDesc a;
+  a.kv_len = d.kv_len;
+  a.scale = d.scale;
+  a.pos_addr = d.pos_addr;
+  return a;
+}
+
 std::vector<ExecOp> checked_exec_ops(const ta_executor &e, const ta_exec_op *ops, size_t n,
                                      const std::string &fn) {
   if (n > 0 && !ops)
@@ -512,6 +532,18 @@ std::vector<ExecOp> checked_exec_ops(const ta_executor &e, const ta_exec_op *ops
     case TA_EXEC_FLASH_ATTENTION:
       out.push_back(ExecOp::flash_attn(t(o.in[0], "q"), t(o.in[1], "kt"), t(o.in[2], "v"),
                                        t(o.out, "out"), flash_desc(o.flash, where)));
+      break;
+    case TA_EXEC_ARGMAX:
+      out.push_back(ExecOp::argmax(t(o.in[0], "input"), *checked_cell(e, o.cell, where, "cell")));
+      break;
+    case TA_EXEC_EMBED_GATHER:
+      out.push_back(ExecOp::embed_gather(*checked_cell(e, o.cell, where, "cell"),
+                                         t(o.in[0], "table"), t(o.out, "out")));
+      break;
+    case TA_EXEC_ATTN_DECODE:
+      out.push_back(ExecOp::attn_decode(t(o.in[0], "q"), t(o.in[1], "kt"), t(o.in[2], "v"),
+                                        t(o.aux, "scratch"), t(o.out, "out"),
+                                        attn_decode_desc(o.attn)));
       break;
     default:
       fail(where + ": kind " + std::to_string(o.kind) + " is invalid");
@@ -607,6 +639,72 @@ int ta_flash_attention(const ta_executor *exec, const ta_tensor *q, const ta_ten
     const Tensor *to = checked_tensor(e, out, fn, "out");
     const ta_flash_desc &d = checked_ref(desc, "ta_flash_attention: desc is null");
     write_stats(stats, e.exec->run_flash_attention(*tq, *tk, *tv, *to, flash_desc(d, fn)));
+  });
+}
+
+// src/executor/cells.rs:163-205.
+ta_u32_cell *ta_u32_cell_create(ta_context *ctx, uint32_t cap) {
+  return ffi_create<ta_u32_cell>([&] {
+    const ta_context &c = checked_ref(ctx, "ta_u32_cell_create: ctx is null");
+    return new ta_u32_cell{U32Cell::create(c.ctx, cap)};
+  });
+}
+void ta_u32_cell_destroy(ta_u32_cell *cell) { delete cell; }
+int ta_u32_cell_write(ta_u32_cell *cell, const uint32_t *values, size_t n) {
+  return ffi_status([&] {
+    ta_u32_cell &c = const_cast<ta_u32_cell &>(checked_ref(cell, "ta_u32_cell_write: cell is null"));
+    if (n > 0 && !values)
+      fail("ta_u32_cell_write: values is null");
+    c.cell->write(values, n);
+  });
+}
+int ta_u32_cell_read(const ta_u32_cell *cell, uint32_t *value) {
+  return ffi_status([&] {
+    const ta_u32_cell &c = checked_ref(cell, "ta_u32_cell_read: cell is null");
+    if (!value)
+      fail("ta_u32_cell_read: value is null");
+    *value = c.cell->read();
+  });
+}
+uint64_t ta_u32_cell_device_address(const ta_u32_cell *cell) {
+  return cell ? cell->cell->device_address() : 0;
+}
+uint32_t ta_u32_cell_cap(const ta_u32_cell *cell) { return cell ? cell->cell->cap() : 0; }
+
+// src/executor/elementwise/ops.rs:456-595 and attn.rs:14-185.
+int ta_argmax(const ta_executor *exec, const ta_tensor *input, ta_u32_cell *result,
+              ta_run_stats *stats) {
+  return ffi_status([&] {
+    const char *fn = "ta_argmax";
+    const ta_executor &e = checked_ref(exec, "ta_argmax: exec is null");
+    const Tensor *in = checked_tensor(e, input, fn, "input");
+    write_stats(stats, e.exec->run_argmax(*in, *checked_cell(e, result, fn, "result")));
+  });
+}
+int ta_embed_gather(const ta_executor *exec, const ta_u32_cell *tokens, const ta_tensor *table,
+                    const ta_tensor *out, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const char *fn = "ta_embed_gather";
+    const ta_executor &e = checked_ref(exec, "ta_embed_gather: exec is null");
+    const U32Cell *tc = checked_cell(e, tokens, fn, "tokens");
+    const Tensor *tt = checked_tensor(e, table, fn, "table");
+    const Tensor *to = checked_tensor(e, out, fn, "out");
+    write_stats(stats, e.exec->run_embed_gather(*tc, *tt, *to));
+  });
+}
+int ta_attn_decode(const ta_executor *exec, const ta_tensor *q, const ta_tensor *kt,
+                   const ta_tensor *v, const ta_tensor *scratch, const ta_tensor *out,
+                   const ta_attn_decode_desc *desc, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const char *fn = "ta_attn_decode";
+    const ta_executor &e = checked_ref(exec, "ta_attn_decode: exec is null");
+    const Tensor *tq = checked_tensor(e, q, fn, "q");
+    const Tensor *tk = checked_tensor(e, kt, fn, "kt");
+    const Tensor *tv = checked_tensor(e, v, fn, "v");
+    const Tensor *ts = checked_tensor(e, scratch, fn, "scratch");
+    const Tensor *to = checked_tensor(e, out, fn, "out");
+    const ta_attn_decode_desc &d = checked_ref(desc, "ta_attn_decode: desc is null");
+    write_stats(stats, e.exec->run_attn_decode(*tq, *tk, *tv, *ts, *to, attn_decode_desc(d)));
   });
 }
 

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cctype>
 #include <cstdlib>
+#include <cstring>
 #include <fstream>
 #include <iterator>
 #include <sstream>
@@ -240,5 +241,46 @@ uint64_t Tensor::len() const {
 uint64_t Tensor::size_bytes() const { return len() * dtype_size(dtype_); }
 void *Tensor::device_ptr() const { return buffer_->ptr; }
 bool Tensor::belongs_to(const Context *ctx) const { return buffer_->ctx.get() == ctx; }
+
+// src/executor/cells.rs:163-205 (create_pos_buffer / create_host_u32_buffer
+// / create_token_id_buffer): pinned, mapped host memory, zero-filled.
+std::unique_ptr<U32Cell> U32Cell::create(const std::shared_ptr<Context> &ctx, uint32_t cap) {
+  if (!ctx)
+    fail("create_u32_cell: null context");
+  if (cap == 0)
+    fail("create_token_id_buffer: cap must be non-zero");
+  ctx->make_current();
+  std::unique_ptr<U32Cell> c(new U32Cell());
+  void *host = nullptr;
+  hip_check(hipHostMalloc(&host, (size_t)cap * 4, hipHostMallocMapped), "hipHostMalloc (u32 cell)");
+  void *dev = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&dev, host, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(host);
+    hip_check(e, "hipHostGetDevicePointer (u32 cell)");
+  }
+  std::memset(host, 0, (size_t)cap * 4);
+  c->ctx_ = ctx;
+  c->host_ = static_cast<uint32_t *>(host);
+  c->device_ = reinterpret_cast<uint64_t>(dev);
+  c->cap_ = cap;
+  return c;
+}
+
+U32Cell::~U32Cell() {
+  if (host_)
+    (void)hipHostFree(host_);
+}
+
+// cells.rs:134-149 (TokenIdBuffer::write): the first n slots.
+void U32Cell::write(const uint32_t *values, size_t n) {
+  if (n > cap_)
+    fail("TokenIdBuffer::write: " + std::to_string(n) + " ids exceeds cap " + std::to_string(cap_));
+  volatile uint32_t *dst = host_;
+  for (size_t i = 0; i < n; ++i)
+    dst[i] = values[i];
+}
+
+uint32_t U32Cell::read() const { return *static_cast<volatile uint32_t *>(host_); }
 
 } // namespace tensor_ash

@@ -152,14 +152,16 @@ struct ScratchNeed {
 // anything is recorded.
 struct ElemLaunch {
   std::string symbol;
-  uint32_t groups = 0;
+  uint32_t groups = 0, gy = 1, threads = 256;
   std::vector<uint8_t> args;
 };
+// A model op: one launch, or several in stream order (decode attention).
+using ElemLaunches = std::vector<ElemLaunch>;
 
 } // namespace
 
 struct ExecutorImpl;
-ElemLaunch plan_exec_elem(ExecutorImpl &e, const ExecOp &op);
+ElemLaunches plan_exec_elem(ExecutorImpl &e, const ExecOp &op);
 
 struct ExecutorImpl {
   std::shared_ptr<Context> ctx;
@@ -797,17 +799,23 @@ struct ExecutorImpl {
 
   // One model-op launch on a slot between its events
   // (elementwise/mod.rs:498-515: n_calls 1, no flops).
-  RunStats run_elem(const ElemLaunch &l) {
+  RunStats run_elem(const ElemLaunch &l) { return run_elem(ElemLaunches{l}); }
+  RunStats run_elem(const ElemLaunches &ls) {
     ctx->make_current();
     Lease lease(this);
     Slot *slot = lease.s;
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
-    launch(l.symbol, l.groups, 1, 1, 256, const_cast<uint8_t *>(l.args.data()), slot->stream);
+    record_elem(ls, slot->stream);
     hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
     hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
     float ms = 0.f;
     hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
-    return RunStats{(uint64_t)((double)ms * 1e6), 1, 0};
+    return RunStats{(uint64_t)((double)ms * 1e6), ls.size(), 0};
+  }
+  void record_elem(const ElemLaunches &ls, hipStream_t stream) const {
+    for (const ElemLaunch &l : ls)
+      launch(l.symbol, l.groups, l.gy, 1, l.threads, const_cast<uint8_t *>(l.args.data()),
+             stream);
   }
 
   // ---- mixed-op graphs (src/executor/graph_ops.rs:244-620) ----
@@ -819,7 +827,7 @@ struct ExecutorImpl {
     std::vector<MatmulOp> ops;
     std::vector<ResolvedMatmul> res;
     std::vector<OpPlan> plans;
-    ElemLaunch elem;
+    ElemLaunches elems;
   };
   std::vector<ExecStep> plan_exec(const std::vector<ExecOp> &ops, uint64_t &flops) {
     std::vector<ExecStep> steps;
@@ -834,7 +842,7 @@ struct ExecutorImpl {
         steps.back().res.push_back(ResolvedMatmul::from_op(op.matmul));
       } else {
         steps.emplace_back();
-        steps.back().elem = plan_exec_elem(*this, op);
+        steps.back().elems = plan_exec_elem(*this, op);
       }
     }
     flops = 0;
@@ -872,8 +880,7 @@ struct ExecutorImpl {
       if (st.matmul)
         record(st.ops, st.res, st.plans, scratch, status, stream);
       else
-        launch(st.elem.symbol, st.elem.groups, 1, 1, 256,
-               const_cast<uint8_t *>(st.elem.args.data()), stream);
+        record_elem(st.elems, stream);
     }
   }
   RunStats run_exec_impl(const std::vector<ExecOp> &ops) {
@@ -1587,9 +1594,156 @@ ElemLaunch plan_flash(ExecutorImpl &e, const Tensor &q, const Tensor &kt, const 
                           : (dh == 64 ? "ta_flash_attention_dh64" : "ta_flash_attention_dh128");
   return elem(sym, (uint32_t)groups, a);
 }
+
+// ops.rs:467-500 (plan_argmax): f32 input, any shape, read flat.
+ElemLaunch plan_argmax(ExecutorImpl &e, const Tensor &input, const U32Cell &result) {
+  const std::string op = "run_argmax";
+  e.validate_tensor(&input, "input");
+  ensure_f32(input, op, "input");
+  if (result.context() != e.ctx.get())
+    fail(op + ": result buffer belongs to a different context");
+  if (input.len() > UINT32_MAX)
+    fail(op + ": input length exceeds u32");
+  if (input.len() == 0)
+    fail(op + ": input is empty");
+  ArgmaxArgs a{};
+  a.in = static_cast<const float *>(input.device_ptr());
+  a.result = reinterpret_cast<uint32_t *>(result.device_address());
+  a.n = (uint32_t)input.len();
+  ElemLaunch l = elem("ta_argmax_f32", 1, a);
+  l.threads = 1024;
+  return l;
+}
+
+// ops.rs:529-595 (plan_embed_gather): table [vocab, embd] f32 or f16, out
+// [embd] or [t, embd] f32 or f16, ids from the cell's first t slots.
+ElemLaunch plan_embed_gather(ExecutorImpl &e, const U32Cell &tokens, const Tensor &table,
+                             const Tensor &out) {
+  const std::string op = "run_embed_gather";
+  e.validate_tensor(&table, "table");
+  e.validate_tensor(&out, "out");
+  if (tokens.context() != e.ctx.get())
+    fail(op + ": token buffer belongs to a different context");
+  if (table.shape().size() != 2)
+    fail(op + ": table must be [vocab, embd], got " + fmt_shape(table.shape()));
+  const uint32_t vocab = table.shape()[0], embd = table.shape()[1];
+  if (vocab == 0 || embd == 0)
+    fail(op + ": table " + fmt_shape(table.shape()) + " has a zero axis");
+  uint32_t n_tokens = 0;
+  const auto &os = out.shape();
+  if (os.size() == 1 && os[0] == embd)
+    n_tokens = 1;
+  else if (os.size() == 2 && os[1] == embd && os[0] > 0)
+    n_tokens = os[0];
+  else
+    fail(op + ": out shape " + fmt_shape(os) + " must be [embd] or [t, embd] with embd=" +
+         std::to_string(embd));
+  const uint64_t need = (uint64_t)n_tokens * 4;
+  if ((uint64_t)tokens.cap() * 4 < need)
+    fail(op + ": token buffer " + std::to_string((uint64_t)tokens.cap() * 4) + " B < " +
+         std::to_string(need) + " B for " + std::to_string(n_tokens) + " ids");
+  if (n_tokens > 65535)
+    fail(op + ": " + std::to_string(n_tokens) + " rows exceed the launch grid (65535)");
+  EmbedArgs a{};
+  a.tokens = reinterpret_cast<const uint32_t *>(tokens.device_address());
+  a.table = table.device_ptr();
+  a.out = out.device_ptr();
+  a.embd = embd;
+  a.vocab = vocab;
+  a.n_tokens = n_tokens;
+  a.table_f16 = table.dtype() == DType::F16;
+  a.out_f16 = out.dtype() == DType::F16;
+  ElemLaunch l = elem("ta_embed_gather", (embd + 1023) / 1024, a);
+  l.gy = n_tokens;
+  return l;
+}
+
+// Decode-attention chunk count (elementwise/mod.rs:233-241): about 64
+// positions (one wave block) per chunk, at least 8 and at most
+// kAttnDecodeMaxChunks chunks; position-driven launches always use the cap.
+uint32_t attn_decode_num_chunks(uint32_t kv_len) {
+  return std::min(kAttnDecodeMaxChunks, std::max(8u, (kv_len + 63) / 64));
+}
+
+// attn.rs:61-184 (plan_attn_decode): the same checks in the same order;
+// dh 64 and 128 are compiled.
+ElemLaunches plan_attn_decode(ExecutorImpl &e, const Tensor &q, const Tensor &kt, const Tensor &v,
+                              const Tensor &scratch, const Tensor &out,
+                              const AttnDecodeDesc &desc) {
+  const std::string op = "run_attn_decode";
+  e.validate_tensor(&q, "q");
+  ensure_f32(q, op, "q");
+  e.validate_tensor(&kt, "kt");
+  e.validate_tensor(&v, "v");
+  e.validate_tensor(&scratch, "scratch");
+  ensure_f32(scratch, op, "scratch");
+  e.validate_tensor(&out, "out");
+  ensure_f32(out, op, "out");
+  if (kt.dtype() != v.dtype())
+    fail(op + ": kt (" + dtype_name(kt.dtype()) + ") and v (" + dtype_name(v.dtype()) +
+         ") must share a storage type");
+  const bool kv16 = kt.dtype() == DType::F16;
+  if (kt.shape().size() != 3)
+    fail(op + ": kt must be [H_kv, dh, T_max], got " + fmt_shape(kt.shape()));
+  if (v.shape().size() != 3)
+    fail(op + ": v must be [H_kv, T_max, dh], got " + fmt_shape(v.shape()));
+  const uint32_t kv_heads = kt.shape()[0], dh = kt.shape()[1], t_max = kt.shape()[2];
+  if (v.shape()[2] != dh || v.shape()[1] != t_max || v.shape()[0] != kv_heads || kv_heads == 0)
+    fail(op + ": inconsistent caches kt " + fmt_shape(kt.shape()) + ", v " +
+         fmt_shape(v.shape()));
+  if (dh != 64 && dh != 128)
+    fail(op + ": head dimension " + std::to_string(dh) +
+         " unsupported (compiled variants: 64, 128)");
+  const uint64_t heads_elems = (uint64_t)kv_heads * dh;
+  if (q.len() == 0 || q.len() % heads_elems != 0)
+    fail(op + ": q length " + std::to_string(q.len()) + " must be kv_heads*group*dh (kv_heads " +
+         std::to_string(kv_heads) + ", dh " + std::to_string(dh) + ")");
+  const uint64_t group = q.len() / heads_elems;
+  if (group == 0 || group > 8)
+    fail(op + ": GQA group " + std::to_string(group) + " unsupported (1..=8)");
+  if (out.len() != q.len())
+    fail(op + ": out length " + std::to_string(out.len()) + " must equal q length " +
+         std::to_string(q.len()));
+  if (desc.kv_len == 0 || desc.kv_len > t_max)
+    fail(op + ": kv_len " + std::to_string(desc.kv_len) + " out of range 1..=" +
+         std::to_string(t_max));
+  const uint32_t num_chunks =
+      desc.pos_addr ? kAttnDecodeMaxChunks : attn_decode_num_chunks(desc.kv_len);
+  const uint64_t needed = (uint64_t)kv_heads * num_chunks * group * (dh + 2);
+  if (scratch.len() < needed)
+    fail(op + ": scratch length " + std::to_string(scratch.len()) + " < required " +
+         std::to_string(needed) + " (kv_heads " + std::to_string(kv_heads) + " * chunks " +
+         std::to_string(num_chunks) + " * group " + std::to_string(group) + " * (dh+2))");
+  if (kv_heads > 65535)
+    fail(op + ": " + std::to_string(kv_heads) + " kv heads exceed the launch grid (65535)");
+  AttnDecodeArgs a{};
+  a.q = static_cast<const float *>(q.device_ptr());
+  a.kt = kt.device_ptr();
+  a.v = v.device_ptr();
+  a.scratch = static_cast<float *>(scratch.device_ptr());
+  a.pos = reinterpret_cast<const uint32_t *>(desc.pos_addr);
+  a.kv_len = desc.kv_len;
+  a.num_chunks = num_chunks;
+  a.group = (uint32_t)group;
+  a.t_max = t_max;
+  a.scale = desc.scale;
+  const char *sym = kv16 ? (dh == 64 ? "ta_attn_decode_kv16_dh64" : "ta_attn_decode_kv16_dh128")
+                         : (dh == 64 ? "ta_attn_decode_dh64" : "ta_attn_decode_dh128");
+  ElemLaunch stage1 = elem(sym, num_chunks, a);
+  stage1.gy = kv_heads;
+  AttnCombineArgs c{};
+  c.scratch = a.scratch;
+  c.out = static_cast<float *>(out.device_ptr());
+  c.num_chunks = num_chunks;
+  c.group = (uint32_t)group;
+  c.dh = dh;
+  ElemLaunch combine = elem("ta_attn_decode_combine", (uint32_t)(kv_heads * group), c);
+  combine.threads = 64;
+  return {stage1, combine};
+}
 } // namespace
 
-ElemLaunch plan_exec_elem(ExecutorImpl &e, const ExecOp &op) {
+ElemLaunches plan_exec_elem(ExecutorImpl &e, const ExecOp &op) {
   auto need = [&](const Tensor *t, const char *role) -> const Tensor & {
     if (!t)
       fail(std::string("run_exec_ops: ") + role + " tensor is null");
@@ -1597,21 +1751,32 @@ ElemLaunch plan_exec_elem(ExecutorImpl &e, const ExecOp &op) {
   };
   switch (op.kind) {
   case ExecOp::Kind::RmsNorm:
-    return plan_norm(e, "run_rms_norm", need(op.in[0], "input"), need(op.in[1], "weight"),
-                     nullptr, need(op.out, "output"), op.scalar);
+    return {plan_norm(e, "run_rms_norm", need(op.in[0], "input"), need(op.in[1], "weight"),
+                     nullptr, need(op.out, "output"), op.scalar)};
   case ExecOp::Kind::LayerNorm:
-    return plan_norm(e, "run_layer_norm", need(op.in[0], "input"), need(op.in[1], "weight"),
-                     &need(op.in[2], "bias"), need(op.out, "output"), op.scalar);
+    return {plan_norm(e, "run_layer_norm", need(op.in[0], "input"), need(op.in[1], "weight"),
+                     &need(op.in[2], "bias"), need(op.out, "output"), op.scalar)};
   case ExecOp::Kind::SoftmaxRows:
-    return plan_softmax(e, need(op.in[0], "input"), need(op.out, "output"), op.scalar, op.mask);
+    return {plan_softmax(e, need(op.in[0], "input"), need(op.out, "output"), op.scalar, op.mask)};
   case ExecOp::Kind::Rope:
-    return plan_rope(e, need(op.in[0], "input"), need(op.in[1], "table"), need(op.out, "output"),
-                     op.rope);
+    return {plan_rope(e, need(op.in[0], "input"), need(op.in[1], "table"), need(op.out, "output"),
+                     op.rope)};
   case ExecOp::Kind::CopyStrided:
-    return plan_copy(e, need(op.in[0], "src"), need(op.out, "dst"), op.copy);
+    return {plan_copy(e, need(op.in[0], "src"), need(op.out, "dst"), op.copy)};
   case ExecOp::Kind::FlashAttn:
-    return plan_flash(e, need(op.in[0], "q"), need(op.in[1], "kt"), need(op.in[2], "v"),
-                      need(op.out, "out"), op.flash);
+    return {plan_flash(e, need(op.in[0], "q"), need(op.in[1], "kt"), need(op.in[2], "v"),
+                      need(op.out, "out"), op.flash)};
+  case ExecOp::Kind::Argmax:
+    if (!op.cell)
+      fail("run_exec_ops: result cell is null");
+    return {plan_argmax(e, need(op.in[0], "input"), *op.cell)};
+  case ExecOp::Kind::EmbedGather:
+    if (!op.cell)
+      fail("run_exec_ops: token cell is null");
+    return {plan_embed_gather(e, *op.cell, need(op.in[0], "table"), need(op.out, "out"))};
+  case ExecOp::Kind::AttnDecode:
+    return plan_attn_decode(e, need(op.in[0], "q"), need(op.in[1], "kt"), need(op.in[2], "v"),
+                            need(op.aux, "scratch"), need(op.out, "out"), op.attn);
   case ExecOp::Kind::Matmul:
     break;
   }
@@ -1641,6 +1806,18 @@ RunStats Executor::run_copy_strided(const Tensor &src, const Tensor &dst,
 RunStats Executor::run_flash_attention(const Tensor &q, const Tensor &kt, const Tensor &v,
                                        const Tensor &out, const FlashAttentionDesc &desc) const {
   return impl_->run_elem(plan_flash(*impl_, q, kt, v, out, desc));
+}
+RunStats Executor::run_argmax(const Tensor &input, const U32Cell &result) const {
+  return impl_->run_elem(plan_argmax(*impl_, input, result));
+}
+RunStats Executor::run_embed_gather(const U32Cell &tokens, const Tensor &table,
+                                    const Tensor &out) const {
+  return impl_->run_elem(plan_embed_gather(*impl_, tokens, table, out));
+}
+RunStats Executor::run_attn_decode(const Tensor &q, const Tensor &kt, const Tensor &v,
+                                   const Tensor &scratch, const Tensor &out,
+                                   const AttnDecodeDesc &desc) const {
+  return impl_->run_elem(plan_attn_decode(*impl_, q, kt, v, scratch, out, desc));
 }
 RunStats Executor::run_exec_ops(const std::vector<ExecOp> &ops) const {
   return impl_->run_exec_impl(ops);

@@ -213,6 +213,48 @@ struct FlashAttentionDesc {
   std::optional<uint32_t> out_token_major_heads;
 };
 
+// Fused split-K decode attention geometry (src/executor/elementwise/mod.rs:
+// 200-227): one query row per head attends to the kv_len valid cache
+// positions.  pos_addr (device address of a u32 cell, 0 = none) makes the
+// effective length kv_len + *pos_addr, read at execution time, and fixes
+// the chunk count at kAttnDecodeMaxChunks.
+struct AttnDecodeDesc {
+  uint32_t kv_len = 0;
+  float scale = 1.0f;
+  uint64_t pos_addr = 0;
+};
+// Chunk bound of decode attention; sizes its scratch: kv_heads *
+// kAttnDecodeMaxChunks * group * (dh + 2) f32 (elementwise/mod.rs:229-232).
+constexpr uint32_t kAttnDecodeMaxChunks = 32;
+
+class Context;
+
+// Host-visible u32 cells (src/executor/cells.rs:10-205): pinned, mapped
+// host memory that kernels read and write through device_address() and
+// the host through write()/read() between submissions.  One type serves
+// the reference's PosBuffer and HostU32Buffer (cap 1) and TokenIdBuffer
+// (cap ids).
+class U32Cell {
+public:
+  static std::unique_ptr<U32Cell> create(const std::shared_ptr<Context> &ctx, uint32_t cap);
+  ~U32Cell();
+  U32Cell(const U32Cell &) = delete;
+  U32Cell &operator=(const U32Cell &) = delete;
+  void set(uint32_t value) { write(&value, 1); }
+  void write(const uint32_t *values, size_t n);
+  uint32_t read() const; // element 0, after the writing submission completed
+  uint64_t device_address() const { return device_; }
+  uint32_t cap() const { return cap_; }
+  const Context *context() const { return ctx_.get(); }
+
+private:
+  U32Cell() = default;
+  std::shared_ptr<Context> ctx_;
+  uint32_t *host_ = nullptr;
+  uint64_t device_ = 0;
+  uint32_t cap_ = 0;
+};
+
 // One step of a mixed-op graph (src/executor/graph_ops.rs:23-171): ops run
 // in list order and each sees every earlier op's writes.  Operand roles:
 //   Matmul      `matmul`
@@ -222,17 +264,34 @@ struct FlashAttentionDesc {
 //   Rope        in[0] input, in[1] table, out, rope
 //   CopyStrided in[0] src, out dst, copy
 //   FlashAttn   in[0] q, in[1] kt, in[2] v, out, flash
+//   Argmax      in[0] input, cell result
+//   EmbedGather cell token ids, in[0] table, out
+//   AttnDecode  in[0] q, in[1] kt, in[2] v, aux scratch, out, attn
 struct ExecOp {
-  enum class Kind { Matmul, RmsNorm, LayerNorm, SoftmaxRows, Rope, CopyStrided, FlashAttn };
+  enum class Kind {
+    Matmul,
+    RmsNorm,
+    LayerNorm,
+    SoftmaxRows,
+    Rope,
+    CopyStrided,
+    FlashAttn,
+    Argmax,
+    EmbedGather,
+    AttnDecode
+  };
   Kind kind = Kind::Matmul;
   MatmulOp matmul;
   std::array<const Tensor *, 3> in{};
   const Tensor *out = nullptr;
+  const Tensor *aux = nullptr;
+  const U32Cell *cell = nullptr;
   float scalar = 0.0f;
   SoftmaxMask mask;
   RopeDesc rope;
   CopyDesc copy;
   FlashAttentionDesc flash;
+  AttnDecodeDesc attn;
 
   static ExecOp from_matmul(const MatmulOp &op) {
     ExecOp e;
@@ -268,6 +327,24 @@ struct ExecOp {
                            const FlashAttentionDesc &desc) {
     ExecOp e = make(Kind::FlashAttn, {&q, &kt, &v}, &out, 0.0f);
     e.flash = desc;
+    return e;
+  }
+
+  static ExecOp argmax(const Tensor &input, const U32Cell &result) {
+    ExecOp e = make(Kind::Argmax, {&input, nullptr, nullptr}, nullptr, 0.0f);
+    e.cell = &result;
+    return e;
+  }
+  static ExecOp embed_gather(const U32Cell &tokens, const Tensor &table, const Tensor &out) {
+    ExecOp e = make(Kind::EmbedGather, {&table, nullptr, nullptr}, &out, 0.0f);
+    e.cell = &tokens;
+    return e;
+  }
+  static ExecOp attn_decode(const Tensor &q, const Tensor &kt, const Tensor &v,
+                            const Tensor &scratch, const Tensor &out, const AttnDecodeDesc &desc) {
+    ExecOp e = make(Kind::AttnDecode, {&q, &kt, &v}, &out, 0.0f);
+    e.aux = &scratch;
+    e.attn = desc;
     return e;
   }
 
@@ -453,6 +530,15 @@ public:
   // v [H_kv, T_max, dh], dh 64 or 128, H a multiple of H_kv.
   RunStats run_flash_attention(const Tensor &q, const Tensor &kt, const Tensor &v,
                                const Tensor &out, const FlashAttentionDesc &desc) const;
+  // The GPU token loop (elementwise/ops.rs:456-595, attn.rs:14-185):
+  // greedy argmax into a cell, the embedding rows of the cell's token ids
+  // (out [embd] or [t, embd]), and split-K decode attention (q / out
+  // [kv_heads, group, dh], group <= 8, dh 64 or 128).
+  RunStats run_argmax(const Tensor &input, const U32Cell &result) const;
+  RunStats run_embed_gather(const U32Cell &tokens, const Tensor &table, const Tensor &out) const;
+  RunStats run_attn_decode(const Tensor &q, const Tensor &kt, const Tensor &v,
+                           const Tensor &scratch, const Tensor &out,
+                           const AttnDecodeDesc &desc) const;
 
   // Mixed-op graphs (src/executor/graph_ops.rs:244-336): every op is
   // validated and planned before anything is launched.

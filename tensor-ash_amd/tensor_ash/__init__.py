@@ -85,12 +85,17 @@ class _FlashDesc(C.Structure):
                 ("reserved", C.c_uint32)]
 
 
+class _AttnDecodeDesc(C.Structure):
+    _fields_ = [("kv_len", C.c_uint32), ("scale", C.c_float), ("pos_addr", C.c_uint64)]
+
+
 class _ExecOp(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("mask_kind", C.c_uint32), ("valid_or_prefix", C.c_uint32),
                 ("rows_per_group", C.c_uint32), ("scalar", C.c_float), ("pos_scale", C.c_uint32),
                 ("pos_addr", C.c_uint64), ("inp", C.c_void_p * 3), ("out", C.c_void_p),
                 ("matmul", C.POINTER(_OpV3)), ("rope", _RopeDesc), ("copy", _CopyDesc),
-                ("flash", _FlashDesc)]
+                ("flash", _FlashDesc), ("cell", C.c_void_p), ("aux", C.c_void_p),
+                ("attn", _AttnDecodeDesc)]
 
 
 class _DispatchInfo(C.Structure):
@@ -142,6 +147,15 @@ _sig("ta_prepared_create_v3", P, P, C.POINTER(_OpV3), sz, u32)
 _sig("ta_tensor_device_address", u64, P)
 _sig("ta_flash_attention", C.c_int, P, P, P, P, P, C.POINTER(_FlashDesc), C.POINTER(RunStats))
 _sig("ta_run_exec_ops", C.c_int, P, C.POINTER(_ExecOp), sz, C.POINTER(RunStats))
+_sig("ta_u32_cell_create", P, P, u32)
+_sig("ta_u32_cell_destroy", None, P)
+_sig("ta_u32_cell_write", C.c_int, P, C.POINTER(u32), sz)
+_sig("ta_u32_cell_read", C.c_int, P, C.POINTER(u32))
+_sig("ta_u32_cell_device_address", u64, P)
+_sig("ta_u32_cell_cap", u32, P)
+_sig("ta_argmax", C.c_int, P, P, P, C.POINTER(RunStats))
+_sig("ta_embed_gather", C.c_int, P, P, P, P, C.POINTER(RunStats))
+_sig("ta_attn_decode", C.c_int, P, P, P, P, P, P, C.POINTER(_AttnDecodeDesc), C.POINTER(RunStats))
 _sig("ta_prepared_create_exec", P, P, C.POINTER(_ExecOp), sz)
 _sig("ta_softmax_rows", C.c_int, P, P, P, f32, u32, u32, u32, C.POINTER(RunStats))
 _sig("ta_rms_norm", C.c_int, P, P, P, P, f32, C.POINTER(RunStats))
@@ -342,7 +356,72 @@ def _ops_array(ops: Sequence[MatmulOp]):
 
 SOFTMAX_MASK_FULL, SOFTMAX_MASK_PREFIX, SOFTMAX_MASK_CAUSAL = 0, 1, 2
 EXEC_MATMUL, EXEC_RMS_NORM, EXEC_LAYER_NORM, EXEC_SOFTMAX_ROWS, EXEC_ROPE, EXEC_COPY_STRIDED, \
-    EXEC_FLASH_ATTENTION = range(7)
+    EXEC_FLASH_ATTENTION, EXEC_ARGMAX, EXEC_EMBED_GATHER, EXEC_ATTN_DECODE = range(10)
+# Chunk bound of decode attention; scratch holds kv_heads * ATTN_DECODE_MAX_CHUNKS
+# * group * (dh + 2) f32 (src/executor/elementwise/mod.rs:229-232).
+ATTN_DECODE_MAX_CHUNKS = 32
+
+
+class U32Cell:
+    """Host-visible u32 cells (src/executor/cells.rs:10-205): pinned, mapped
+    host memory that kernels read and write through `device_address` and the
+    host through set / write / read between submissions.  The reference's
+    PosBuffer and HostU32Buffer are cells of one value, TokenIdBuffer a
+    cell of `cap` values; all start zeroed."""
+
+    def __init__(self, ctx: "Context", cap: int = 1):
+        self._h = _checkp(_lib.ta_u32_cell_create(ctx.handle, cap))
+        self._ctx = ctx
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def device_address(self) -> int:
+        return int(_lib.ta_u32_cell_device_address(self._h))
+
+    @property
+    def cap(self) -> int:
+        return int(_lib.ta_u32_cell_cap(self._h))
+
+    def set(self, value: int) -> None:
+        self.write([value])
+
+    def write(self, values: Sequence[int]) -> None:
+        a = np.ascontiguousarray(values, dtype=np.uint32).reshape(-1)
+        _check(_lib.ta_u32_cell_write(self._h, a.ctypes.data_as(C.POINTER(u32)), a.size))
+
+    def read(self) -> int:
+        v = u32()
+        _check(_lib.ta_u32_cell_read(self._h, C.byref(v)))
+        return int(v.value)
+
+    def close(self):
+        if self._h:
+            _lib.ta_u32_cell_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+PosBuffer = HostU32Buffer = TokenIdBuffer = U32Cell
+
+
+@dataclass
+class AttnDecodeDesc:
+    """src/executor/elementwise/mod.rs:200-227; pos_addr: device address of a
+    u32 cell added to kv_len when the op runs (0 = none)."""
+    kv_len: int
+    scale: float = 1.0
+    pos_addr: int = 0
+
+    def _raw(self) -> _AttnDecodeDesc:
+        return _AttnDecodeDesc(self.kv_len, self.scale, self.pos_addr)
 
 
 @dataclass
@@ -441,6 +520,22 @@ class ExecOp:
     @staticmethod
     def flash_attn(q, kt, v, out, desc: FlashAttentionDesc) -> "ExecOp":
         return ExecOp(EXEC_FLASH_ATTENTION, keep=[q, kt, v, out], inp=[q, kt, v], out=out, flash=desc._raw())
+
+    @staticmethod
+    def argmax(input, result: U32Cell) -> "ExecOp":
+        return ExecOp(EXEC_ARGMAX, keep=[input, result], inp=[input], cell=result.handle)
+
+    @staticmethod
+    def embed_gather(tokens: U32Cell, table, out) -> "ExecOp":
+        """EmbedGather (one id, out [embd]) and EmbedGatherRows (t ids, out [t, embd])."""
+        return ExecOp(EXEC_EMBED_GATHER, keep=[tokens, table, out], inp=[table], out=out, cell=tokens.handle)
+
+    embed_gather_rows = embed_gather
+
+    @staticmethod
+    def attn_decode(q, kt, v, scratch, out, desc: AttnDecodeDesc) -> "ExecOp":
+        return ExecOp(EXEC_ATTN_DECODE, keep=[q, kt, v, scratch, out], inp=[q, kt, v], out=out,
+                      aux=scratch.handle, attn=desc._raw())
 
 
 def _exec_array(ops: Sequence[ExecOp]):
@@ -596,6 +691,36 @@ class Executor:
         st = RunStats()
         d = desc._raw()
         _check(_lib.ta_flash_attention(self._h, q.handle, kt.handle, v.handle, out.handle, C.byref(d), C.byref(st)))
+        return st
+
+    # ---- the GPU token loop (src/executor/elementwise/ops.rs:456-595, attn.rs) ----
+    def create_pos_buffer(self) -> U32Cell:
+        return U32Cell(self.ctx, 1)
+
+    def create_host_u32_buffer(self) -> U32Cell:
+        return U32Cell(self.ctx, 1)
+
+    def create_token_id_buffer(self, cap: int) -> U32Cell:
+        return U32Cell(self.ctx, cap)
+
+    def argmax(self, input: Tensor, result: U32Cell) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_argmax(self._h, input.handle, result.handle, C.byref(st)))
+        return st
+
+    def embed_gather(self, tokens: U32Cell, table: Tensor, out: Tensor) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_embed_gather(self._h, tokens.handle, table.handle, out.handle, C.byref(st)))
+        return st
+
+    embed_gather_rows = embed_gather
+
+    def attn_decode(self, q: Tensor, kt: Tensor, v: Tensor, scratch: Tensor, out: Tensor,
+                    desc: AttnDecodeDesc) -> RunStats:
+        st = RunStats()
+        d = desc._raw()
+        _check(_lib.ta_attn_decode(self._h, q.handle, kt.handle, v.handle, scratch.handle, out.handle,
+                                   C.byref(d), C.byref(st)))
         return st
 
     def run_exec_ops(self, ops: Sequence[ExecOp]) -> RunStats:

@@ -443,3 +443,66 @@ def test_flash_attention_pinned(oracle):
     flat = flat.reshape(heads, t_q, dh)
     assert np.allclose(flat[3, 10], vv[0, :41].astype(np.float64).mean(axis=0), atol=1e-7)
     assert not np.any(oracle.flash_attention(q, kt, v, heads, kv_heads, t_q, t_max, dh, 0, 0, 0.125))
+
+
+def _scan_argmax(v):
+    """The greedy sampler as a scan: keep the last element >= the running best."""
+    best, idx = float("-inf"), 0
+    for i, x in enumerate(v):
+        if x >= best:
+            best, idx = x, i
+    return idx
+
+
+def test_argmax_last_pinned(oracle):
+    """tests/correctness/token_loop.rs:55-95 known answers (last maximum wins),
+    a brute-force scan on tie-heavy vectors, and numpy on reversed input."""
+    n = 32000
+    assert oracle.argmax_last(np.full(n, 1.5, np.float32)) == n - 1
+    x = oracle.fill_det(n, 7201)
+    x[5] = 1.0e6
+    x[20000] = 1.0e6
+    assert oracle.argmax_last(x) == 20000
+    x = np.full(n, -2.0, np.float32)
+    x[0] = 3.0
+    assert oracle.argmax_last(x) == 0
+    assert oracle.argmax_last(np.full(n, -np.inf, np.float32)) == n - 1
+    rng = np.random.default_rng(7)
+    for size in (1, 2, 7, 64, 1000):
+        v = rng.integers(-3, 4, size).astype(np.float32)
+        assert oracle.argmax_last(v) == _scan_argmax(v.tolist())
+        assert oracle.argmax_last(v) == size - 1 - int(np.argmax(v[::-1]))
+    v = np.array([1.0, np.nan, 3.0, np.nan, 3.0, 2.0], np.float32)
+    assert oracle.argmax_last(v) == 4
+    assert oracle.argmax_last(np.full(4, np.nan, np.float32)) == 0
+
+
+def test_embed_gather_pinned(oracle):
+    """tests/correctness/token_loop.rs:97-142: rows by id, ids past the
+    vocabulary clamp to the last row, f16 outputs round each value."""
+    vocab, embd = 301, 320
+    table = oracle.fill_det(vocab * embd, 7301)
+    rows = oracle.embed_gather(table, vocab, embd, [0, 7, vocab - 1, vocab + 100])
+    t = table.reshape(vocab, embd)
+    assert np.array_equal(rows.reshape(4, embd), np.stack([t[0], t[7], t[vocab - 1], t[vocab - 1]]))
+    r16 = oracle.embed_gather(table, vocab, embd, [7], out_f16=True)
+    assert np.array_equal(r16, t[7].astype(np.float16).astype(np.float32))
+
+
+def test_attn_decode_pinned(oracle):
+    """Decode attention equals the (separately pinned) causal prefill oracle
+    for one query row per head at position kv_len - 1; uniform scores (q = 0)
+    give the mean of the valid V rows; a single position returns its V row."""
+    kv_heads, group, t_max, dh, kv_len = 3, 4, 96, 64, 70
+    q = oracle.fill_det(kv_heads * group * dh, 7300)
+    kt = oracle.fill_det(kv_heads * dh * t_max, 7301)
+    v = oracle.fill_det(kv_heads * t_max * dh, 7302)
+    got = oracle.attn_decode(q, kt, v, kv_heads, group, t_max, dh, kv_len, 0.125)
+    ref = oracle.flash_attention(q, kt, v, kv_heads * group, kv_heads, 1, t_max, dh, kv_len, kv_len - 1, 0.125)
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
+    vv = v.reshape(kv_heads, t_max, dh)
+    flat = oracle.attn_decode(np.zeros_like(q), kt, v, kv_heads, group, t_max, dh, kv_len, 0.125)
+    flat = flat.reshape(kv_heads, group, dh)
+    assert np.allclose(flat[2, 3], vv[2, :kv_len].astype(np.float64).mean(axis=0), atol=1e-7)
+    one = oracle.attn_decode(q, kt, v, kv_heads, group, t_max, dh, 1, 0.125).reshape(kv_heads, group, dh)
+    assert np.array_equal(one[1, 2], vv[1, 0])
