@@ -238,6 +238,50 @@ def attention(ta, ex, iters=10):
     return out
 
 
+# (name, kv_heads, group, dh, t_max, kv_len): TinyLlama-1.1B and Llama-3-8B
+# decode steps.
+DECODE_ATTN_CASES = [("tinyllama_kv640", 4, 8, 64, 2048, 640),
+                     ("tinyllama_kv2048", 4, 8, 64, 2048, 2048),
+                     ("llama3_8b_kv4096", 8, 4, 128, 8192, 4096)]
+
+
+def token_loop(ta, ex, iters=20):
+    """The GPU token loop ops: split-K decode attention (f32 and f16
+    caches; bytes = the valid K and V prefix plus q and out), greedy argmax
+    over a vocabulary, and the embedding gather of one token row."""
+    rng = np.random.default_rng(81)
+    out = {}
+    for name, kvh, group, dh, t_max, kv_len in DECODE_ATTN_CASES:
+        q = ex.tensor_from(rng.uniform(-1, 1, (kvh, group, dh)).astype(np.float32))
+        scratch = ex.tensor([kvh * ta.ATTN_DECODE_MAX_CHUNKS * group * (dh + 2)])
+        o = ex.tensor([kvh, group, dh])
+        for kv16 in (False, True):
+            kt = ex.tensor_from(rng.uniform(-1, 1, (kvh, dh, t_max)).astype(np.float32), f16=kv16)
+            v = ex.tensor_from(rng.uniform(-1, 1, (kvh, t_max, dh)).astype(np.float32), f16=kv16)
+            desc = ta.AttnDecodeDesc(kv_len, float(1.0 / np.sqrt(dh)))
+            for _ in range(3):
+                ex.attn_decode(q, kt, v, scratch, o, desc)
+            ns = median_ns([ex.attn_decode(q, kt, v, scratch, o, desc) for _ in range(iters)])
+            nbytes = 2 * kvh * kv_len * dh * (2 if kv16 else 4) + 2 * kvh * group * dh * 4
+            out["attn_decode_" + name + ("_kv16" if kv16 else "_f32")] = dict(
+                us=ns / 1e3, gbps=nbytes / ns, frac_hbm=nbytes / ns / PEAK_HBM)
+    cell = ex.create_host_u32_buffer()
+    for vocab in (32000, 128256):
+        logits = ex.tensor_from(rng.uniform(-1, 1, vocab).astype(np.float32))
+        for _ in range(3):
+            ex.argmax(logits, cell)
+        ns = median_ns([ex.argmax(logits, cell) for _ in range(iters)])
+        out[f"argmax_{vocab}"] = dict(us=ns / 1e3, gbps=vocab * 4 / ns)
+    table = ex.tensor_from(rng.uniform(-1, 1, (32000, 2048)).astype(np.float32), f16=True)
+    row = ex.tensor([1, 2048])
+    cell.set(12345)
+    for _ in range(3):
+        ex.embed_gather(cell, table, row)
+    ns = median_ns([ex.embed_gather(cell, table, row) for _ in range(iters)])
+    out["embed_gather_2048_f16"] = dict(us=ns / 1e3)
+    return out
+
+
 def vendor_reference(iters=20):
     """The vendor libraries on the same shapes, for reference only (not part
     of the product path; the role of the reference's
@@ -357,7 +401,7 @@ def main() -> int:
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (rocprof counter calibration)")
-    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,attention,vendor",
+    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,attention,token_loop,vendor",
                     help="comma list of secondary sections to run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -403,6 +447,9 @@ def main() -> int:
     if "attention" in sections:
         log("causal prefill attention ...")
         secondary["causal_prefill_attention"] = attention(ta, ex)
+    if "token_loop" in sections:
+        log("token loop (decode attention, argmax, gather) ...")
+        secondary["token_loop"] = token_loop(ta, ex)
     if "vendor" in sections:
         log("vendor library reference ...")
         secondary["vendor_reference"] = vendor_reference()

@@ -14,16 +14,18 @@
 //    greedy sampler defines it (Rust `max_by(total_cmp)` on finite data).
 //  * gather: one thread per four columns of an output row, the token id
 //    read on the device and clamped to vocab - 1.
-//  * decode attention, stage 1: workgroup (chunk, kv head), 4 waves that
-//    take 64-position blocks of the chunk in turn.  Per block, lane =
-//    position for the scores (K^T rows are contiguous along positions,
-//    one 256-byte wave load per head dimension), a wave max per query row
-//    sets the block's running maximum, the probabilities go to LDS, and
-//    lane = head dimension for P @ V (V rows are contiguous along dh).
-//    Softmax runs in base 2 (scale folded with log2(e)); the stored max is
-//    in log2 units, which stage 2 undoes with exp2.  Positions at or past
-//    the chunk end are never read.  The four waves' states merge exactly
-//    in LDS.
+//  * decode attention, stage 1: workgroup (chunk, kv head) of 4 waves; wave
+//    w owns query rows w and w + 4 of the GQA group.  The chunk is walked
+//    in 64-position blocks: the four waves stage a block's K^T columns and
+//    V rows into LDS with one batch of coalesced loads each (one memory
+//    round trip per block; positions past the chunk end are never read and
+//    stage as zeros), then every wave computes its rows: lane = position
+//    for the scores, lane = head dimension for P @ V.  q (lane = head
+//    dimension) and the block's probabilities (lane = position) reach the
+//    FMAs through v_readlane as scalar operands.  A wave max per row sets
+//    the block's running maximum.  Softmax runs in base 2 (q pre-scaled by
+//    scale * log2(e)); the stored max is in log2 units, which stage 2
+//    undoes with exp2.
 //  * stage 2: per (kv head, row), the chunks merge exactly:
 //    m* = max m_i, w_i = 2^(m_i - m*), out = sum acc_i w_i / sum l_i w_i.
 #include "common.h"
@@ -73,134 +75,147 @@ template <bool KV16> TA_DEVICE float load_kv(const void *p, uint64_t i) {
 }
 
 template <int DH, bool KV16> struct AttnDecode {
-  static constexpr int DPL = DH / 64; // head dimensions per lane in P @ V
-  static constexpr int KU = 16;       // K^T loads in flight per group
+  static constexpr int DPL = DH / 64;                 // head dimensions per lane
+  static constexpr int RPW = kAttnRows / kAttnWaves;  // query rows per wave
+  static constexpr int KPW = DH / kAttnWaves;         // K^T rows each wave stages
+  static constexpr int VPW = 64 / kAttnWaves;         // V rows each wave stages
   struct Smem {
-    f32x4 qT[DH][kAttnRows / 4];             // q transposed: [d][row]
-    f32x4 P[kAttnWaves][64][kAttnRows / 4];  // block probabilities: [pos][row]
-    float mrg[kAttnWaves][kAttnRows][DH + 2]; // wave states: acc, m, l
+    float k[DH][64]; // K^T block: [d][position]
+    float v[64][DH]; // V block: [position][d]
   };
+
+  static TA_DEVICE float bcast(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+  }
 
   static TA_DEVICE void run(const AttnDecodeArgs &p) {
     __shared__ Smem sm;
     const uint32_t chunk = blockIdx.x, kvh = blockIdx.y;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t group = p.group;
-    float *qT = reinterpret_cast<float *>(sm.qT);
-    for (uint32_t i = tid; i < DH * kAttnRows; i += kAttnThreads) {
-      const uint32_t d = i / kAttnRows, r = i % kAttnRows;
-      qT[i] = r < group ? p.q[((uint64_t)kvh * group + r) * DH + d] : 0.0f;
-    }
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t len = min(p.t_max, p.kv_len + (p.pos ? *p.pos : 0u));
     const uint32_t cs = (len + p.num_chunks - 1) / p.num_chunks;
     const uint32_t p0 = min(chunk * cs, len), p1 = min(p0 + cs, len);
-    const float scale2 = p.scale * 1.4426950408889634f;
     const uint64_t kt_base = (uint64_t)kvh * DH * p.t_max;
     const uint64_t v_base = (uint64_t)kvh * p.t_max * DH;
-    __syncthreads();
-
-    float m[kAttnRows], lp[kAttnRows], acc[kAttnRows][DPL];
+    // This wave's rows (wave + 4 i); q pre-scaled by scale * log2(e), lane
+    // = head dimension.
+    const float scale2 = p.scale * 1.4426950408889634f;
+    const bool rows = wave < p.group;
+    float qr[RPW][DPL], m[RPW], lp[RPW], acc[RPW][DPL];
 #pragma unroll
-    for (int r = 0; r < kAttnRows; ++r) {
-      m[r] = -FLT_MAX;
-      lp[r] = 0.0f;
+    for (int i = 0; i < RPW; ++i) {
+      const uint32_t r = wave + kAttnWaves * i;
+      m[i] = -FLT_MAX;
+      lp[i] = 0.0f;
 #pragma unroll
-      for (int c = 0; c < DPL; ++c)
-        acc[r][c] = 0.0f;
+      for (int c = 0; c < DPL; ++c) {
+        qr[i][c] = r < p.group ? p.q[((uint64_t)kvh * p.group + r) * DH + lane + 64 * c] * scale2 : 0.0f;
+        acc[i][c] = 0.0f;
+      }
     }
 
-    for (uint32_t blk = p0 + wave * 64; blk < p1; blk += kAttnWaves * 64) {
+    for (uint32_t blk = p0; blk < p1; blk += 64) {
       const uint32_t pos = blk + lane;
       const bool valid = pos < p1;
-      const uint64_t kcol = kt_base + (valid ? pos : blk);
-      // Scores of this lane's position for every row.
-      float s[kAttnRows];
+      // Stage the block: wave w loads K^T rows w * KPW .. (lane = position)
+      // and V rows w * VPW .. (lane = head dimension), all in one batch;
+      // positions past the chunk end are never read (zeros are staged).
+      // (Loads past the end re-read an in-range element, zeroed after the
+      // load, so no load is predicated.)
+      float kl[KPW], vl[VPW][DPL];
+      const uint32_t kpos = valid ? pos : blk;
 #pragma unroll
-      for (int r = 0; r < kAttnRows; ++r)
-        s[r] = 0.0f;
+      for (int u = 0; u < KPW; ++u)
+        kl[u] = load_kv<KV16>(p.kt, kt_base + (uint64_t)(wave * KPW + u) * p.t_max + kpos);
 #pragma unroll
-      for (int d0 = 0; d0 < DH; d0 += KU) {
-        float k[KU];
+      for (int u = 0; u < VPW; ++u) {
+        const uint32_t row = min(blk + wave * VPW + u, p1 - 1);
 #pragma unroll
-        for (int u = 0; u < KU; ++u)
-          k[u] = load_kv<KV16>(p.kt, kcol + (uint64_t)(d0 + u) * p.t_max);
+        for (int c = 0; c < DPL; ++c)
+          vl[u][c] = load_kv<KV16>(p.v, v_base + (uint64_t)row * DH + lane + 64 * c);
+      }
 #pragma unroll
-        for (int u = 0; u < KU; ++u) {
-          const f32x4 qa = sm.qT[d0 + u][0], qb = sm.qT[d0 + u][1];
+      for (int u = 0; u < KPW; ++u)
+        kl[u] = valid ? kl[u] : 0.0f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            s[r] = fmaf(qa[r], k[u], s[r]);
-            s[r + 4] = fmaf(qb[r], k[u], s[r + 4]);
-          }
-        }
+      for (int u = 0; u < VPW; ++u)
+#pragma unroll
+        for (int c = 0; c < DPL; ++c)
+          vl[u][c] = blk + wave * VPW + u < p1 ? vl[u][c] : 0.0f;
+      __syncthreads(); // the previous block's reads are done
+#pragma unroll
+      for (int u = 0; u < KPW; ++u)
+        sm.k[wave * KPW + u][lane] = kl[u];
+#pragma unroll
+      for (int u = 0; u < VPW; ++u)
+#pragma unroll
+        for (int c = 0; c < DPL; ++c)
+          sm.v[wave * VPW + u][lane + 64 * c] = vl[u][c];
+      __syncthreads();
+      if (!rows)
+        continue;
+      // Scores of this lane's position: q[r][d] from lane d % 64 of its
+      // register (v_readlane), K^T from LDS.
+      float s[RPW];
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+        s[i] = 0.0f;
+#pragma unroll
+      for (int d = 0; d < DH; ++d) {
+        const float k = sm.k[d][lane];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i)
+          s[i] = fmaf(bcast(qr[i][d / 64], d % 64), k, s[i]);
       }
       // Online softmax over the block: one running max per row (uniform
       // over the wave), per-lane partial sums rescaled with it.
-      float e[kAttnRows];
+      float e[RPW];
 #pragma unroll
-      for (int r = 0; r < kAttnRows; ++r) {
-        const float s2 = valid ? s[r] * scale2 : -INFINITY;
-        const float mn = fmaxf(m[r], wave_max(s2));
-        const float corr = exp2f(m[r] - mn);
-        e[r] = exp2f(s2 - mn);
-        lp[r] = fmaf(lp[r], corr, e[r]);
+      for (int i = 0; i < RPW; ++i) {
+        const float s2 = valid ? s[i] : -INFINITY;
+        const float mn = fmaxf(m[i], wave_max(s2));
+        const float corr = exp2f(m[i] - mn);
+        e[i] = exp2f(s2 - mn);
+        lp[i] = fmaf(lp[i], corr, e[i]);
 #pragma unroll
         for (int c = 0; c < DPL; ++c)
-          acc[r][c] *= corr;
-        m[r] = mn;
+          acc[i][c] *= corr;
+        m[i] = mn;
       }
-      sm.P[wave][lane][0] = f32x4{e[0], e[1], e[2], e[3]};
-      sm.P[wave][lane][1] = f32x4{e[4], e[5], e[6], e[7]};
-      wave_lds_sync();
-      // P @ V: lane = head dimension.
-      const uint32_t nv = min(64u, p1 - blk);
-      const uint64_t vrow = v_base + (uint64_t)blk * DH + lane;
-      for (uint32_t j = 0; j < nv; ++j) {
+      // P @ V: probability j sits in lane j (v_readlane), lane = head
+      // dimension for the accumulators.
+#pragma unroll
+      for (int j = 0; j < 64; ++j) {
         float vv[DPL];
 #pragma unroll
         for (int c = 0; c < DPL; ++c)
-          vv[c] = load_kv<KV16>(p.v, vrow + (uint64_t)j * DH + 64 * c);
-        const f32x4 pa = sm.P[wave][j][0], pb = sm.P[wave][j][1];
+          vv[c] = sm.v[j][lane + 64 * c];
 #pragma unroll
-        for (int c = 0; c < DPL; ++c)
+        for (int i = 0; i < RPW; ++i) {
+          const float pj = bcast(e[i], j);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            acc[r][c] = fmaf(pa[r], vv[c], acc[r][c]);
-            acc[r + 4][c] = fmaf(pb[r], vv[c], acc[r + 4][c]);
-          }
+          for (int c = 0; c < DPL; ++c)
+            acc[i][c] = fmaf(pj, vv[c], acc[i][c]);
+        }
       }
-      wave_lds_sync(); // P is rewritten by the next block
     }
 
-    // Merge the four waves' states (an idle wave holds the identity).
+    // Row state {acc, m, l} to scratch[kv_head][chunk][row].
 #pragma unroll
-    for (int r = 0; r < kAttnRows; ++r) {
-      const float l = wave_sum(lp[r]);
+    for (int i = 0; i < RPW; ++i) {
+      const uint32_t r = wave + kAttnWaves * i;
+      const float l = wave_sum(lp[i]);
+      if (r >= p.group)
+        continue;
+      float *dst = p.scratch + (((uint64_t)kvh * p.num_chunks + chunk) * p.group + r) * (DH + 2);
 #pragma unroll
       for (int c = 0; c < DPL; ++c)
-        sm.mrg[wave][r][lane + 64 * c] = acc[r][c];
+        dst[lane + 64 * c] = acc[i][c];
       if (lane == 0) {
-        sm.mrg[wave][r][DH] = m[r];
-        sm.mrg[wave][r][DH + 1] = l;
+        dst[DH] = m[i];
+        dst[DH + 1] = l;
       }
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < group * (DH + 2); i += kAttnThreads) {
-      const uint32_t r = i / (DH + 2), d = i % (DH + 2);
-      float ms = sm.mrg[0][r][DH];
-#pragma unroll
-      for (int w = 1; w < kAttnWaves; ++w)
-        ms = fmaxf(ms, sm.mrg[w][r][DH]);
-      float v;
-      if (d == DH) {
-        v = ms;
-      } else {
-        v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w)
-          v = fmaf(sm.mrg[w][r][d], exp2f(sm.mrg[w][r][DH] - ms), v);
-      }
-      p.scratch[(((uint64_t)kvh * p.num_chunks + chunk) * group + r) * (DH + 2) + d] = v;
     }
   }
 };
@@ -215,15 +230,29 @@ extern "C" __global__ __launch_bounds__(kArgmaxThreads) void ta_argmax_f32(Argma
   uint32_t bi = 0;
   // Ascending per thread: its quads, then its tail elements (all past the
   // quads), so ">=" keeps the thread's last maximum.
+  // Quads in batches of 8 per thread, all loads of a batch in flight
+  // together (a batch past the end re-reads quad 0 and skips it).
   const uint32_t nq = (reinterpret_cast<uintptr_t>(p.in) & 15u) == 0 ? p.n / 4 : 0;
-  for (uint32_t q = tid; q < nq; q += kArgmaxThreads) {
-    const f32x4 v = reinterpret_cast<const f32x4 *>(p.in)[q];
+  constexpr uint32_t QB = 8;
+  for (uint32_t q0 = tid; q0 < nq; q0 += QB * kArgmaxThreads) {
+    f32x4 v[QB];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      if (v[c] >= best) {
-        best = v[c];
-        bi = 4 * q + c;
+    for (uint32_t b = 0; b < QB; ++b) {
+      const uint32_t q = q0 + b * kArgmaxThreads;
+      v[b] = reinterpret_cast<const f32x4 *>(p.in)[q < nq ? q : 0u];
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < QB; ++b) {
+      const uint32_t q = q0 + b * kArgmaxThreads;
+      if (q < nq) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (v[b][c] >= best) {
+            best = v[b][c];
+            bi = 4 * q + c;
+          }
       }
+    }
   }
   for (uint32_t i = 4 * nq + tid; i < p.n; i += kArgmaxThreads) {
     const float v = p.in[i];
@@ -284,7 +313,8 @@ extern "C" __global__ __launch_bounds__(256) void ta_embed_gather(EmbedArgs p) {
 }
 
 #define TA_ATTN_DECODE(NAME, DH, KV16)                                                 \
-  extern "C" __global__ __launch_bounds__(kAttnThreads) void NAME(AttnDecodeArgs p) { \
+  extern "C" __global__ __launch_bounds__(kAttnThreads)                                \
+      __attribute__((amdgpu_waves_per_eu(1, 2))) void NAME(AttnDecodeArgs p) {       \
     AttnDecode<DH, KV16>::run(p);                                                      \
   }
 TA_ATTN_DECODE(ta_attn_decode_dh64, 64, false)
@@ -292,27 +322,32 @@ TA_ATTN_DECODE(ta_attn_decode_dh128, 128, false)
 TA_ATTN_DECODE(ta_attn_decode_kv16_dh64, 64, true)
 TA_ATTN_DECODE(ta_attn_decode_kv16_dh128, 128, true)
 
+// One wave per (kv head, row): lane i < num_chunks (<= 64) loads chunk i's
+// max and sum; the chunk weights go to LDS; the normaliser and each output
+// sum over the chunks in chunk order.
 extern "C" __global__ __launch_bounds__(64) void ta_attn_decode_combine(AttnCombineArgs p) {
-  const uint32_t row_id = blockIdx.x, tid = threadIdx.x;
+  __shared__ float wsh[64], lsh[64];
+  const uint32_t row_id = blockIdx.x, lane = threadIdx.x;
   const uint32_t kvh = row_id / p.group, r = row_id % p.group;
   const uint32_t stride = p.dh + 2;
   const uint64_t row0 = ((uint64_t)kvh * p.num_chunks * p.group + r) * stride;
   const uint64_t step = (uint64_t)p.group * stride;
-  float ms = -FLT_MAX;
-  for (uint32_t i = 0; i < p.num_chunks; ++i)
-    ms = fmaxf(ms, p.scratch[row0 + i * step + p.dh]);
+  const bool live = lane < p.num_chunks;
+  const float mi = live ? p.scratch[row0 + lane * step + p.dh] : -FLT_MAX;
+  const float li = live ? p.scratch[row0 + lane * step + p.dh + 1] : 0.0f;
+  const float ms = wave_max(mi);
+  wsh[lane] = exp2f(mi - ms);
+  lsh[lane] = li;
+  __syncthreads();
   float l = 0.0f;
-  for (uint32_t i = 0; i < p.num_chunks; ++i) {
-    const float *c = p.scratch + row0 + i * step;
-    l = fmaf(c[p.dh + 1], exp2f(c[p.dh] - ms), l);
-  }
+  for (uint32_t i = 0; i < p.num_chunks; ++i)
+    l = fmaf(lsh[i], wsh[i], l);
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  for (uint32_t d = tid; d < p.dh; d += 64) {
+  for (uint32_t d = lane; d < p.dh; d += 64) {
     float num = 0.0f;
-    for (uint32_t i = 0; i < p.num_chunks; ++i) {
-      const float *c = p.scratch + row0 + i * step;
-      num = fmaf(c[d], exp2f(c[p.dh] - ms), num);
-    }
+#pragma unroll 8
+    for (uint32_t i = 0; i < p.num_chunks; ++i)
+      num = fmaf(p.scratch[row0 + i * step + d], wsh[i], num);
     p.out[(uint64_t)row_id * p.dh + d] = num * inv;
   }
 }
