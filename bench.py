@@ -145,7 +145,9 @@ def batched_gelu(ta, ex, iters=10):
     bias = ex.tensor_from(rng.uniform(-1, 1, (bt, n)).astype(np.float32))
     c = ex.tensor([bt, m, n])
     op = ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_GELU))
-    for _ in range(3):
+    # ~25 ms of MFMA load first: the section follows memory-bound ones, and
+    # the clock needs that long to settle.
+    for _ in range(25):
         ex.run_ops([op])
     ns = median_ns([ex.run_ops([op]) for _ in range(iters)])
     flops = 2.0 * bt * m * n * k
