@@ -302,6 +302,47 @@ int ta_flash_attention(const ta_executor *exec, const ta_tensor *q,
                        const ta_tensor *out, const ta_flash_desc *desc,
                        ta_run_stats *stats);
 
+/* Fused RoPE + strided scatter, Executor::run_rope_scatter
+ * (src/executor/elementwise/ops.rs:243-316; RopeScatterDesc,
+ * src/executor/elementwise/mod.rs:144-159; Rust API only in the
+ * reference): ta_rope's rotation of f32 input [T, heads, head_dim], every
+ * element (t, h, d) written to dst[dst_offset + t*dst_strides[0] +
+ * h*dst_strides[1] + d*dst_strides[2]] (dst f32, or f16 with RNE; not the
+ * input).  pos_scale applies when a graph op carries a position cell. */
+typedef struct ta_rope_scatter_desc {
+  uint32_t dst_offset;
+  uint32_t dst_strides[3];
+  uint32_t pos_scale;
+  uint32_t reserved; /* must be zero */
+} ta_rope_scatter_desc;
+int ta_rope_scatter(const ta_executor *exec, const ta_tensor *input, const ta_tensor *table,
+                    const ta_tensor *dst, const ta_rope_desc *desc,
+                    const ta_rope_scatter_desc *scatter, ta_run_stats *stats);
+
+/* Binary combine, Executor::run_binary (ops.rs:318-380; BinaryOp,
+ * elementwise/mod.rs:242-252; Rust API only in the reference): over
+ * equal-length a, b, out (all f32 or all f16; out may alias a or b),
+ * TA_BINARY_OP_ADD_SCALED: out = a + beta * b; TA_BINARY_OP_SILU_MUL: out =
+ * silu(a) * b (beta ignored). */
+enum { TA_BINARY_OP_ADD_SCALED = 0, TA_BINARY_OP_SILU_MUL = 1 };
+int ta_binary(const ta_executor *exec, const ta_tensor *a, const ta_tensor *b,
+              const ta_tensor *out, uint32_t op, float beta, ta_run_stats *stats);
+
+/* Prefill QKV pack, Executor::run_prefill_qkv_pack
+ * (src/executor/elementwise/flash.rs:255-402; PrefillQkvPackDesc,
+ * elementwise/mod.rs:186-199; Rust API only in the reference): from f16 qkv
+ * [T, H*dh + 2*H_kv*dh], RoPE Q into head-major f16 q [H, T, dh], RoPE K
+ * into the f16 Kt cache [H_kv, dh, T_max] and copy V into the f16 V cache
+ * [H_kv, T_max, dh], both at positions pos_base .. pos_base + T - 1; table
+ * f32 [T_max, rot_dim/2, 2]; dh a multiple of 4. */
+typedef struct ta_prefill_qkv_pack_desc {
+  uint32_t heads, kv_heads, head_dim, rot_dim, pos_base;
+  uint32_t reserved; /* must be zero */
+} ta_prefill_qkv_pack_desc;
+int ta_prefill_qkv_pack(const ta_executor *exec, const ta_tensor *qkv, const ta_tensor *table,
+                        const ta_tensor *q, const ta_tensor *kt, const ta_tensor *v,
+                        const ta_prefill_qkv_pack_desc *desc, ta_run_stats *stats);
+
 /* Host-visible u32 cells (src/executor/cells.rs:10-205; Rust API only in
  * the reference): pinned, mapped host memory that kernels read and write
  * through ta_u32_cell_device_address and the host through
@@ -368,6 +409,11 @@ int ta_attn_decode(const ta_executor *exec, const ta_tensor *q, const ta_tensor 
  *   ARGMAX          in[0] input; cell result
  *   EMBED_GATHER    cell token ids, in[0] table, out
  *   ATTN_DECODE     in[0] q, in[1] kt, in[2] v, aux scratch, out; attn
+ *   ROPE_SCATTER    in[0] input, in[1] table, out dst; rope, scatter
+ *                   (pos_addr as for ROPE, advancing dst by
+ *                   scatter.pos_scale per position)
+ *   BINARY          in[0] a, in[1] b, out; binary_op, scalar = beta
+ *   PREFILL_QKV_PACK in[0] qkv, in[1] table, out q, aux kt, aux2 v; qkv
  * pos_addr (ROPE, COPY_STRIDED): device address of a u32 position cell
  * read when the op runs (added to rope.pos_base; times pos_scale added to
  * copy.dst_offset), so a prepared graph replays at a new position after
@@ -383,6 +429,9 @@ enum {
   TA_EXEC_ARGMAX = 7,
   TA_EXEC_EMBED_GATHER = 8,
   TA_EXEC_ATTN_DECODE = 9,
+  TA_EXEC_ROPE_SCATTER = 10,
+  TA_EXEC_BINARY = 11,
+  TA_EXEC_PREFILL_QKV_PACK = 12,
 };
 typedef struct ta_exec_op {
   uint32_t kind; /* TA_EXEC_* */
@@ -401,6 +450,10 @@ typedef struct ta_exec_op {
   const ta_u32_cell *cell;
   const ta_tensor *aux;
   ta_attn_decode_desc attn;
+  const ta_tensor *aux2;
+  ta_rope_scatter_desc scatter;
+  uint32_t binary_op; /* TA_BINARY_OP_* */
+  ta_prefill_qkv_pack_desc qkv;
 } ta_exec_op;
 int ta_run_exec_ops(const ta_executor *exec, const ta_exec_op *ops,
                     size_t n_ops, ta_run_stats *stats);

@@ -366,3 +366,49 @@ def attn_decode(q, kt, v, kv_heads: int, group: int, t_max: int, dh: int, kv_len
         p = np.exp(s)
         out[h] = (p / p.sum(axis=1, keepdims=True)) @ v64[h]
     return out.astype(np.float32).reshape(-1)
+
+
+def binary_combine(a, b, mode: int, beta: float = 0.0) -> np.ndarray:
+    """Binary combine of shaders/op_binary_body.glsl in f64: mode 0 a + beta * b
+    (residual add), mode 1 silu(a) * b = a / (1 + exp(-a)) * b (SwiGLU gating)."""
+    a64 = np.asarray(a, np.float32).astype(np.float64)
+    b64 = np.asarray(b, np.float32).astype(np.float64)
+    if mode == 0:
+        return (a64 + float(np.float32(beta)) * b64).astype(np.float32)
+    return (a64 / (1.0 + np.exp(-a64)) * b64).astype(np.float32)
+
+
+def rope_scatter(x, table, tokens: int, heads: int, head_dim: int, rot_dim: int, pos_base: int,
+                 dst, dst_offset: int, dst_strides, dst_f16: bool = False) -> np.ndarray:
+    """Fused RoPE + scatter of src/executor/elementwise/ops.rs:243-316: the rotation
+    of rope_tokens, element (t, h, d) stored at dst_offset + t*s0 + h*s1 + d*s2 of
+    a copy of dst (f16 destinations hold the RNE-rounded value)."""
+    y = rope_tokens(x, table, tokens, heads, head_dim, rot_dim, pos_base).reshape(tokens, heads, head_dim)
+    out = np.asarray(dst, np.float32).reshape(-1).copy()
+    t, h, d = np.meshgrid(np.arange(tokens), np.arange(heads), np.arange(head_dim), indexing="ij")
+    idx = dst_offset + t * dst_strides[0] + h * dst_strides[1] + d * dst_strides[2]
+    out[idx.reshape(-1)] = round_via_f16(y.reshape(-1)) if dst_f16 else y.reshape(-1)
+    return out
+
+
+def prefill_qkv_pack(qkv, table, tokens: int, heads: int, kv_heads: int, head_dim: int, rot_dim: int,
+                     pos_base: int, kt, v):
+    """Prefill QKV pack of src/executor/elementwise/flash.rs:255-402 on f16 data
+    (inputs hold f16 values): Q of each token (rope_tokens rotation, rounded to
+    f16) in head-major [H, T, dh]; K rotated and rounded into kt [H_kv, dh, T_max]
+    at column pos_base + t; V copied into v [H_kv, T_max, dh] at row pos_base + t.
+    Returns (q, kt, v) as new arrays."""
+    x = np.asarray(qkv, np.float32).reshape(tokens, -1)
+    embd, kv_dim = heads * head_dim, kv_heads * head_dim
+    q = rope_tokens(np.ascontiguousarray(x[:, :embd]).reshape(-1), table, tokens, heads, head_dim, rot_dim,
+                    pos_base)
+    q = round_via_f16(q).reshape(tokens, heads, head_dim).transpose(1, 0, 2).copy()
+    k = rope_tokens(np.ascontiguousarray(x[:, embd:embd + kv_dim]).reshape(-1), table, tokens, kv_heads,
+                    head_dim, rot_dim, pos_base)
+    k = round_via_f16(k).reshape(tokens, kv_heads, head_dim)
+    kt_out = np.asarray(kt, np.float32).copy()
+    v_out = np.asarray(v, np.float32).copy()
+    for t in range(tokens):
+        kt_out[:, :, pos_base + t] = k[t]
+        v_out[:, pos_base + t, :] = x[t, embd + kv_dim:].reshape(kv_heads, head_dim)
+    return q, kt_out, v_out

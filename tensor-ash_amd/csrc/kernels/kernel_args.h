@@ -175,6 +175,49 @@ typedef struct RopeArgs {
   uint64_t table_len; // elements; pairs whose angle lies past it are skipped
 } RopeArgs;
 
+// Fused RoPE + strided scatter: the rotation of RopeArgs (f32 input),
+// every element (token, head, dim) of the rotated [tokens, heads, head_dim]
+// vectors written to dst[dst_offset + *pos_addr * pos_scale + token * ds0 +
+// head * ds1 + dim * ds2] (f32, or f16 with RNE); destinations past
+// dst_len are skipped.
+typedef struct RopeScatterArgs {
+  RopeArgs rope; // in, table, pos_addr, geometry (out and io_f16 unused)
+  void *dst;
+  uint32_t dst_offset;
+  uint32_t dst_strides[3];
+  uint32_t pos_scale;
+  uint32_t dst_f16;
+  uint64_t dst_len;
+} RopeScatterArgs;
+
+// Elementwise combine over n elements: mode 0 out = a + beta * b, mode 1
+// out = silu(a) * b; a, b, out all f32 or all f16 (f32 math, RNE store).
+typedef struct BinaryArgs {
+  const void *a;
+  const void *b;
+  void *out;
+  uint64_t n;
+  uint32_t mode;
+  float beta;
+  uint32_t io_f16;
+  uint32_t pad;
+} BinaryArgs;
+
+// Prefill QKV pack (f16): from qkv [tokens, qkv_stride] = [Q (heads*dh) |
+// K (kv_heads*dh) | V (kv_heads*dh)] per token, RoPE Q into head-major
+// q [heads, tokens, dh], RoPE K into kt [kv_heads, dh, t_max] at column
+// pos_base + token, copy V into v [kv_heads, t_max, dh] at row pos_base +
+// token.  Lanes past rot_dim pass through.
+typedef struct QkvPackArgs {
+  const uint16_t *qkv; // f16 bits throughout
+  uint16_t *q;
+  uint16_t *kt;
+  uint16_t *v;
+  const float *table;
+  uint32_t tokens, heads, kv_heads, head_dim, rot_dim, pos_base;
+  uint32_t qkv_stride, t_max, k_offset, v_offset;
+} QkvPackArgs;
+
 // Strided 3-D copy: for (x, y, z) < extent, dst[dst_offset + *pos_addr *
 // pos_scale + x*ds0 + y*ds1 + z*ds2] = src[src_offset + x*ss0 + y*ss1 +
 // z*ss2]; f16 sides widen exactly / narrow with RNE.

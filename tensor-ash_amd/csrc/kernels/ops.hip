@@ -1,6 +1,8 @@
 // Model ops around the GEMM path for gfx950: row softmax, RMSNorm /
-// LayerNorm, RoPE and strided copy (the reference's ta_softmax_rows,
-// ta_rms_norm, ta_layer_norm, ta_rope, ta_copy_strided;
+// LayerNorm, RoPE (plain, scattered into a cache, and the prefill QKV
+// pack), strided copy and the binary combine (the reference's
+// ta_softmax_rows, ta_rms_norm, ta_layer_norm, ta_rope, ta_copy_strided,
+// run_rope_scatter, run_prefill_qkv_pack, run_binary;
 // src/executor/elementwise/ops.rs with shaders/op_softmax_f32_row.comp,
 // op_rmsnorm_body.glsl, op_rope_body.glsl, op_copy_strided_body.glsl).
 // All are HBM-bound streaming kernels:
@@ -153,16 +155,18 @@ extern "C" __global__ __launch_bounds__(kOpThreads) void ta_norm_rows(NormArgs p
 // r1 = fma(x0, s, x1 c); lanes past rot_dim are copied by the pairs of
 // their head vector.  A device position past the table skips the pair.  Each element is read and written by one thread, so
 // in-place is safe.
-extern "C" __global__ __launch_bounds__(kOpThreads) void ta_rope(RopeArgs p) {
+// One thread per rotated pair of a [tokens, heads, head_dim] input:
+// put(token, head, dim, value) receives the pair's two rotated values (the
+// reference's fma order) and the pass-through lanes the pair owns.
+template <class Put> TA_DEVICE void rope_pairs(const RopeArgs &p, bool f16, Put &&put) {
   const uint32_t half = p.rot_dim / 2;
   const uint64_t pairs = (uint64_t)p.tokens * p.heads * half;
-  const bool f16 = p.io_f16 != 0;
   const uint32_t pos0 = p.pos_base + (p.pos_addr ? *p.pos_addr : 0u);
   for (uint64_t id = (uint64_t)blockIdx.x * kOpThreads + threadIdx.x; id < pairs;
        id += (uint64_t)gridDim.x * kOpThreads) {
     const uint32_t pair = (uint32_t)(id % half);
     const uint64_t vecid = id / half; // token * heads + head
-    const uint32_t token = (uint32_t)(vecid / p.heads);
+    const uint32_t token = (uint32_t)(vecid / p.heads), head = (uint32_t)(vecid % p.heads);
     const uint64_t vbase = vecid * p.head_dim;
     const uint64_t i0 = vbase + 2 * pair;
     const float x0 = load_io(p.in, i0, f16), x1 = load_io(p.in, i0 + 1, f16);
@@ -170,11 +174,104 @@ extern "C" __global__ __launch_bounds__(kOpThreads) void ta_rope(RopeArgs p) {
     if (angle + 1 >= p.table_len)
       continue;
     const float c = p.table[angle], s = p.table[angle + 1];
-    store_io(p.out, i0, fmaf(x0, c, -x1 * s), f16);
-    store_io(p.out, i0 + 1, fmaf(x0, s, x1 * c), f16);
-    for (uint32_t lane = pair; lane < p.head_dim - p.rot_dim; lane += half) {
-      const uint64_t idx = vbase + p.rot_dim + lane;
-      store_io(p.out, idx, load_io(p.in, idx, f16), f16);
+    put(token, head, 2 * pair, fmaf(x0, c, -x1 * s));
+    put(token, head, 2 * pair + 1, fmaf(x0, s, x1 * c));
+    for (uint32_t lane = pair; lane < p.head_dim - p.rot_dim; lane += half)
+      put(token, head, p.rot_dim + lane, load_io(p.in, vbase + p.rot_dim + lane, f16));
+  }
+}
+
+extern "C" __global__ __launch_bounds__(kOpThreads) void ta_rope(RopeArgs p) {
+  const bool f16 = p.io_f16 != 0;
+  rope_pairs(p, f16, [&](uint32_t token, uint32_t head, uint32_t dim, float v) {
+    store_io(p.out, ((uint64_t)token * p.heads + head) * p.head_dim + dim, v, f16);
+  });
+}
+
+// src/executor/elementwise/ops.rs:243-316 (run_rope_scatter): the RoPE
+// above with each element stored at its strided cache location.
+extern "C" __global__ __launch_bounds__(kOpThreads) void ta_rope_scatter(RopeScatterArgs p) {
+  const uint64_t base =
+      p.dst_offset + (uint64_t)(p.rope.pos_addr ? *p.rope.pos_addr : 0u) * p.pos_scale;
+  rope_pairs(p.rope, false, [&](uint32_t token, uint32_t head, uint32_t dim, float v) {
+    const uint64_t d = base + (uint64_t)token * p.dst_strides[0] +
+                       (uint64_t)head * p.dst_strides[1] + (uint64_t)dim * p.dst_strides[2];
+    if (d < p.dst_len)
+      store_io(p.dst, d, v, p.dst_f16 != 0);
+  });
+}
+
+// src/executor/elementwise/ops.rs:318-380 (run_binary): four elements per
+// thread, grid-strided; SiLU with the library exp and an IEEE divide.
+extern "C" __global__ __launch_bounds__(kOpThreads) void ta_binary(BinaryArgs p) {
+  const bool f16 = p.io_f16 != 0;
+  for (uint64_t i = ((uint64_t)blockIdx.x * kOpThreads + threadIdx.x) * 4; i < p.n;
+       i += (uint64_t)gridDim.x * kOpThreads * 4) {
+#pragma unroll
+    for (uint32_t c = 0; c < 4; ++c) {
+      if (i + c >= p.n)
+        break;
+      const float a = load_io(p.a, i + c, f16), b = load_io(p.b, i + c, f16);
+      const float v = p.mode == 0 ? fmaf(p.beta, b, a) : (a / (1.0f + expf(-a))) * b;
+      store_io(p.out, i + c, v, f16);
+    }
+  }
+}
+
+// src/executor/elementwise/flash.rs:255-402 (run_prefill_qkv_pack): the
+// work is Q pairs, then K pairs, then V quads, one item per thread
+// (grid-strided); rotations as ta_rope (f32 math, RNE store).
+extern "C" __global__ __launch_bounds__(kOpThreads) void ta_prefill_qkv_pack(QkvPackArgs args) {
+  struct {
+    const _Float16 *qkv;
+    _Float16 *q, *kt, *v;
+  } h{reinterpret_cast<const _Float16 *>(args.qkv), reinterpret_cast<_Float16 *>(args.q),
+      reinterpret_cast<_Float16 *>(args.kt), reinterpret_cast<_Float16 *>(args.v)};
+  const QkvPackArgs &p = args;
+  const uint32_t half = p.rot_dim / 2, tail = p.head_dim - p.rot_dim;
+  const uint64_t q_pairs = (uint64_t)p.tokens * p.heads * half;
+  const uint64_t k_pairs = (uint64_t)p.tokens * p.kv_heads * half;
+  const uint64_t v_quads = (uint64_t)p.tokens * p.kv_heads * (p.head_dim / 4);
+  const uint64_t total = q_pairs + k_pairs + v_quads;
+  for (uint64_t id = (uint64_t)blockIdx.x * kOpThreads + threadIdx.x; id < total;
+       id += (uint64_t)gridDim.x * kOpThreads) {
+    if (id < q_pairs + k_pairs) {
+      const bool is_q = id < q_pairs;
+      const uint64_t kid = is_q ? id : id - q_pairs;
+      const uint32_t nh = is_q ? p.heads : p.kv_heads;
+      const uint32_t pair = (uint32_t)(kid % half);
+      const uint32_t head = (uint32_t)((kid / half) % nh);
+      const uint32_t token = (uint32_t)(kid / ((uint64_t)half * nh));
+      const uint64_t src = (uint64_t)token * p.qkv_stride + (is_q ? 0u : p.k_offset) +
+                           (uint64_t)head * p.head_dim;
+      const float x0 = (float)h.qkv[src + 2 * pair], x1 = (float)h.qkv[src + 2 * pair + 1];
+      const uint64_t angle = ((uint64_t)(p.pos_base + token) * half + pair) * 2;
+      const float c = p.table[angle], s = p.table[angle + 1];
+      const _Float16 y0 = (_Float16)fmaf(x0, c, -x1 * s), y1 = (_Float16)fmaf(x0, s, x1 * c);
+      const uint32_t pos = p.pos_base + token;
+      if (is_q) {
+        const uint64_t dst = ((uint64_t)head * p.tokens + token) * p.head_dim;
+        h.q[dst + 2 * pair] = y0;
+        h.q[dst + 2 * pair + 1] = y1;
+        for (uint32_t lane = pair; lane < tail; lane += half)
+          h.q[dst + p.rot_dim + lane] = h.qkv[src + p.rot_dim + lane];
+      } else {
+        const uint64_t col = (uint64_t)head * p.head_dim;
+        h.kt[(col + 2 * pair) * p.t_max + pos] = y0;
+        h.kt[(col + 2 * pair + 1) * p.t_max + pos] = y1;
+        for (uint32_t lane = pair; lane < tail; lane += half)
+          h.kt[(col + p.rot_dim + lane) * p.t_max + pos] = h.qkv[src + p.rot_dim + lane];
+      }
+    } else {
+      const uint64_t vid = id - q_pairs - k_pairs;
+      const uint32_t n4 = p.head_dim / 4;
+      const uint32_t d4 = (uint32_t)(vid % n4);
+      const uint32_t head = (uint32_t)((vid / n4) % p.kv_heads);
+      const uint32_t token = (uint32_t)(vid / ((uint64_t)n4 * p.kv_heads));
+      const uint64_t src = (uint64_t)token * p.qkv_stride + p.v_offset + (uint64_t)head * p.head_dim;
+      const uint64_t dst = ((uint64_t)head * p.t_max + p.pos_base + token) * p.head_dim;
+      *reinterpret_cast<f16x4 *>(h.v + dst + 4 * d4) =
+          *reinterpret_cast<const f16x4 *>(h.qkv + src + 4 * d4);
     }
   }
 }

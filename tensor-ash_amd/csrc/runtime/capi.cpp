@@ -477,6 +477,37 @@ const U32Cell *checked_cell(const ta_executor &e, const ta_u32_cell *c, const st
   return c->cell.get();
 }
 
+RopeScatterDesc scatter_desc(const ta_rope_scatter_desc &d, const std::string &fn) {
+  if (d.reserved != 0)
+    fail(fn + ": ta_rope_scatter_desc.reserved must be zero");
+  RopeScatterDesc r;
+  r.dst_offset = d.dst_offset;
+  for (int i = 0; i < 3; ++i)
+    r.dst_strides[i] = d.dst_strides[i];
+  r.pos_scale = d.pos_scale;
+  return r;
+}
+
+BinaryOp binary_op(uint32_t op, float beta, const std::string &fn) {
+  if (op == TA_BINARY_OP_ADD_SCALED)
+    return BinaryOp::add_scaled(beta);
+  if (op == TA_BINARY_OP_SILU_MUL)
+    return BinaryOp::silu_mul();
+  fail(fn + ": binary op " + std::to_string(op) + " is invalid");
+}
+
+PrefillQkvPackDesc qkv_pack_desc(const ta_prefill_qkv_pack_desc &d, const std::string &fn) {
+  if (d.reserved != 0)
+    fail(fn + ": ta_prefill_qkv_pack_desc.reserved must be zero");
+  PrefillQkvPackDesc r;
+  r.heads = d.heads;
+  r.kv_heads = d.kv_heads;
+  r.head_dim = d.head_dim;
+  r.rot_dim = d.rot_dim;
+  r.pos_base = d.pos_base;
+  return r;
+}
+
 AttnDecodeDesc attn_decode_desc(const ta_attn_decode_desc &d) {
   AttnDecodeDesc a;
   a.kv_len = d.kv_len;
@@ -539,6 +570,22 @@ std::vector<ExecOp> checked_exec_ops(const ta_executor &e, const ta_exec_op *ops
     case TA_EXEC_EMBED_GATHER:
       out.push_back(ExecOp::embed_gather(*checked_cell(e, o.cell, where, "cell"),
                                          t(o.in[0], "table"), t(o.out, "out")));
+      break;
+    case TA_EXEC_ROPE_SCATTER: {
+      RopeDesc rd = rope_desc(o.rope);
+      rd.pos_addr = o.pos_addr;
+      out.push_back(ExecOp::rope_scatter(t(o.in[0], "input"), t(o.in[1], "table"), t(o.out, "dst"),
+                                         rd, scatter_desc(o.scatter, where)));
+      break;
+    }
+    case TA_EXEC_BINARY:
+      out.push_back(ExecOp::binary_op(t(o.in[0], "a"), t(o.in[1], "b"), t(o.out, "out"),
+                                      binary_op(o.binary_op, o.scalar, where)));
+      break;
+    case TA_EXEC_PREFILL_QKV_PACK:
+      out.push_back(ExecOp::prefill_qkv_pack(t(o.in[0], "qkv"), t(o.in[1], "table"), t(o.out, "q"),
+                                             t(o.aux, "kt"), t(o.aux2, "v"),
+                                             qkv_pack_desc(o.qkv, where)));
       break;
     case TA_EXEC_ATTN_DECODE:
       out.push_back(ExecOp::attn_decode(t(o.in[0], "q"), t(o.in[1], "kt"), t(o.in[2], "v"),
@@ -670,6 +717,48 @@ uint64_t ta_u32_cell_device_address(const ta_u32_cell *cell) {
   return cell ? cell->cell->device_address() : 0;
 }
 uint32_t ta_u32_cell_cap(const ta_u32_cell *cell) { return cell ? cell->cell->cap() : 0; }
+
+// src/executor/elementwise/ops.rs:243-380 and flash.rs:255-402.
+int ta_rope_scatter(const ta_executor *exec, const ta_tensor *input, const ta_tensor *table,
+                    const ta_tensor *dst, const ta_rope_desc *desc,
+                    const ta_rope_scatter_desc *scatter, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const char *fn = "ta_rope_scatter";
+    const ta_executor &e = checked_ref(exec, "ta_rope_scatter: exec is null");
+    const Tensor *ti = checked_tensor(e, input, fn, "input");
+    const Tensor *tt = checked_tensor(e, table, fn, "table");
+    const Tensor *td = checked_tensor(e, dst, fn, "dst");
+    const ta_rope_desc &d = checked_ref(desc, "ta_rope_scatter: desc is null");
+    const ta_rope_scatter_desc &sd = checked_ref(scatter, "ta_rope_scatter: scatter is null");
+    write_stats(stats, e.exec->run_rope_scatter(*ti, *tt, *td, rope_desc(d), scatter_desc(sd, fn)));
+  });
+}
+int ta_binary(const ta_executor *exec, const ta_tensor *a, const ta_tensor *b,
+              const ta_tensor *out, uint32_t op, float beta, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const char *fn = "ta_binary";
+    const ta_executor &e = checked_ref(exec, "ta_binary: exec is null");
+    const Tensor *ta_ = checked_tensor(e, a, fn, "a");
+    const Tensor *tb = checked_tensor(e, b, fn, "b");
+    const Tensor *to = checked_tensor(e, out, fn, "out");
+    write_stats(stats, e.exec->run_binary(*ta_, *tb, *to, binary_op(op, beta, fn)));
+  });
+}
+int ta_prefill_qkv_pack(const ta_executor *exec, const ta_tensor *qkv, const ta_tensor *table,
+                        const ta_tensor *q, const ta_tensor *kt, const ta_tensor *v,
+                        const ta_prefill_qkv_pack_desc *desc, ta_run_stats *stats) {
+  return ffi_status([&] {
+    const char *fn = "ta_prefill_qkv_pack";
+    const ta_executor &e = checked_ref(exec, "ta_prefill_qkv_pack: exec is null");
+    const Tensor *tx = checked_tensor(e, qkv, fn, "qkv");
+    const Tensor *tt = checked_tensor(e, table, fn, "table");
+    const Tensor *tq = checked_tensor(e, q, fn, "q");
+    const Tensor *tk = checked_tensor(e, kt, fn, "kt");
+    const Tensor *tv = checked_tensor(e, v, fn, "v");
+    const ta_prefill_qkv_pack_desc &d = checked_ref(desc, "ta_prefill_qkv_pack: desc is null");
+    write_stats(stats, e.exec->run_prefill_qkv_pack(*tx, *tt, *tq, *tk, *tv, qkv_pack_desc(d, fn)));
+  });
+}
 
 // src/executor/elementwise/ops.rs:456-595 and attn.rs:14-185.
 int ta_argmax(const ta_executor *exec, const ta_tensor *input, ta_u32_cell *result,

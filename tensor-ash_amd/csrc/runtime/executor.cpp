@@ -1398,16 +1398,10 @@ ElemLaunch plan_norm(ExecutorImpl &e, const std::string &op, const Tensor &input
   return elem("ta_norm_rows", grid_for(rows, 1, e.ctx->cu_count()), a);
 }
 
-ElemLaunch plan_rope(ExecutorImpl &e, const Tensor &input, const Tensor &table,
-                     const Tensor &output, const RopeDesc &desc) {
-  const std::string op = "run_rope";
-  e.validate_tensor(&input, "input");
-  e.validate_tensor(&output, "output");
-  e.validate_tensor(&table, "table");
-  const bool f16 = io_f16(op, input, output);
-  ensure_f32(table, op, "table");
-  ensure_same_shape(op, input, output);
-  // ops.rs:177-207 (rope_tokens).
+// ops.rs:177-207 (rope_tokens): the token count of `input` under desc,
+// with rot_dim and table coverage checked.
+uint64_t rope_tokens(const std::string &op, const Tensor &input, const Tensor &table,
+                     const RopeDesc &desc) {
   if (desc.rot_dim < 2 || desc.rot_dim % 2 != 0 || desc.rot_dim > desc.head_dim)
     fail(op + ": rot_dim " + std::to_string(desc.rot_dim) +
          " must be even, >= 2, and <= head_dim " + std::to_string(desc.head_dim));
@@ -1423,6 +1417,19 @@ ElemLaunch plan_rope(ExecutorImpl &e, const Tensor &input, const Tensor &table,
     fail(op + ": table length " + std::to_string(table.len()) + " < required " +
          std::to_string(needed) + " (pos_base " + std::to_string(desc.pos_base) + " + " +
          std::to_string(tokens) + " tokens, rot_dim " + std::to_string(desc.rot_dim) + ")");
+  return tokens;
+}
+
+ElemLaunch plan_rope(ExecutorImpl &e, const Tensor &input, const Tensor &table,
+                     const Tensor &output, const RopeDesc &desc) {
+  const std::string op = "run_rope";
+  e.validate_tensor(&input, "input");
+  e.validate_tensor(&output, "output");
+  e.validate_tensor(&table, "table");
+  const bool f16 = io_f16(op, input, output);
+  ensure_f32(table, op, "table");
+  ensure_same_shape(op, input, output);
+  const uint64_t tokens = rope_tokens(op, input, table, desc);
   RopeArgs a{};
   a.in = input.device_ptr();
   a.out = output.device_ptr();
@@ -1658,6 +1665,148 @@ ElemLaunch plan_embed_gather(ExecutorImpl &e, const U32Cell &tokens, const Tenso
   return l;
 }
 
+// ops.rs:243-316 (plan_rope_scatter): f32 input, dst f32 or f16 and not
+// the input, every destination element inside dst.
+ElemLaunch plan_rope_scatter(ExecutorImpl &e, const Tensor &input, const Tensor &table,
+                             const Tensor &dst, const RopeDesc &desc,
+                             const RopeScatterDesc &scatter) {
+  const std::string op = "run_rope_scatter";
+  e.validate_tensor(&input, "input");
+  ensure_f32(input, op, "input");
+  e.validate_tensor(&table, "table");
+  ensure_f32(table, op, "table");
+  e.validate_tensor(&dst, "dst");
+  if (input.buffer_id() == dst.buffer_id())
+    fail(op + ": input and dst must be different tensors");
+  const uint64_t tokens = rope_tokens(op, input, table, desc);
+  const uint64_t max_index = scatter.dst_offset + (tokens - 1) * scatter.dst_strides[0] +
+                             (uint64_t)(desc.heads - 1) * scatter.dst_strides[1] +
+                             (uint64_t)(desc.head_dim - 1) * scatter.dst_strides[2];
+  if (max_index >= dst.len())
+    fail(op + ": destination access reaches element " + std::to_string(max_index) +
+         " but dst has " + std::to_string(dst.len()));
+  RopeScatterArgs a{};
+  a.rope.in = input.device_ptr();
+  a.rope.table = static_cast<const float *>(table.device_ptr());
+  a.rope.pos_addr = reinterpret_cast<const uint32_t *>(desc.pos_addr);
+  a.rope.tokens = (uint32_t)tokens;
+  a.rope.heads = desc.heads;
+  a.rope.head_dim = desc.head_dim;
+  a.rope.rot_dim = desc.rot_dim;
+  a.rope.pos_base = desc.pos_base;
+  a.rope.table_len = table.len();
+  a.dst = dst.device_ptr();
+  a.dst_offset = scatter.dst_offset;
+  for (int i = 0; i < 3; ++i)
+    a.dst_strides[i] = scatter.dst_strides[i];
+  a.pos_scale = scatter.pos_scale;
+  a.dst_f16 = dst.dtype() == DType::F16;
+  a.dst_len = dst.len();
+  const uint64_t pairs = tokens * desc.heads * (desc.rot_dim / 2);
+  return elem("ta_rope_scatter", grid_for(pairs, 256, e.ctx->cu_count()), a);
+}
+
+// ops.rs:318-380 (plan_binary): a, b and out share a storage type and an
+// element count; out may alias either input.
+ElemLaunch plan_binary(ExecutorImpl &e, const Tensor &a, const Tensor &b, const Tensor &out,
+                       BinaryOp bop) {
+  const std::string op = "run_binary";
+  e.validate_tensor(&a, "a");
+  e.validate_tensor(&out, "out");
+  const bool f16 = io_f16(op, a, out);
+  e.validate_tensor(&b, "b");
+  if (b.dtype() != a.dtype())
+    fail(op + ": b (" + dtype_name(b.dtype()) + ") must match a (" + dtype_name(a.dtype()) +
+         ") storage");
+  if (a.len() != b.len() || a.len() != out.len())
+    fail(op + ": element counts differ (a " + std::to_string(a.len()) + ", b " +
+         std::to_string(b.len()) + ", out " + std::to_string(out.len()) + ")");
+  if (a.len() > UINT32_MAX)
+    fail(op + ": too large");
+  BinaryArgs ba{};
+  ba.a = a.device_ptr();
+  ba.b = b.device_ptr();
+  ba.out = out.device_ptr();
+  ba.n = a.len();
+  ba.mode = (uint32_t)bop.kind;
+  ba.beta = bop.kind == BinaryOp::Kind::AddScaled ? bop.beta : 0.0f;
+  ba.io_f16 = f16 ? 1u : 0u;
+  return elem("ta_binary", grid_for((a.len() + 3) / 4, 256, e.ctx->cu_count()), ba);
+}
+
+// flash.rs:272-402 (plan_prefill_qkv_pack): the same checks in the same
+// order.
+ElemLaunch plan_prefill_qkv_pack(ExecutorImpl &e, const Tensor &qkv, const Tensor &table,
+                                 const Tensor &q, const Tensor &kt, const Tensor &v,
+                                 const PrefillQkvPackDesc &d) {
+  const std::string op = "run_prefill_qkv_pack";
+  for (auto [t, name] : {std::pair<const Tensor *, const char *>{&qkv, "qkv"},
+                         {&q, "q"},
+                         {&kt, "kt"},
+                         {&v, "v"}}) {
+    e.validate_tensor(t, name);
+    if (t->dtype() != DType::F16)
+      fail(op + ": " + name + " must be f16 storage, got " + dtype_name(t->dtype()));
+  }
+  e.validate_tensor(&table, "table");
+  ensure_f32(table, op, "table");
+  if (d.heads == 0 || d.kv_heads == 0 || d.head_dim == 0 || d.rot_dim == 0 || d.rot_dim % 2 != 0 ||
+      d.rot_dim > d.head_dim)
+    fail(op + ": invalid heads/kv_heads/dh/rot_dim (" + std::to_string(d.heads) + "/" +
+         std::to_string(d.kv_heads) + "/" + std::to_string(d.head_dim) + "/" +
+         std::to_string(d.rot_dim) + ")");
+  if (qkv.shape().size() != 2)
+    fail(op + ": qkv must be [T, n_qkv], got " + fmt_shape(qkv.shape()));
+  const uint32_t tokens = qkv.shape()[0], qkv_stride = qkv.shape()[1];
+  const uint64_t embd = (uint64_t)d.heads * d.head_dim, kv_dim = (uint64_t)d.kv_heads * d.head_dim;
+  const uint64_t want_stride = embd + 2 * kv_dim;
+  if (qkv_stride != want_stride)
+    fail(op + ": qkv N " + std::to_string(qkv_stride) + " != H*dh + 2*H_kv*dh (" +
+         std::to_string(want_stride) + ")");
+  if (q.shape() != std::vector<uint32_t>{d.heads, tokens, d.head_dim})
+    fail(op + ": q must be head-major [H=" + std::to_string(d.heads) + ", T=" +
+         std::to_string(tokens) + ", dh=" + std::to_string(d.head_dim) + "], got " +
+         fmt_shape(q.shape()));
+  if (kt.shape().size() != 3)
+    fail(op + ": kt must be [H_kv, dh, T_max], got " + fmt_shape(kt.shape()));
+  if (v.shape().size() != 3)
+    fail(op + ": v must be [H_kv, T_max, dh], got " + fmt_shape(v.shape()));
+  const uint32_t t_max = kt.shape()[2];
+  if (kt.shape()[0] != d.kv_heads || v.shape()[0] != d.kv_heads || kt.shape()[1] != d.head_dim ||
+      v.shape()[2] != d.head_dim || v.shape()[1] != t_max)
+    fail(op + ": cache shapes kt " + fmt_shape(kt.shape()) + " v " + fmt_shape(v.shape()) +
+         " vs H_kv=" + std::to_string(d.kv_heads) + " dh=" + std::to_string(d.head_dim));
+  if ((uint64_t)d.pos_base + tokens > t_max)
+    fail(op + ": pos_base " + std::to_string(d.pos_base) + " + T " + std::to_string(tokens) +
+         " exceeds T_max " + std::to_string(t_max));
+  const uint64_t needed = ((uint64_t)d.pos_base + tokens) * d.rot_dim;
+  if (table.len() < needed)
+    fail(op + ": table length " + std::to_string(table.len()) + " < required " +
+         std::to_string(needed) + " (pos_base " + std::to_string(d.pos_base) + " + " +
+         std::to_string(tokens) + " tokens, rot_dim " + std::to_string(d.rot_dim) + ")");
+  if (d.head_dim % 4 != 0)
+    fail(op + ": head_dim " + std::to_string(d.head_dim) + " must be a multiple of 4");
+  QkvPackArgs a{};
+  a.qkv = static_cast<const uint16_t *>(qkv.device_ptr());
+  a.q = static_cast<uint16_t *>(q.device_ptr());
+  a.kt = static_cast<uint16_t *>(kt.device_ptr());
+  a.v = static_cast<uint16_t *>(v.device_ptr());
+  a.table = static_cast<const float *>(table.device_ptr());
+  a.tokens = tokens;
+  a.heads = d.heads;
+  a.kv_heads = d.kv_heads;
+  a.head_dim = d.head_dim;
+  a.rot_dim = d.rot_dim;
+  a.pos_base = d.pos_base;
+  a.qkv_stride = qkv_stride;
+  a.t_max = t_max;
+  a.k_offset = (uint32_t)embd;
+  a.v_offset = (uint32_t)(embd + kv_dim);
+  const uint64_t items = (uint64_t)tokens * (d.heads + d.kv_heads) * (d.rot_dim / 2) +
+                         (uint64_t)tokens * d.kv_heads * (d.head_dim / 4);
+  return elem("ta_prefill_qkv_pack", grid_for(items, 256, e.ctx->cu_count()), a);
+}
+
 // Decode-attention chunk count (elementwise/mod.rs:233-241): about 64
 // positions (one wave block) per chunk, at least 8 and at most
 // kAttnDecodeMaxChunks chunks; position-driven launches always use the cap.
@@ -1777,6 +1926,16 @@ ElemLaunches plan_exec_elem(ExecutorImpl &e, const ExecOp &op) {
   case ExecOp::Kind::AttnDecode:
     return plan_attn_decode(e, need(op.in[0], "q"), need(op.in[1], "kt"), need(op.in[2], "v"),
                             need(op.aux, "scratch"), need(op.out, "out"), op.attn);
+  case ExecOp::Kind::RopeScatter:
+    return {plan_rope_scatter(e, need(op.in[0], "input"), need(op.in[1], "table"),
+                              need(op.out, "dst"), op.rope, op.scatter)};
+  case ExecOp::Kind::Binary:
+    return {plan_binary(e, need(op.in[0], "a"), need(op.in[1], "b"), need(op.out, "out"),
+                        op.binary)};
+  case ExecOp::Kind::PrefillQkvPack:
+    return {plan_prefill_qkv_pack(e, need(op.in[0], "qkv"), need(op.in[1], "table"),
+                                  need(op.out, "q"), need(op.aux, "kt"), need(op.aux2, "v"),
+                                  op.qkv)};
   case ExecOp::Kind::Matmul:
     break;
   }
@@ -1806,6 +1965,19 @@ RunStats Executor::run_copy_strided(const Tensor &src, const Tensor &dst,
 RunStats Executor::run_flash_attention(const Tensor &q, const Tensor &kt, const Tensor &v,
                                        const Tensor &out, const FlashAttentionDesc &desc) const {
   return impl_->run_elem(plan_flash(*impl_, q, kt, v, out, desc));
+}
+RunStats Executor::run_rope_scatter(const Tensor &input, const Tensor &table, const Tensor &dst,
+                                    const RopeDesc &desc, const RopeScatterDesc &scatter) const {
+  return impl_->run_elem(plan_rope_scatter(*impl_, input, table, dst, desc, scatter));
+}
+RunStats Executor::run_binary(const Tensor &a, const Tensor &b, const Tensor &out,
+                              BinaryOp op) const {
+  return impl_->run_elem(plan_binary(*impl_, a, b, out, op));
+}
+RunStats Executor::run_prefill_qkv_pack(const Tensor &qkv, const Tensor &table, const Tensor &q,
+                                        const Tensor &kt, const Tensor &v,
+                                        const PrefillQkvPackDesc &desc) const {
+  return impl_->run_elem(plan_prefill_qkv_pack(*impl_, qkv, table, q, kt, v, desc));
 }
 RunStats Executor::run_argmax(const Tensor &input, const U32Cell &result) const {
   return impl_->run_elem(plan_argmax(*impl_, input, result));

@@ -191,6 +191,30 @@ struct RopeDesc {
   uint32_t heads = 0, head_dim = 0, rot_dim = 0, pos_base = 0;
   uint64_t pos_addr = 0; // device address of a u32 position, 0 = none
 };
+// Destination of the fused RoPE + scatter (elementwise/mod.rs:144-159):
+// element (token, head, dim) goes to dst_offset (+ *pos_addr * pos_scale
+// when the RopeDesc has a position cell) + token * dst_strides[0] + head *
+// dst_strides[1] + dim * dst_strides[2].
+struct RopeScatterDesc {
+  uint32_t dst_offset = 0;
+  std::array<uint32_t, 3> dst_strides{};
+  uint32_t pos_scale = 0;
+};
+// Standalone binary combine (elementwise/mod.rs:242-252): out = a + beta *
+// b, or out = silu(a) * b.
+struct BinaryOp {
+  enum class Kind : uint32_t { AddScaled = 0, SiluMul = 1 };
+  Kind kind = Kind::AddScaled;
+  float beta = 0.0f;
+  static BinaryOp add_scaled(float beta) { return {Kind::AddScaled, beta}; }
+  static BinaryOp silu_mul() { return {Kind::SiluMul, 0.0f}; }
+};
+// Prefill QKV pack geometry (elementwise/mod.rs:186-199).
+struct PrefillQkvPackDesc {
+  uint32_t heads = 0, kv_heads = 0, head_dim = 0;
+  uint32_t rot_dim = 0; // even, <= head_dim; lanes past it pass through
+  uint32_t pos_base = 0; // absolute position of token 0
+};
 struct CopyDesc {
   std::array<uint32_t, 3> extent{};
   uint32_t src_offset = 0;
@@ -267,6 +291,9 @@ private:
 //   Argmax      in[0] input, cell result
 //   EmbedGather cell token ids, in[0] table, out
 //   AttnDecode  in[0] q, in[1] kt, in[2] v, aux scratch, out, attn
+//   RopeScatter in[0] input, in[1] table, out dst, rope, scatter
+//   Binary      in[0] a, in[1] b, out, binary
+//   PrefillQkvPack in[0] qkv, in[1] table, out q, aux kt, aux2 v, qkv
 struct ExecOp {
   enum class Kind {
     Matmul,
@@ -278,13 +305,17 @@ struct ExecOp {
     FlashAttn,
     Argmax,
     EmbedGather,
-    AttnDecode
+    AttnDecode,
+    RopeScatter,
+    Binary,
+    PrefillQkvPack
   };
   Kind kind = Kind::Matmul;
   MatmulOp matmul;
   std::array<const Tensor *, 3> in{};
   const Tensor *out = nullptr;
   const Tensor *aux = nullptr;
+  const Tensor *aux2 = nullptr;
   const U32Cell *cell = nullptr;
   float scalar = 0.0f;
   SoftmaxMask mask;
@@ -292,6 +323,9 @@ struct ExecOp {
   CopyDesc copy;
   FlashAttentionDesc flash;
   AttnDecodeDesc attn;
+  RopeScatterDesc scatter;
+  BinaryOp binary;
+  PrefillQkvPackDesc qkv;
 
   static ExecOp from_matmul(const MatmulOp &op) {
     ExecOp e;
@@ -338,6 +372,27 @@ struct ExecOp {
   static ExecOp embed_gather(const U32Cell &tokens, const Tensor &table, const Tensor &out) {
     ExecOp e = make(Kind::EmbedGather, {&table, nullptr, nullptr}, &out, 0.0f);
     e.cell = &tokens;
+    return e;
+  }
+  static ExecOp rope_scatter(const Tensor &input, const Tensor &table, const Tensor &dst,
+                             const RopeDesc &desc, const RopeScatterDesc &scatter) {
+    ExecOp e = make(Kind::RopeScatter, {&input, &table, nullptr}, &dst, 0.0f);
+    e.rope = desc;
+    e.scatter = scatter;
+    return e;
+  }
+  static ExecOp binary_op(const Tensor &a, const Tensor &b, const Tensor &out, BinaryOp op) {
+    ExecOp e = make(Kind::Binary, {&a, &b, nullptr}, &out, 0.0f);
+    e.binary = op;
+    return e;
+  }
+  static ExecOp prefill_qkv_pack(const Tensor &qkv, const Tensor &table, const Tensor &q,
+                                 const Tensor &kt, const Tensor &v,
+                                 const PrefillQkvPackDesc &desc) {
+    ExecOp e = make(Kind::PrefillQkvPack, {&qkv, &table, nullptr}, &q, 0.0f);
+    e.aux = &kt;
+    e.aux2 = &v;
+    e.qkv = desc;
     return e;
   }
   static ExecOp attn_decode(const Tensor &q, const Tensor &kt, const Tensor &v,
@@ -526,6 +581,14 @@ public:
   RunStats run_rope(const Tensor &input, const Tensor &table, const Tensor &output,
                     const RopeDesc &desc) const;
   RunStats run_copy_strided(const Tensor &src, const Tensor &dst, const CopyDesc &desc) const;
+  // ops.rs:243-380 and flash.rs:255-402: RoPE scattered into a cache,
+  // the binary combine, and the f16 prefill QKV pack.
+  RunStats run_rope_scatter(const Tensor &input, const Tensor &table, const Tensor &dst,
+                            const RopeDesc &desc, const RopeScatterDesc &scatter) const;
+  RunStats run_binary(const Tensor &a, const Tensor &b, const Tensor &out, BinaryOp op) const;
+  RunStats run_prefill_qkv_pack(const Tensor &qkv, const Tensor &table, const Tensor &q,
+                                const Tensor &kt, const Tensor &v,
+                                const PrefillQkvPackDesc &desc) const;
   // src/executor/elementwise/flash.rs:13-250: kt [H_kv, dh, T_max],
   // v [H_kv, T_max, dh], dh 64 or 128, H a multiple of H_kv.
   RunStats run_flash_attention(const Tensor &q, const Tensor &kt, const Tensor &v,

@@ -89,13 +89,24 @@ class _AttnDecodeDesc(C.Structure):
     _fields_ = [("kv_len", C.c_uint32), ("scale", C.c_float), ("pos_addr", C.c_uint64)]
 
 
+class _RopeScatterDesc(C.Structure):
+    _fields_ = [("dst_offset", C.c_uint32), ("dst_strides", C.c_uint32 * 3), ("pos_scale", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+class _QkvPackDesc(C.Structure):
+    _fields_ = [("heads", C.c_uint32), ("kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("rot_dim", C.c_uint32), ("pos_base", C.c_uint32), ("reserved", C.c_uint32)]
+
+
 class _ExecOp(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("mask_kind", C.c_uint32), ("valid_or_prefix", C.c_uint32),
                 ("rows_per_group", C.c_uint32), ("scalar", C.c_float), ("pos_scale", C.c_uint32),
                 ("pos_addr", C.c_uint64), ("inp", C.c_void_p * 3), ("out", C.c_void_p),
                 ("matmul", C.POINTER(_OpV3)), ("rope", _RopeDesc), ("copy", _CopyDesc),
                 ("flash", _FlashDesc), ("cell", C.c_void_p), ("aux", C.c_void_p),
-                ("attn", _AttnDecodeDesc)]
+                ("attn", _AttnDecodeDesc), ("aux2", C.c_void_p), ("scatter", _RopeScatterDesc),
+                ("binary_op", C.c_uint32), ("qkv", _QkvPackDesc)]
 
 
 class _DispatchInfo(C.Structure):
@@ -154,6 +165,9 @@ _sig("ta_u32_cell_read", C.c_int, P, C.POINTER(u32))
 _sig("ta_u32_cell_device_address", u64, P)
 _sig("ta_u32_cell_cap", u32, P)
 _sig("ta_argmax", C.c_int, P, P, P, C.POINTER(RunStats))
+_sig("ta_rope_scatter", C.c_int, P, P, P, P, C.POINTER(_RopeDesc), C.POINTER(_RopeScatterDesc), C.POINTER(RunStats))
+_sig("ta_binary", C.c_int, P, P, P, P, u32, f32, C.POINTER(RunStats))
+_sig("ta_prefill_qkv_pack", C.c_int, P, P, P, P, P, P, C.POINTER(_QkvPackDesc), C.POINTER(RunStats))
 _sig("ta_embed_gather", C.c_int, P, P, P, P, C.POINTER(RunStats))
 _sig("ta_attn_decode", C.c_int, P, P, P, P, P, P, C.POINTER(_AttnDecodeDesc), C.POINTER(RunStats))
 _sig("ta_prepared_create_exec", P, P, C.POINTER(_ExecOp), sz)
@@ -356,7 +370,10 @@ def _ops_array(ops: Sequence[MatmulOp]):
 
 SOFTMAX_MASK_FULL, SOFTMAX_MASK_PREFIX, SOFTMAX_MASK_CAUSAL = 0, 1, 2
 EXEC_MATMUL, EXEC_RMS_NORM, EXEC_LAYER_NORM, EXEC_SOFTMAX_ROWS, EXEC_ROPE, EXEC_COPY_STRIDED, \
-    EXEC_FLASH_ATTENTION, EXEC_ARGMAX, EXEC_EMBED_GATHER, EXEC_ATTN_DECODE = range(10)
+    EXEC_FLASH_ATTENTION, EXEC_ARGMAX, EXEC_EMBED_GATHER, EXEC_ATTN_DECODE, EXEC_ROPE_SCATTER, EXEC_BINARY, \
+    EXEC_PREFILL_QKV_PACK = range(13)
+# Binary combine ops (src/executor/elementwise/mod.rs:242-252).
+BINARY_OP_ADD_SCALED, BINARY_OP_SILU_MUL = 0, 1
 # Chunk bound of decode attention; scratch holds kv_heads * ATTN_DECODE_MAX_CHUNKS
 # * group * (dh + 2) f32 (src/executor/elementwise/mod.rs:229-232).
 ATTN_DECODE_MAX_CHUNKS = 32
@@ -410,6 +427,32 @@ class U32Cell:
 
 
 PosBuffer = HostU32Buffer = TokenIdBuffer = U32Cell
+
+
+@dataclass
+class RopeScatterDesc:
+    """src/executor/elementwise/mod.rs:144-159: element (t, h, d) goes to
+    dst_offset (+ position * pos_scale in a graph with a position cell) +
+    t * dst_strides[0] + h * dst_strides[1] + d * dst_strides[2]."""
+    dst_offset: int
+    dst_strides: Sequence[int]
+    pos_scale: int = 0
+
+    def _raw(self) -> _RopeScatterDesc:
+        return _RopeScatterDesc(self.dst_offset, (C.c_uint32 * 3)(*self.dst_strides), self.pos_scale, 0)
+
+
+@dataclass
+class PrefillQkvPackDesc:
+    """src/executor/elementwise/mod.rs:186-199."""
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rot_dim: int
+    pos_base: int = 0
+
+    def _raw(self) -> _QkvPackDesc:
+        return _QkvPackDesc(self.heads, self.kv_heads, self.head_dim, self.rot_dim, self.pos_base, 0)
 
 
 @dataclass
@@ -520,6 +563,21 @@ class ExecOp:
     @staticmethod
     def flash_attn(q, kt, v, out, desc: FlashAttentionDesc) -> "ExecOp":
         return ExecOp(EXEC_FLASH_ATTENTION, keep=[q, kt, v, out], inp=[q, kt, v], out=out, flash=desc._raw())
+
+    @staticmethod
+    def rope_scatter(input, table, dst, desc: RopeDesc, scatter: RopeScatterDesc) -> "ExecOp":
+        return ExecOp(EXEC_ROPE_SCATTER, keep=[input, table, dst], inp=[input, table], out=dst,
+                      rope=_RopeDesc(desc.heads, desc.head_dim, desc.rot_dim, desc.pos_base),
+                      pos_addr=desc.pos_addr, scatter=scatter._raw())
+
+    @staticmethod
+    def binary(a, b, out, op: int, beta: float = 0.0) -> "ExecOp":
+        return ExecOp(EXEC_BINARY, keep=[a, b, out], inp=[a, b], out=out, binary_op=op, scalar=beta)
+
+    @staticmethod
+    def prefill_qkv_pack(qkv, table, q, kt, v, desc: PrefillQkvPackDesc) -> "ExecOp":
+        return ExecOp(EXEC_PREFILL_QKV_PACK, keep=[qkv, table, q, kt, v], inp=[qkv, table], out=q,
+                      aux=kt.handle, aux2=v.handle, qkv=desc._raw())
 
     @staticmethod
     def argmax(input, result: U32Cell) -> "ExecOp":
@@ -691,6 +749,27 @@ class Executor:
         st = RunStats()
         d = desc._raw()
         _check(_lib.ta_flash_attention(self._h, q.handle, kt.handle, v.handle, out.handle, C.byref(d), C.byref(st)))
+        return st
+
+    def rope_scatter(self, input: Tensor, table: Tensor, dst: Tensor, desc: RopeDesc,
+                     scatter: RopeScatterDesc) -> RunStats:
+        st = RunStats()
+        rd, sd = _RopeDesc(desc.heads, desc.head_dim, desc.rot_dim, desc.pos_base), scatter._raw()
+        _check(_lib.ta_rope_scatter(self._h, input.handle, table.handle, dst.handle, C.byref(rd), C.byref(sd),
+                                    C.byref(st)))
+        return st
+
+    def binary(self, a: Tensor, b: Tensor, out: Tensor, op: int, beta: float = 0.0) -> RunStats:
+        st = RunStats()
+        _check(_lib.ta_binary(self._h, a.handle, b.handle, out.handle, op, beta, C.byref(st)))
+        return st
+
+    def prefill_qkv_pack(self, qkv: Tensor, table: Tensor, q: Tensor, kt: Tensor, v: Tensor,
+                         desc: PrefillQkvPackDesc) -> RunStats:
+        st = RunStats()
+        d = desc._raw()
+        _check(_lib.ta_prefill_qkv_pack(self._h, qkv.handle, table.handle, q.handle, kt.handle, v.handle,
+                                        C.byref(d), C.byref(st)))
         return st
 
     # ---- the GPU token loop (src/executor/elementwise/ops.rs:456-595, attn.rs) ----

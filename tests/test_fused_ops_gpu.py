@@ -1,0 +1,134 @@
+"""The remaining model ops of the reference's mixed-op graphs: the binary
+combine, RoPE scattered into a KV cache, and the f16 prefill QKV pack
+(tests/correctness/elementwise.rs:526-558, 668-697 and fusion.rs:250-345,
+346-535, 537-620), through the C ABI against the CPU oracle.
+
+Bars: rope-scatter and the QKV pack are bit-exact (same rotation and
+rounding as the oracle and as the composed rope + copy path); the binary
+combine is within 1e-6 (add) / 1e-5 (SiLU) of the f64 oracle, and its f16
+form equals the f32 form rounded to f16.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_binary_add_scaled_and_silu_mul(ta, ex, oracle):
+    n = 4099  # not a multiple of 4: the tail
+    ha, hb = oracle.fill_det(n, 7100), oracle.fill_det(n, 7101)
+    a, b, out = ex.tensor_from(ha, shape=[n]), ex.tensor_from(hb, shape=[n]), ex.tensor([n])
+    ex.binary(a, b, out, ta.BINARY_OP_ADD_SCALED, 0.5)
+    assert np.abs(ex.download(out) - oracle.binary_combine(ha, hb, 0, 0.5)).max() <= 1e-6
+    ex.binary(a, b, a, ta.BINARY_OP_SILU_MUL)  # in place
+    assert np.abs(ex.download(a) - oracle.binary_combine(ha, hb, 1)).max() <= 1e-5
+
+
+def test_binary_f16_matches_narrowed_f32(ta, ex, oracle):
+    n = 4099
+    ha = oracle.round_via_f16(oracle.fill_det(n, 6300))
+    hb = oracle.round_via_f16(oracle.fill_det(n, 6301))
+    a16, b16 = ex.tensor_from(ha, shape=[n], f16=True), ex.tensor_from(hb, shape=[n], f16=True)
+    a32, b32 = ex.tensor_from(ha, shape=[n]), ex.tensor_from(hb, shape=[n])
+    for op, beta in ((ta.BINARY_OP_ADD_SCALED, 0.5), (ta.BINARY_OP_SILU_MUL, 0.0)):
+        o16, o32 = ex.tensor([n], f16=True), ex.tensor([n])
+        ex.binary(a16, b16, o16, op, beta)
+        ex.binary(a32, b32, o32, op, beta)
+        assert np.array_equal(ex.download(o16), oracle.round_via_f16(ex.download(o32)))
+    with pytest.raises(ta.TensorAshError, match="must match a"):
+        ex.binary(a16, b32, ex.tensor([n], f16=True), ta.BINARY_OP_SILU_MUL)
+    with pytest.raises(ta.TensorAshError, match="element counts differ"):
+        ex.binary(a32, ex.tensor([n - 1]), ex.tensor([n]), ta.BINARY_OP_ADD_SCALED, 1.0)
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_rope_scatter_matches_rope_plus_copy(ta, ex, oracle, kv_f16):
+    """fusion.rs:250-329: partial rotary, a warm pos_base; the fused op equals
+    rope + strided copy bit for bit, and the oracle."""
+    tokens, heads, dh, rot, t_max, pos = 3, 2, 8, 6, 16, 5
+    hx = oracle.fill_det(tokens * heads * dh, 41000)
+    htab = oracle.fill_det(t_max * rot, 41001)
+    x, table = ex.tensor_from(hx, shape=[tokens, heads * dh]), ex.tensor_from(htab, shape=[t_max, rot // 2, 2])
+    poison = np.full(heads * dh * t_max, 7.0, np.float32)
+    ref = ex.tensor_from(poison, shape=[heads, dh, t_max], f16=kv_f16)
+    fused = ex.tensor_from(poison, shape=[heads, dh, t_max], f16=kv_f16)
+    desc = ta.RopeDesc(heads, dh, rot, pos)
+    roped = ex.tensor([tokens, heads * dh])
+    ex.rope(x, table, roped, heads, dh, rot, pos)
+    ex.copy_strided(roped, ref, (dh, heads, tokens), (1, dh, heads * dh), (t_max, dh * t_max, 1), dst_offset=pos)
+    ex.rope_scatter(x, table, fused, desc, ta.RopeScatterDesc(pos, (1, dh * t_max, t_max)))
+    got = ex.download(fused).reshape(-1)
+    assert np.array_equal(got, ex.download(ref).reshape(-1))
+    want = oracle.rope_scatter(hx, htab, tokens, heads, dh, rot, pos, poison, pos, (1, dh * t_max, t_max), kv_f16)
+    assert np.array_equal(got, want)
+
+
+def test_rope_scatter_graph_with_position_cell_and_bounds(ta, ex, oracle):
+    """fusion.rs:537-620: the decode k-rope + Kt append as one graph op,
+    replayed at new positions through a position cell; a destination past
+    the cache is rejected."""
+    heads, dh, rot, t_max = 4, 16, 16, 32
+    htab = oracle.fill_det(t_max * rot, 43001)
+    table = ex.tensor_from(htab, shape=[t_max, rot // 2, 2])
+    x = ex.tensor([1, heads * dh])
+    cache = ex.tensor_from(np.zeros(heads * dh * t_max, np.float32), shape=[heads, dh, t_max])
+    pos = ex.create_pos_buffer()
+    op = ta.ExecOp.rope_scatter(x, table, cache, ta.RopeDesc(heads, dh, rot, 0, pos.device_address),
+                                ta.RopeScatterDesc(0, (1, dh * t_max, t_max), pos_scale=1))
+    prep = ex.prepare_exec_ops([op])
+    want = np.zeros(heads * dh * t_max, np.float32)
+    for p in (0, 7, 31):
+        hx = oracle.fill_det(heads * dh, 43100 + p)
+        ex.upload(x, hx)
+        pos.set(p)
+        prep.run()
+        want = oracle.rope_scatter(hx, htab, 1, heads, dh, rot, p, want, p, (1, dh * t_max, t_max))
+        assert np.array_equal(ex.download(cache).reshape(-1), want), f"pos {p}"
+    prep.close()
+    with pytest.raises(ta.TensorAshError, match="destination access reaches element"):
+        ex.rope_scatter(x, table, cache, ta.RopeDesc(heads, dh, rot, 0),
+                        ta.RopeScatterDesc(t_max, (1, dh * t_max, t_max)))
+    with pytest.raises(ta.TensorAshError, match="must be different tensors"):
+        ex.rope_scatter(x, table, x, ta.RopeDesc(heads, dh, rot, 0), ta.RopeScatterDesc(0, (1, 1, 1)))
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_prefill_qkv_pack(ta, ex, oracle, graph):
+    """fusion.rs:346-535: GQA, a warm pos_base and partial rotary; Q, the Kt
+    columns and the V rows equal the oracle bit for bit and the rest of the
+    caches is untouched."""
+    tokens, heads, kvh, dh, rot, pos, t_max = 37, 8, 2, 64, 48, 9, 64
+    n = heads * dh + 2 * kvh * dh
+    hqkv = oracle.round_via_f16(oracle.fill_det(tokens * n, 44000))
+    htab = oracle.fill_det(t_max * rot, 44001)
+    kt0 = oracle.round_via_f16(oracle.fill_det(kvh * dh * t_max, 44002)).reshape(kvh, dh, t_max)
+    v0 = oracle.round_via_f16(oracle.fill_det(kvh * t_max * dh, 44003)).reshape(kvh, t_max, dh)
+    qkv = ex.tensor_from(hqkv, shape=[tokens, n], f16=True)
+    table = ex.tensor_from(htab, shape=[t_max, rot // 2, 2])
+    q = ex.tensor([heads, tokens, dh], f16=True)
+    kt = ex.tensor_from(kt0, shape=[kvh, dh, t_max], f16=True)
+    v = ex.tensor_from(v0, shape=[kvh, t_max, dh], f16=True)
+    desc = ta.PrefillQkvPackDesc(heads, kvh, dh, rot, pos)
+    if graph:
+        ex.run_exec_ops([ta.ExecOp.prefill_qkv_pack(qkv, table, q, kt, v, desc)])
+    else:
+        ex.prefill_qkv_pack(qkv, table, q, kt, v, desc)
+    wq, wkt, wv = oracle.prefill_qkv_pack(hqkv, htab, tokens, heads, kvh, dh, rot, pos, kt0, v0)
+    assert np.array_equal(ex.download(q).reshape(wq.shape), wq)
+    assert np.array_equal(ex.download(kt).reshape(wkt.shape), wkt)
+    assert np.array_equal(ex.download(v).reshape(wv.shape), wv)
+
+
+def test_prefill_qkv_pack_rejects_bad_geometry(ta, ex):
+    desc = ta.PrefillQkvPackDesc(2, 1, 8, 8, 0)
+    qkv, table = ex.tensor([4, 32], f16=True), ex.tensor([16, 4, 2])
+    q, kt, v = ex.tensor([2, 4, 8], f16=True), ex.tensor([1, 8, 16], f16=True), ex.tensor([1, 16, 8], f16=True)
+    with pytest.raises(ta.TensorAshError, match="qkv must be f16 storage"):
+        ex.prefill_qkv_pack(ex.tensor([4, 32]), table, q, kt, v, desc)
+    with pytest.raises(ta.TensorAshError, match="qkv N 32 != H\\*dh \\+ 2\\*H_kv\\*dh \\(32\\)|qkv N"):
+        ex.prefill_qkv_pack(ex.tensor([4, 30], f16=True), table, q, kt, v, desc)
+    with pytest.raises(ta.TensorAshError, match="exceeds T_max"):
+        ex.prefill_qkv_pack(qkv, table, q, kt, v, ta.PrefillQkvPackDesc(2, 1, 8, 8, 13))
+    with pytest.raises(ta.TensorAshError, match="invalid heads/kv_heads/dh/rot_dim"):
+        ex.prefill_qkv_pack(qkv, table, q, kt, v, ta.PrefillQkvPackDesc(2, 1, 8, 3, 0))

@@ -506,3 +506,61 @@ def test_attn_decode_pinned(oracle):
     assert np.allclose(flat[2, 3], vv[2, :kv_len].astype(np.float64).mean(axis=0), atol=1e-7)
     one = oracle.attn_decode(q, kt, v, kv_heads, group, t_max, dh, 1, 0.125).reshape(kv_heads, group, dh)
     assert np.array_equal(one[1, 2], vv[1, 0])
+
+
+def test_binary_combine_pinned(oracle):
+    """op_binary_body.glsl: a + beta*b, and silu(a)*b against torch's silu."""
+    import torch
+    a, b = oracle.fill_det(4099, 7100), oracle.fill_det(4099, 7101)
+    assert np.allclose(oracle.binary_combine(a, b, 0, 0.5), a.astype(np.float64) + 0.5 * b, rtol=1e-7, atol=0)
+    ref = (torch.nn.functional.silu(torch.from_numpy(a).double()) * torch.from_numpy(b).double()).numpy()
+    assert np.allclose(oracle.binary_combine(a, b, 1), ref, rtol=1e-6, atol=1e-7)
+    assert oracle.binary_combine(np.zeros(3, np.float32), np.ones(3, np.float32), 1).tolist() == [0.0] * 3
+
+
+def test_rope_scatter_pinned(oracle):
+    """rope_scatter equals the (pinned) rope_tokens followed by the (pinned)
+    strided copy into the Kt cache layout, for f32 and f16 destinations
+    (tests/correctness/fusion.rs:250-329)."""
+    tokens, heads, dh, rot, t_max, pos = 3, 2, 8, 6, 16, 5
+    x = oracle.fill_det(tokens * heads * dh, 41000)
+    table = oracle.fill_det(t_max * rot // 2 * 2, 41001)
+    cache = np.full(heads * dh * t_max, 7.0, np.float32)
+    got = oracle.rope_scatter(x, table, tokens, heads, dh, rot, pos, cache, pos, (1, dh * t_max, t_max))
+    roped = oracle.rope_tokens(x, table, tokens, heads, dh, rot, pos)
+    want = oracle.copy_strided(roped, cache, (dh, heads, tokens), 0, (1, dh, heads * dh), pos,
+                               (t_max, dh * t_max, 1))
+    assert np.array_equal(got, want)
+    got16 = oracle.rope_scatter(x, table, tokens, heads, dh, rot, pos, cache, pos, (1, dh * t_max, t_max), True)
+    assert np.array_equal(got16, np.where(got == 7.0, 7.0, oracle.round_via_f16(got)))
+
+
+def test_prefill_qkv_pack_pinned(oracle):
+    """prefill_qkv_pack against a per-element restatement of the three jobs
+    (Q head-major, K into Kt columns, V into V rows) on a GQA case with a
+    warm pos_base and partial rotary."""
+    tokens, heads, kvh, dh, rot, pos, t_max = 5, 4, 2, 8, 6, 3, 12
+    n = heads * dh + 2 * kvh * dh
+    qkv = oracle.round_via_f16(oracle.fill_det(tokens * n, 42000))
+    table = oracle.fill_det(t_max * rot, 42001)
+    kt0, v0 = np.zeros((kvh, dh, t_max), np.float32), np.zeros((kvh, t_max, dh), np.float32)
+    q, kt, v = oracle.prefill_qkv_pack(qkv, table, tokens, heads, kvh, dh, rot, pos, kt0, v0)
+    x = qkv.reshape(tokens, n)
+    tab = table.reshape(t_max, rot // 2, 2)
+    def rot_vec(vec, p):
+        out = vec.astype(np.float64).copy()
+        for i in range(rot // 2):
+            c, s = float(tab[p, i, 0]), float(tab[p, i, 1])
+            x0, x1 = float(vec[2 * i]), float(vec[2 * i + 1])
+            out[2 * i], out[2 * i + 1] = x0 * c - x1 * s, x0 * s + x1 * c
+        return out
+    for t in range(tokens):
+        for h in range(heads):
+            assert np.allclose(q[h, t], rot_vec(x[t, h * dh:(h + 1) * dh], pos + t), atol=2e-3)
+        for h in range(kvh):
+            k = x[t, heads * dh + h * dh: heads * dh + (h + 1) * dh]
+            assert np.allclose(kt[h, :, pos + t], rot_vec(k, pos + t), atol=2e-3)
+            assert np.array_equal(v[h, pos + t], x[t, heads * dh + kvh * dh + h * dh:][:dh])
+            assert np.array_equal(q[0, t, rot:], x[t, rot:dh])  # pass-through lanes
+    assert not kt[:, :, :pos].any() and not v[:, pos + tokens:].any()
+    assert np.array_equal(q, oracle.round_via_f16(q).reshape(q.shape))
