@@ -343,6 +343,15 @@ int ta_prefill_qkv_pack(const ta_executor *exec, const ta_tensor *qkv, const ta_
                         const ta_tensor *q, const ta_tensor *kt, const ta_tensor *v,
                         const ta_prefill_qkv_pack_desc *desc, ta_run_stats *stats);
 
+/* Executor::run_gemv_chain (src/executor/elementwise/gemv_chain.rs:14-194;
+ * Rust API only in the reference): up to TA_GEMV_CHAIN_MAX_JOBS M = 1 row
+ * GEMVs on row-major f16 B (f32 A and C; no bias, store, accumulate or
+ * packed B; activation none or SiLU; normed-A not with AddScaled), run in
+ * list order. */
+#define TA_GEMV_CHAIN_MAX_JOBS 8
+int ta_run_gemv_chain(const ta_executor *exec, const ta_matmul_op_v3 *jobs, size_t n_jobs,
+                      ta_run_stats *stats);
+
 /* Host-visible u32 cells (src/executor/cells.rs:10-205; Rust API only in
  * the reference): pinned, mapped host memory that kernels read and write
  * through ta_u32_cell_device_address and the host through
@@ -414,6 +423,7 @@ int ta_attn_decode(const ta_executor *exec, const ta_tensor *q, const ta_tensor 
  *                   scatter.pos_scale per position)
  *   BINARY          in[0] a, in[1] b, out; binary_op, scalar = beta
  *   PREFILL_QKV_PACK in[0] qkv, in[1] table, out q, aux kt, aux2 v; qkv
+ *   GEMV_CHAIN      matmul -> n_jobs jobs (ta_run_gemv_chain's rules)
  * pos_addr (ROPE, COPY_STRIDED): device address of a u32 position cell
  * read when the op runs (added to rope.pos_base; times pos_scale added to
  * copy.dst_offset), so a prepared graph replays at a new position after
@@ -432,6 +442,7 @@ enum {
   TA_EXEC_ROPE_SCATTER = 10,
   TA_EXEC_BINARY = 11,
   TA_EXEC_PREFILL_QKV_PACK = 12,
+  TA_EXEC_GEMV_CHAIN = 13,
 };
 typedef struct ta_exec_op {
   uint32_t kind; /* TA_EXEC_* */
@@ -454,6 +465,7 @@ typedef struct ta_exec_op {
   ta_rope_scatter_desc scatter;
   uint32_t binary_op; /* TA_BINARY_OP_* */
   ta_prefill_qkv_pack_desc qkv;
+  uint32_t n_jobs; /* GEMV_CHAIN */
 } ta_exec_op;
 int ta_run_exec_ops(const ta_executor *exec, const ta_exec_op *ops,
                     size_t n_ops, ta_run_stats *stats);

@@ -402,6 +402,15 @@ int ta_run_op_graph_v3(const ta_executor *exec, const ta_matmul_op_v3 *ops, size
   });
 }
 
+int ta_run_gemv_chain(const ta_executor *exec, const ta_matmul_op_v3 *jobs, size_t n_jobs,
+                      ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_gemv_chain: exec is null");
+    write_stats(stats,
+                e.exec->run_gemv_chain(checked_ops_v3(e, jobs, n_jobs, "ta_run_gemv_chain")));
+  });
+}
+
 int ta_run_op_graph_v2(const ta_executor *exec, const ta_matmul_op_v2 *ops, size_t n_ops,
                        ta_run_stats *stats) {
   return ffi_status([&] {
@@ -570,6 +579,11 @@ std::vector<ExecOp> checked_exec_ops(const ta_executor &e, const ta_exec_op *ops
     case TA_EXEC_EMBED_GATHER:
       out.push_back(ExecOp::embed_gather(*checked_cell(e, o.cell, where, "cell"),
                                          t(o.in[0], "table"), t(o.out, "out")));
+      break;
+    case TA_EXEC_GEMV_CHAIN:
+      if (!o.matmul && o.n_jobs > 0)
+        fail(where + ": matmul is null");
+      out.push_back(ExecOp::gemv_chain(checked_ops_v3(e, o.matmul, o.n_jobs, where)));
       break;
     case TA_EXEC_ROPE_SCATTER: {
       RopeDesc rd = rope_desc(o.rope);

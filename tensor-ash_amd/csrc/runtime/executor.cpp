@@ -162,6 +162,7 @@ using ElemLaunches = std::vector<ElemLaunch>;
 
 struct ExecutorImpl;
 ElemLaunches plan_exec_elem(ExecutorImpl &e, const ExecOp &op);
+void check_gemv_chain(const ExecutorImpl &e, const std::vector<MatmulOp> &jobs);
 
 struct ExecutorImpl {
   std::shared_ptr<Context> ctx;
@@ -832,14 +833,21 @@ struct ExecutorImpl {
   std::vector<ExecStep> plan_exec(const std::vector<ExecOp> &ops, uint64_t &flops) {
     std::vector<ExecStep> steps;
     for (const ExecOp &op : ops) {
-      if (op.kind == ExecOp::Kind::Matmul) {
-        validate_op(op.matmul);
+      if (op.kind == ExecOp::Kind::Matmul || op.kind == ExecOp::Kind::GemvChain) {
+        // A GEMV chain's jobs join the matmul segment in list order.
+        std::vector<MatmulOp> one{op.matmul};
+        const std::vector<MatmulOp> &list = op.kind == ExecOp::Kind::Matmul ? one : op.jobs;
+        if (op.kind == ExecOp::Kind::GemvChain)
+          check_gemv_chain(*this, op.jobs);
         if (steps.empty() || !steps.back().matmul) {
           steps.emplace_back();
           steps.back().matmul = true;
         }
-        steps.back().ops.push_back(op.matmul);
-        steps.back().res.push_back(ResolvedMatmul::from_op(op.matmul));
+        for (const MatmulOp &m : list) {
+          validate_op(m);
+          steps.back().ops.push_back(m);
+          steps.back().res.push_back(ResolvedMatmul::from_op(m));
+        }
       } else {
         steps.emplace_back();
         steps.back().elems = plan_exec_elem(*this, op);
@@ -1288,6 +1296,13 @@ RunStats Executor::run_ops(const std::vector<MatmulOp> &ops) const {
 RunStats Executor::run_op_graph(const std::vector<MatmulOp> &ops) const {
   return impl_->run_ops_impl(ops, true);
 }
+RunStats Executor::run_gemv_chain(const std::vector<MatmulOp> &jobs) const {
+  check_gemv_chain(*impl_, jobs);
+  RunStats st = impl_->run_ops_impl(jobs, true);
+  st.n_calls = jobs.size();
+  return st;
+}
+
 RunStats Executor::run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const {
   return impl_->run_split_k2(call, num_k_splits);
 }
@@ -1892,6 +1907,41 @@ ElemLaunches plan_attn_decode(ExecutorImpl &e, const Tensor &q, const Tensor &kt
 }
 } // namespace
 
+// gemv_chain.rs:17-45 and 106-179 (plan_gemv_chain, pack_gemv_job): the
+// same job rules and messages.
+void check_gemv_chain(const ExecutorImpl &e, const std::vector<MatmulOp> &jobs) {
+  if (jobs.empty())
+    fail("gemv_chain: empty job list");
+  if (jobs.size() > kGemvChainMaxJobs)
+    fail("gemv_chain: " + std::to_string(jobs.size()) + " jobs exceeds max " +
+         std::to_string(kGemvChainMaxJobs));
+  for (size_t i = 0; i < jobs.size(); ++i) {
+    const MatmulOp &op = jobs[i];
+    const std::string at = "gemv_chain[" + std::to_string(i) + "]: ";
+    e.validate_op(op);
+    if (!op.store.is_none())
+      fail(at + "fused store epilogues are not supported");
+    if (op.call.accumulate)
+      fail(at + "accumulate is not supported");
+    if (op.call.a->dtype() != DType::F32 || op.call.c->dtype() != DType::F32)
+      fail(at + "A and C must be f32 storage");
+    if (op.call.b->dtype() != DType::F16)
+      fail(at + "B must be f16 storage");
+    if (op.packed_b)
+      fail(at + "packed-B layout is not supported");
+    if (op.epilogue.bias)
+      fail(at + "bias epilogue is not supported");
+    const ResolvedMatmul d = ResolvedMatmul::from_op(op);
+    if (d.batch != 1 || d.m != 1)
+      fail(at + "requires batch=1 M=1 (got B=" + std::to_string(d.batch) + " M=" +
+           std::to_string(d.m) + ")");
+    if (op.epilogue.activation != Activation::None && op.epilogue.activation != Activation::Silu)
+      fail(at + "unsupported activation " + std::to_string((uint32_t)op.epilogue.activation));
+    if (op.normed_a && op.epilogue.binary.kind == EpilogueBinary::Kind::AddScaled)
+      fail(at + "NORM_A cannot combine with AddScaled");
+  }
+}
+
 ElemLaunches plan_exec_elem(ExecutorImpl &e, const ExecOp &op) {
   auto need = [&](const Tensor *t, const char *role) -> const Tensor & {
     if (!t)
@@ -1937,6 +1987,7 @@ ElemLaunches plan_exec_elem(ExecutorImpl &e, const ExecOp &op) {
                                   need(op.out, "q"), need(op.aux, "kt"), need(op.aux2, "v"),
                                   op.qkv)};
   case ExecOp::Kind::Matmul:
+  case ExecOp::Kind::GemvChain:
     break;
   }
   fail("internal: plan_exec_elem on a matmul step");

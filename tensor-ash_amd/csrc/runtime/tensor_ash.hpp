@@ -247,6 +247,8 @@ struct AttnDecodeDesc {
   float scale = 1.0f;
   uint64_t pos_addr = 0;
 };
+// Jobs of one run_gemv_chain (elementwise/mod.rs GEMV_CHAIN_MAX_JOBS).
+constexpr size_t kGemvChainMaxJobs = 8;
 // Chunk bound of decode attention; sizes its scratch: kv_heads *
 // kAttnDecodeMaxChunks * group * (dh + 2) f32 (elementwise/mod.rs:229-232).
 constexpr uint32_t kAttnDecodeMaxChunks = 32;
@@ -294,6 +296,7 @@ private:
 //   RopeScatter in[0] input, in[1] table, out dst, rope, scatter
 //   Binary      in[0] a, in[1] b, out, binary
 //   PrefillQkvPack in[0] qkv, in[1] table, out q, aux kt, aux2 v, qkv
+//   GemvChain   jobs (run_gemv_chain's rules)
 struct ExecOp {
   enum class Kind {
     Matmul,
@@ -308,10 +311,12 @@ struct ExecOp {
     AttnDecode,
     RopeScatter,
     Binary,
-    PrefillQkvPack
+    PrefillQkvPack,
+    GemvChain
   };
   Kind kind = Kind::Matmul;
   MatmulOp matmul;
+  std::vector<MatmulOp> jobs;
   std::array<const Tensor *, 3> in{};
   const Tensor *out = nullptr;
   const Tensor *aux = nullptr;
@@ -364,6 +369,12 @@ struct ExecOp {
     return e;
   }
 
+  static ExecOp gemv_chain(const std::vector<MatmulOp> &jobs) {
+    ExecOp e;
+    e.kind = Kind::GemvChain;
+    e.jobs = jobs;
+    return e;
+  }
   static ExecOp argmax(const Tensor &input, const U32Cell &result) {
     ExecOp e = make(Kind::Argmax, {&input, nullptr, nullptr}, nullptr, 0.0f);
     e.cell = &result;
@@ -568,6 +579,11 @@ public:
   RunStats run_matmul_graph(const std::vector<MatmulCall> &calls) const;
   RunStats run_ops(const std::vector<MatmulOp> &ops) const;
   RunStats run_op_graph(const std::vector<MatmulOp> &ops) const;
+  // src/executor/elementwise/gemv_chain.rs:14-194 (run_gemv_chain): up to
+  // kGemvChainMaxJobs M = 1 row GEMVs on row-major f16 weights, validated
+  // with the reference's rules, run in list order (each job sees the
+  // earlier jobs' writes) on the decode GEMV launches.
+  RunStats run_gemv_chain(const std::vector<MatmulOp> &jobs) const;
   RunStats run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const;
 
   // Model ops (src/executor/elementwise/ops.rs); in-place (input ==
@@ -593,6 +609,12 @@ public:
   // v [H_kv, T_max, dh], dh 64 or 128, H a multiple of H_kv.
   RunStats run_flash_attention(const Tensor &q, const Tensor &kt, const Tensor &v,
                                const Tensor &out, const FlashAttentionDesc &desc) const;
+  // flash.rs:41-50: the reference's SIMT route.  There is one route here,
+  // the same kernels as run_flash_attention.
+  RunStats run_flash_attention_simt(const Tensor &q, const Tensor &kt, const Tensor &v,
+                                    const Tensor &out, const FlashAttentionDesc &desc) const {
+    return run_flash_attention(q, kt, v, out, desc);
+  }
   // The GPU token loop (elementwise/ops.rs:456-595, attn.rs:14-185):
   // greedy argmax into a cell, the embedding rows of the cell's token ids
   // (out [embd] or [t, embd]), and split-K decode attention (q / out

@@ -106,7 +106,7 @@ class _ExecOp(C.Structure):
                 ("matmul", C.POINTER(_OpV3)), ("rope", _RopeDesc), ("copy", _CopyDesc),
                 ("flash", _FlashDesc), ("cell", C.c_void_p), ("aux", C.c_void_p),
                 ("attn", _AttnDecodeDesc), ("aux2", C.c_void_p), ("scatter", _RopeScatterDesc),
-                ("binary_op", C.c_uint32), ("qkv", _QkvPackDesc)]
+                ("binary_op", C.c_uint32), ("qkv", _QkvPackDesc), ("n_jobs", C.c_uint32)]
 
 
 class _DispatchInfo(C.Structure):
@@ -155,6 +155,7 @@ _sig("ta_prepared_create_v2", P, P, C.POINTER(_OpV2), sz, u32)
 _sig("ta_run_ops_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
 _sig("ta_run_op_graph_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
 _sig("ta_prepared_create_v3", P, P, C.POINTER(_OpV3), sz, u32)
+_sig("ta_run_gemv_chain", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
 _sig("ta_tensor_device_address", u64, P)
 _sig("ta_flash_attention", C.c_int, P, P, P, P, P, C.POINTER(_FlashDesc), C.POINTER(RunStats))
 _sig("ta_run_exec_ops", C.c_int, P, C.POINTER(_ExecOp), sz, C.POINTER(RunStats))
@@ -371,7 +372,7 @@ def _ops_array(ops: Sequence[MatmulOp]):
 SOFTMAX_MASK_FULL, SOFTMAX_MASK_PREFIX, SOFTMAX_MASK_CAUSAL = 0, 1, 2
 EXEC_MATMUL, EXEC_RMS_NORM, EXEC_LAYER_NORM, EXEC_SOFTMAX_ROWS, EXEC_ROPE, EXEC_COPY_STRIDED, \
     EXEC_FLASH_ATTENTION, EXEC_ARGMAX, EXEC_EMBED_GATHER, EXEC_ATTN_DECODE, EXEC_ROPE_SCATTER, EXEC_BINARY, \
-    EXEC_PREFILL_QKV_PACK = range(13)
+    EXEC_PREFILL_QKV_PACK, EXEC_GEMV_CHAIN = range(14)
 # Binary combine ops (src/executor/elementwise/mod.rs:242-252).
 BINARY_OP_ADD_SCALED, BINARY_OP_SILU_MUL = 0, 1
 # Chunk bound of decode attention; scratch holds kv_heads * ATTN_DECODE_MAX_CHUNKS
@@ -427,6 +428,18 @@ class U32Cell:
 
 
 PosBuffer = HostU32Buffer = TokenIdBuffer = U32Cell
+GEMV_CHAIN_MAX_JOBS = 8
+
+
+def round_f32_via_f16(x):
+    """src/dtype.rs:108-112: f32 -> f16 (RNE) -> f32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def f16w_row_uses_k16(k: int, n: int) -> bool:
+    """src/pipeline/routing.rs:10-12 as this build routes it: whether the
+    packed decode weights of a [k, n] matrix use 32-column tiles."""
+    return f16w_row_tile_n(k, n) == 32
 
 
 @dataclass
@@ -563,6 +576,13 @@ class ExecOp:
     @staticmethod
     def flash_attn(q, kt, v, out, desc: FlashAttentionDesc) -> "ExecOp":
         return ExecOp(EXEC_FLASH_ATTENTION, keep=[q, kt, v, out], inp=[q, kt, v], out=out, flash=desc._raw())
+
+    @staticmethod
+    def gemv_chain(jobs: Sequence["MatmulOp"]) -> "ExecOp":
+        raws = [j._raw_v3() for j in jobs]
+        arr = (_OpV3 * len(raws))(*raws)
+        return ExecOp(EXEC_GEMV_CHAIN, keep=[list(jobs), raws, arr], matmul=C.cast(arr, C.POINTER(_OpV3)),
+                      n_jobs=len(raws))
 
     @staticmethod
     def rope_scatter(input, table, dst, desc: RopeDesc, scatter: RopeScatterDesc) -> "ExecOp":
@@ -743,6 +763,15 @@ class Executor:
 
     def prepare_op_graph(self, ops: Sequence[MatmulOp]) -> Prepared:
         return Prepared(self, ops, True)
+
+    def run_gemv_chain(self, jobs: Sequence[MatmulOp]) -> RunStats:
+        """gemv_chain.rs:181-193: up to GEMV_CHAIN_MAX_JOBS M = 1 row GEMVs on
+        row-major f16 weights, in list order."""
+        raws = [j._raw_v3() for j in jobs]
+        arr = (_OpV3 * len(raws))(*raws)
+        st = RunStats()
+        _check(_lib.ta_run_gemv_chain(self._h, arr, len(raws), C.byref(st)))
+        return st
 
     # ---- causal prefill attention and mixed-op graphs ----
     def flash_attention(self, q: Tensor, kt: Tensor, v: Tensor, out: Tensor, desc: FlashAttentionDesc) -> RunStats:

@@ -132,3 +132,63 @@ def test_prefill_qkv_pack_rejects_bad_geometry(ta, ex):
         ex.prefill_qkv_pack(qkv, table, q, kt, v, ta.PrefillQkvPackDesc(2, 1, 8, 8, 13))
     with pytest.raises(ta.TensorAshError, match="invalid heads/kv_heads/dh/rot_dim"):
         ex.prefill_qkv_pack(qkv, table, q, kt, v, ta.PrefillQkvPackDesc(2, 1, 8, 3, 0))
+
+
+# ---------------------------------------------------------------- GEMV chain
+
+def _chain_ops(ta, x, attn, wo, w_up, w_gate, w_down, norm, o, up, gate, out):
+    E = ta.Epilogue
+    return [
+        ta.MatmulOp(attn, wo, o, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0)),
+        ta.MatmulOp(o, w_up, up, normed_a=(norm, 1e-5)),
+        ta.MatmulOp(o, w_gate, gate, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up),
+                    normed_a=(norm, 1e-5)),
+        ta.MatmulOp(gate, w_down, out, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=o, beta=1.0)),
+    ]
+
+
+def test_gemv_chain_mlp_matches_composed_graph(ta, ex, oracle):
+    """gemv_chain.rs:41-143: o-proj + normed SwiGLU MLP as one GEMV chain (and as
+    a graph op) gives the composed graph's bits."""
+    k, n_o, n_ff = 256, 256, 384
+    f16w = lambda r, c, seed: ex.tensor_from(oracle.fill_det(r * c, seed), shape=[r, c], f16=True)
+    x = ex.tensor_from(oracle.fill_det(k, 1), shape=[1, k])
+    attn = ex.tensor_from(oracle.fill_det(k, 2), shape=[1, k])
+    wo, w_up, w_gate, w_down = f16w(k, n_o, 3), f16w(n_o, n_ff, 4), f16w(n_o, n_ff, 5), f16w(n_ff, n_o, 6)
+    norm = ex.tensor_from(oracle.fill_det(n_o, 7), shape=[n_o])
+    bufs = lambda: (ex.tensor([1, n_o]), ex.tensor([1, n_ff]), ex.tensor([1, n_ff]), ex.tensor([1, n_o]))
+    composed, chained, graphed = bufs(), bufs(), bufs()
+    ex.run_exec_ops([ta.ExecOp.matmul(op) for op in
+                     _chain_ops(ta, x, attn, wo, w_up, w_gate, w_down, norm, *composed)])
+    st = ex.run_gemv_chain(_chain_ops(ta, x, attn, wo, w_up, w_gate, w_down, norm, *chained))
+    assert st.n_calls == 4
+    ex.run_exec_ops([ta.ExecOp.gemv_chain(_chain_ops(ta, x, attn, wo, w_up, w_gate, w_down, norm, *graphed))])
+    want = ex.download(composed[3])
+    assert np.array_equal(ex.download(chained[3]), want)
+    assert np.array_equal(ex.download(graphed[3]), want)
+
+
+def test_gemv_chain_single_job_and_rejections(ta, ex, oracle):
+    """gemv_chain.rs:145-175 (one job against the f64 CPU product) and the
+    job rules of pack_gemv_job (gemv_chain.rs:106-179)."""
+    k, n = 128, 96
+    ha, hb = oracle.fill_det(k, 11), oracle.fill_det(k * n, 12)
+    a, b, c = ex.tensor_from(ha, shape=[1, k]), ex.tensor_from(hb, shape=[k, n], f16=True), ex.tensor([1, n])
+    ex.run_gemv_chain([ta.MatmulOp(a, b, c)])
+    ref = oracle.cpu_bmm(ha, oracle.round_via_f16(hb), None, 1, 1, n, k)
+    assert np.abs(ex.download(c).reshape(-1) - ref).max() <= oracle.tolerance(k)
+    with pytest.raises(ta.TensorAshError, match="9 jobs exceeds max 8"):
+        ex.run_gemv_chain([ta.MatmulOp(a, b, c)] * 9)
+    with pytest.raises(ta.TensorAshError, match="B must be f16 storage"):
+        ex.run_gemv_chain([ta.MatmulOp(a, ex.tensor([k, n]), c)])
+    with pytest.raises(ta.TensorAshError, match="requires batch=1 M=1"):
+        ex.run_gemv_chain([ta.MatmulOp(ex.tensor([2, k]), b, ex.tensor([2, n]))])
+    with pytest.raises(ta.TensorAshError, match="bias epilogue is not supported"):
+        ex.run_gemv_chain([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=ex.tensor([n])))])
+    with pytest.raises(ta.TensorAshError, match="unsupported activation"):
+        ex.run_gemv_chain([ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(activation=ta.ACTIVATION_GELU))])
+    with pytest.raises(ta.TensorAshError, match="cannot combine with (the )?AddScaled"):
+        ex.run_gemv_chain([ta.MatmulOp(a, b, c, normed_a=(ex.tensor([k]), 1e-5),
+                                       epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=c, beta=1.0))])
+    with pytest.raises(ta.TensorAshError, match="empty job list"):
+        ex.run_gemv_chain([])
