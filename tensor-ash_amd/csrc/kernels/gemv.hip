@@ -1,5 +1,7 @@
-// Decode GEMV (M = 1..8 rows) for gfx950, HBM-bound, no MFMA, and the
-// persistent decode SwiGLU MLP built from it.
+// Decode GEMV (M = 1..8 rows) for gfx950, HBM-bound, and the persistent
+// decode SwiGLU MLP built from it.  1-2 rows and f32 or 32-column weights
+// use vector FMAs; f16 64-column tiles with 4-8 rows use f16 MFMAs on X
+// split into three f16 pieces (Gemv::stage_split).
 //
 // Replaces the reference's row GEMV family
 // (shaders/matmul_row_bda_kernel.glsl:186-403 and the
@@ -113,6 +115,29 @@ TA_DEVICE void poll_words(At at, Need need, uint32_t tag, float (&out)[N], const
   }
 }
 
+// Decode-MLP hand-off pre-poll.  Before reading a window's published
+// words [col][MR] (a whole round of loads per thread, repeated until all
+// carry the tag), wait on one sentinel word per producer tile -- its
+// column 63 at row `row` (the last row written) -- with 4 or 8 loads a
+// round from wave 0.  The tile's stores go out together, so the rest have
+// nearly always landed by then; the window's words are then read and
+// their tags checked as before (poll_words), so a sentinel seen early
+// costs another round, never a wrong value.  Used from M = 4 up: with
+// fewer rows the window's words are few enough that the extra round trip
+// costs more than the re-reads it saves.  Bounded like poll_words; on the
+// limit the word poll that follows raises the status word.
+TA_DEVICE void poll_sentinels(const uint64_t *words, uint32_t first_tile, uint32_t ntiles,
+                              uint32_t mr, uint32_t row, uint32_t tag, const MlpArgs &m) {
+  const uint32_t tid = threadIdx.x;
+  const uint64_t *f = words + ((uint64_t)(first_tile + tid) * 64u + 63u) * mr + row;
+  for (uint32_t polls = 0;;) {
+    const bool ok = tid >= ntiles || (uint32_t)(load_word(f) >> 32) == tag;
+    if (__syncthreads_and(ok) || ++polls >= m.spin_limit)
+      return;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
 template <int MR, bool DUAL, int TW, bool WF32, int MODE, int XROWS, int UNROLL = 16>
 struct Gemv {
   static constexpr int WAYS = DUAL ? 2 : 1;
@@ -127,14 +152,27 @@ struct Gemv {
   // The X window's LDS is reused to stage the partials of all K windows
   // for the last unit of a tile: PSTAGE floats, 16 loads per thread.
   static constexpr int PSTAGE = 16 * kThreads;
-  static constexpr int XS = XROWS * MR > PSTAGE ? XROWS * MR : PSTAGE;
   // Decode-MLP tile reducers poll the other windows' words in rounds of
-  // MPOLL loads per thread (one round covers them all for M <= 2).
-  static constexpr int MPOLL = 8;
+  // MPOLL loads per thread: each further round is another poll round trip
+  // behind the weight stream.  One round covers the 7 (gate/up) or 10
+  // (down) other windows of the 2048 x 5632 layer up to M = 4; M = 8 takes
+  // two (32 loads a round spill).
+  static constexpr int MPOLL = MODE == kStandalone || MR == 1 ? 8 : 16;
+  static constexpr int PST = PSTAGE > MPOLL * kThreads ? PSTAGE : MPOLL * kThreads;
+  static constexpr int XS0 = XROWS * MR > PST ? XROWS * MR : PST;
+  // Matrix-core route (f16 weights, 64-column tiles, 4..8 rows): each weight
+  // would otherwise feed MR vector FMAs, which at M >= 4 outlast the weight
+  // stream once X has arrived.  X is staged as three f16 pieces per value
+  // (3 * XROWS * MR halfs) instead of f32.
+  static constexpr bool MF = !WF32 && TW == 64 && MR >= 4;
+  static constexpr int XSMF = MF ? (3 * XROWS * MR + 1) / 2 : 0;
+  static constexpr int XS = XS0 > XSMF ? XS0 : XSMF;
 
   struct Smem {
     float xs[XS]; // X window, later the partials of the last unit
     float red[kWaves * OUTS];
+    float xmax[kWaves * 8]; // matrix-core route: per-wave row maxima
+    float xinv[8];          // and the rows' inverse scales
     uint32_t last_flag;
   };
 
@@ -236,6 +274,8 @@ struct Gemv {
       // words of the window ([k][MR] order) until all carry this launch's
       // tag; vmcnt retires in order, so the first poll lands after them.
       issue(0, cur);
+      if constexpr (MR >= 4)
+        poll_sentinels(mlp->tag_h, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag, *mlp);
       poll_words<XPT>(
           [&](int j) {
             bool ok;
@@ -259,6 +299,8 @@ struct Gemv {
       // Chained layer: weights first, then X = the previous layer's y from
       // its tagged words ([k][MR] order, the previous layer's tag).
       issue(0, cur);
+      if constexpr (MR >= 4)
+        poll_sentinels(mlp->tag_y, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag - 1u, *mlp);
       poll_words<XPT>(
           [&](int j) {
             bool ok;
@@ -294,9 +336,13 @@ struct Gemv {
           normalize_x(p, *fu, k0, xr, sm);
       }
     }
+    if constexpr (MF) {
+      stage_split(xr, sm);
+    } else {
 #pragma unroll
-    for (int j = 0; j < XPT; ++j)
-      sm.xs[tid + j * kThreads] = xr[j];
+      for (int j = 0; j < XPT; ++j)
+        sm.xs[tid + j * kThreads] = xr[j];
+    }
     __syncthreads();
     TA_GEMV_TRACE(1);
 
@@ -354,35 +400,117 @@ struct Gemv {
       }
     };
 
+    // Matrix-core route.  v_mfma_f32_16x16x16_f16 computes D[m][n] +=
+    // sum_k A[m][k] B[k][n] with lane l holding A[l%16][4(l/16)+i],
+    // B[4(l/16)+i][l%16] and D[4(l/16)+i][l%16], i = 0..3.  A lane's loads
+    // 4j..4j+3 of a group hold 4 rows x its 4 columns 4cp..4cp+3 (cp =
+    // l%16, row group r0 = l/16), so byte permutes inside the lane give
+    // block c's B operand (those 4 rows of column 4cp+c): k slot 4*r0 + i
+    // is window row kb + 64j + 16i + 4*wave + r0, for every block.  A is
+    // X's three pieces at the same rows (rows m >= MR duplicate row m % MR;
+    // their outputs are dropped).  Passes hi, mid, lo per step, blocks
+    // interleaved so consecutive MFMAs are independent.
+    f32x4 macc[WAYS][4];
+#pragma unroll
+    for (int w = 0; w < WAYS; ++w)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        macc[w][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto consume_mf = [&](uint32_t kb, const uint64_t (&raw)[WAYS][kUnroll]) {
+      const _Float16 *xa = reinterpret_cast<const _Float16 *>(sm.xs);
+      const uint32_t ml = (lane & 15u) % MR;
+#pragma unroll
+      for (int j = 0; j < kUnroll / 4; ++j) {
+        const uint32_t off = ((((kb >> 6) + j) * 16u + my_first) * MR + ml) * 4u;
+        f16x4 a[3];
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+          a[q] = *reinterpret_cast<const f16x4 *>(xa + q * XROWS * MR + off);
+        f16x4 b[WAYS][4];
+#pragma unroll
+        for (int w = 0; w < WAYS; ++w) {
+          uint32_t lo[4], hi[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int u = 4 * j + i;
+            const uint32_t kk = kb + u * RPW + my_first;
+            const bool ok = EXACT || (k0 + kk < kend && col_ok);
+            const uint64_t r = ok ? raw[w][u] : 0ull;
+            lo[i] = (uint32_t)r;
+            hi[i] = (uint32_t)(r >> 32);
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t *src = c < 2 ? lo : hi;
+            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t d0 = __builtin_amdgcn_perm(src[1], src[0], sel);
+            const uint32_t d1 = __builtin_amdgcn_perm(src[3], src[2], sel);
+            b[w][c] = __builtin_bit_cast(f16x4, (uint64_t)d0 | ((uint64_t)d1 << 32));
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+#pragma unroll
+          for (int w = 0; w < WAYS; ++w)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              macc[w][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[q], b[w][c], macc[w][c], 0, 0, 0);
+      }
+    };
+
     // kchunk is a multiple of G (host contract): whole groups only.  The
     // resident grid keeps HBM busy while each wave waits on its group.
-    consume(0, cur);
-    for (uint32_t kb = G; kb < p.kchunk; kb += G) {
-      issue(kb, cur);
-      consume(kb, cur);
+    if constexpr (MF) {
+      consume_mf(0, cur);
+      for (uint32_t kb = G; kb < p.kchunk; kb += G) {
+        issue(kb, cur);
+        consume_mf(kb, cur);
+      }
+    } else {
+      consume(0, cur);
+      for (uint32_t kb = G; kb < p.kchunk; kb += G) {
+        issue(kb, cur);
+        consume(kb, cur);
+      }
     }
     TA_GEMV_TRACE(2);
 
-    // Rows of one wave: lanes cp, cp + LPR, ... hold the same columns.
+    if constexpr (MF) {
+      // D rows 4*(lane/16)+i below MR, unscaled by the row's power of two.
 #pragma unroll
-    for (int off = LPR; off < 64; off <<= 1)
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t m = 4u * (lane >> 4) + i;
+        if (m < MR) {
+          const float inv = sm.xinv[m];
 #pragma unroll
-      for (int w = 0; w < WAYS; ++w)
+          for (int w = 0; w < WAYS; ++w)
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
-#pragma unroll
-          for (int c = 0; c < CPL; ++c)
-            acc[w][m][c] += __shfl_xor(acc[w][m][c], off);
-    if (r0 == 0) {
-#pragma unroll
-      for (int w = 0; w < WAYS; ++w)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-          float *dst = &sm.red[((wave * WAYS + w) * MR + m) * TW + CPL * cp];
-#pragma unroll
-          for (int c = 0; c < CPL; ++c)
-            dst[c] = acc[w][m][c];
+            for (int c = 0; c < 4; ++c)
+              sm.red[((wave * WAYS + w) * MR + m) * TW + 4 * (lane & 15u) + c] = macc[w][c][i] * inv;
         }
+      }
+    } else {
+      // Rows of one wave: lanes cp, cp + LPR, ... hold the same columns.
+#pragma unroll
+      for (int off = LPR; off < 64; off <<= 1)
+#pragma unroll
+        for (int w = 0; w < WAYS; ++w)
+#pragma unroll
+          for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+              acc[w][m][c] += __shfl_xor(acc[w][m][c], off);
+      if (r0 == 0) {
+#pragma unroll
+        for (int w = 0; w < WAYS; ++w)
+#pragma unroll
+          for (int m = 0; m < MR; ++m) {
+            float *dst = &sm.red[((wave * WAYS + w) * MR + m) * TW + CPL * cp];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+              dst[c] = acc[w][m][c];
+          }
+      }
     }
     __syncthreads();
 
@@ -473,6 +601,55 @@ struct Gemv {
           __hip_atomic_store(mlp->gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
+    }
+  }
+
+  // Matrix-core route: stage the window's X as three f16 pieces.  Row m
+  // is scaled by s_m = 2^(15 - e), e = the exponent of the window's max|x|
+  // in that row (max * s_m in [2^14, 2^15)); v = x * s_m splits exactly
+  // into hi = f16(v), mid = f16(v - hi), lo = f16(v - hi - mid), so the
+  // pieces carry v to ~33 significant bits and values down to 2^-39 of
+  // the row maximum.  f16 x f16 products are exact in the f32 MFMA
+  // accumulator; the unit scales its partials by 1/s_m (exact, a power of
+  // two).  Layout: piece q, then window row kk = 64t + 16i + s as
+  // [t][s][m][i], so a lane's A operand (4 rows 16 apart) is one 8-byte
+  // read.  A thread's values all belong to row tid % MR (256 % MR == 0).
+  static TA_DEVICE void stage_split(const float (&xr)[XROWS * MR / kThreads], Smem &sm) {
+    constexpr int XPT = XROWS * MR / kThreads;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t m = tid % MR;
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < XPT; ++j)
+      mx = fmaxf(mx, fabsf(xr[j]));
+#pragma unroll
+    for (int off = MR; off < 64; off <<= 1)
+      mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane < MR)
+      sm.xmax[wave * MR + lane] = mx;
+    __syncthreads();
+    mx = sm.xmax[m];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w)
+      mx = fmaxf(mx, sm.xmax[w * MR + m]);
+    int e = 0;
+    (void)frexpf(mx, &e);
+    const int sx = min(126, max(-126, 15 - e));
+    const float s = ldexpf(1.0f, sx);
+    if (tid < MR)
+      sm.xinv[tid] = ldexpf(1.0f, -sx);
+    _Float16 *xa = reinterpret_cast<_Float16 *>(sm.xs);
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+      const uint32_t kk = (tid + j * kThreads) / MR;
+      const uint32_t off = ((((kk >> 6) * 16u + (kk & 15u)) * MR + m) * 4u) + ((kk >> 4) & 3u);
+      const float v = xr[j] * s;
+      const _Float16 h = (_Float16)v;
+      const float r = v - (float)h;
+      const _Float16 md = (_Float16)r;
+      xa[off] = h;
+      xa[XROWS * MR + off] = md;
+      xa[2 * XROWS * MR + off] = (_Float16)(r - (float)md);
     }
   }
 

@@ -542,12 +542,13 @@ struct ExecutorImpl {
     }
   }
 
-  // Rows up to which op triples become decode-MLP launches.  Above 2 the
-  // per-layer FMA work on the vector ALUs outweighs the saved launch and
-  // hand-off (measured: the separate dual gate/up and down launches are
-  // faster at M = 4 and 8).  TA_MLP_MAX_ROWS overrides (at most 8).
+  // Rows up to which op triples become decode-MLP launches: every M the
+  // kernels have (1..8; from 4 rows the inner product runs on the matrix
+  // cores and the hand-offs pre-poll sentinels, which made the chain
+  // faster than the separate dual gate/up and down launches at M = 4 and
+  // 8 as well).  TA_MLP_MAX_ROWS lowers it (at most 8).
   static uint32_t mlp_max_rows() {
-    uint32_t rows = 2;
+    uint32_t rows = 8;
     if (const char *env = std::getenv("TA_MLP_MAX_ROWS"))
       rows = (uint32_t)std::strtoul(env, nullptr, 10);
     return std::min<uint32_t>(rows, 8);

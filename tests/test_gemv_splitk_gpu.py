@@ -84,7 +84,7 @@ def test_swiglu_mlp_graph(ta, ex, oracle, m, monkeypatch):
     down-proj sums K in 512-row windows inside the MLP launch and in the
     planner's windows standalone, so both are checked against the oracle,
     and repeated MLP launches must repeat their bits."""
-    monkeypatch.setenv("TA_MLP_MAX_ROWS", "8")  # the MLP launch at every M (default: M <= 2)
+    monkeypatch.setenv("TA_MLP_MAX_ROWS", "8")  # the MLP launch at every M (the default)
     hdim, ffn = 2048, 5632
     wg, wgr = f16_weights(oracle, hdim, ffn, 101)
     wu, wur = f16_weights(oracle, hdim, ffn, 102)
