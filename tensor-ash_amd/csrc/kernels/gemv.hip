@@ -47,6 +47,15 @@
 #define TA_GEMV_TRACE_ROLE(role)
 #endif
 
+// Row counts from which the matrix-core route and the hand-off sentinel
+// pre-poll apply (compile-time, for measurement builds).
+#ifndef TA_GEMV_MFMA_MIN_ROWS
+#define TA_GEMV_MFMA_MIN_ROWS 4
+#endif
+#ifndef TA_GEMV_SENTINEL_MIN_ROWS
+#define TA_GEMV_SENTINEL_MIN_ROWS 4
+#endif
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -164,7 +173,7 @@ struct Gemv {
   // would otherwise feed MR vector FMAs, which at M >= 4 outlast the weight
   // stream once X has arrived.  X is staged as three f16 pieces per value
   // (3 * XROWS * MR halfs) instead of f32.
-  static constexpr bool MF = !WF32 && TW == 64 && MR >= 4;
+  static constexpr bool MF = !WF32 && TW == 64 && MR >= TA_GEMV_MFMA_MIN_ROWS;
   static constexpr int XSMF = MF ? (3 * XROWS * MR + 1) / 2 : 0;
   static constexpr int XS = XS0 > XSMF ? XS0 : XSMF;
 
@@ -274,7 +283,7 @@ struct Gemv {
       // words of the window ([k][MR] order) until all carry this launch's
       // tag; vmcnt retires in order, so the first poll lands after them.
       issue(0, cur);
-      if constexpr (MR >= 4)
+      if constexpr (MR >= TA_GEMV_SENTINEL_MIN_ROWS)
         poll_sentinels(mlp->tag_h, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag, *mlp);
       poll_words<XPT>(
           [&](int j) {
@@ -299,7 +308,7 @@ struct Gemv {
       // Chained layer: weights first, then X = the previous layer's y from
       // its tagged words ([k][MR] order, the previous layer's tag).
       issue(0, cur);
-      if constexpr (MR >= 4)
+      if constexpr (MR >= TA_GEMV_SENTINEL_MIN_ROWS)
         poll_sentinels(mlp->tag_y, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag - 1u, *mlp);
       poll_words<XPT>(
           [&](int j) {
