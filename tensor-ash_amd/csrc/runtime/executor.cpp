@@ -1605,7 +1605,7 @@ ElemLaunch plan_flash(ExecutorImpl &e, const Tensor &q, const Tensor &kt, const 
   a.o_head_stride = o_hs;
   a.o_row_stride = o_rs;
   a.heads = heads;
-  a.q_tiles = (t_q + 63) / 64;
+  a.q_tiles = (t_q + 63) / 64; // query rows per workgroup: the kernel's 32 * QB
   const uint64_t groups = (uint64_t)a.q_tiles * heads;
   if (groups == 0 || groups > UINT32_MAX)
     fail(op + ": empty or oversized launch (T_q " + std::to_string(t_q) + ", H " +
@@ -1615,7 +1615,9 @@ ElemLaunch plan_flash(ExecutorImpl &e, const Tensor &q, const Tensor &kt, const 
                    : kv16 ? (dh == 64 ? "ta_flash_attention_kv16_dh64"
                                       : "ta_flash_attention_kv16_dh128")
                           : (dh == 64 ? "ta_flash_attention_dh64" : "ta_flash_attention_dh128");
-  return elem(sym, (uint32_t)groups, a);
+  ElemLaunch l = elem(sym, (uint32_t)groups, a);
+  l.threads = dh == 64 ? 512 : 256; // QB query blocks x KP key parts: 2 x 4 at dh 64, 2 x 2 at 128
+  return l;
 }
 
 // ops.rs:467-500 (plan_argmax): f32 input, any shape, read flat.
