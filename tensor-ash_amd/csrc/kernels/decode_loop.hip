@@ -322,32 +322,51 @@ TA_ATTN_DECODE(ta_attn_decode_dh128, 128, false)
 TA_ATTN_DECODE(ta_attn_decode_kv16_dh64, 64, true)
 TA_ATTN_DECODE(ta_attn_decode_kv16_dh128, 128, true)
 
-// One wave per (kv head, row): lane i < num_chunks (<= 64) loads chunk i's
-// max and sum; the chunk weights go to LDS; the normaliser and each output
-// sum over the chunks in chunk order.
+// One wave per (kv head, row): lane i < num_chunks (<= 32) loads chunk i's
+// max and sum, and every lane loads its output columns (d = lane, and
+// lane + 64 at head dim 128) of all 32 chunk slots in the same batch
+// (slots past num_chunks re-read the last chunk and are not used), so the
+// merge costs one memory round trip.  The chunk weights go to LDS; the
+// normaliser and each output sum over the chunks in chunk order.
 extern "C" __global__ __launch_bounds__(64) void ta_attn_decode_combine(AttnCombineArgs p) {
+  constexpr int MAXC = 32; // TA_ATTN_DECODE_MAX_CHUNKS
   __shared__ float wsh[64], lsh[64];
   const uint32_t row_id = blockIdx.x, lane = threadIdx.x;
   const uint32_t kvh = row_id / p.group, r = row_id % p.group;
-  const uint32_t stride = p.dh + 2;
-  const uint64_t row0 = ((uint64_t)kvh * p.num_chunks * p.group + r) * stride;
+  const uint32_t stride = p.dh + 2, nc = p.num_chunks;
+  const uint64_t row0 = ((uint64_t)kvh * nc * p.group + r) * stride;
   const uint64_t step = (uint64_t)p.group * stride;
-  const bool live = lane < p.num_chunks;
-  const float mi = live ? p.scratch[row0 + lane * step + p.dh] : -FLT_MAX;
-  const float li = live ? p.scratch[row0 + lane * step + p.dh + 1] : 0.0f;
+  const bool live = lane < nc;
+  const uint32_t lc = live ? lane : 0u;
+  float mi = p.scratch[row0 + lc * step + p.dh];
+  float li = p.scratch[row0 + lc * step + p.dh + 1];
+  const uint32_t d1 = lane + 64u < p.dh ? lane + 64u : lane;
+  float o0[MAXC], o1[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const uint64_t at = row0 + (uint64_t)min((uint32_t)i, nc - 1u) * step;
+    o0[i] = p.scratch[at + lane];
+    o1[i] = p.scratch[at + d1];
+  }
+  mi = live ? mi : -FLT_MAX;
+  li = live ? li : 0.0f;
   const float ms = wave_max(mi);
   wsh[lane] = exp2f(mi - ms);
   lsh[lane] = li;
   __syncthreads();
   float l = 0.0f;
-  for (uint32_t i = 0; i < p.num_chunks; ++i)
+  for (uint32_t i = 0; i < nc; ++i)
     l = fmaf(lsh[i], wsh[i], l);
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  for (uint32_t d = lane; d < p.dh; d += 64) {
-    float num = 0.0f;
-#pragma unroll 8
-    for (uint32_t i = 0; i < p.num_chunks; ++i)
-      num = fmaf(p.scratch[row0 + i * step + d], wsh[i], num);
-    p.out[(uint64_t)row_id * p.dh + d] = num * inv;
+  float n0 = 0.0f, n1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    if ((uint32_t)i < nc) {
+      n0 = fmaf(o0[i], wsh[i], n0);
+      n1 = fmaf(o1[i], wsh[i], n1);
+    }
   }
+  p.out[(uint64_t)row_id * p.dh + lane] = n0 * inv;
+  if (lane + 64u < p.dh)
+    p.out[(uint64_t)row_id * p.dh + lane + 64u] = n1 * inv;
 }
