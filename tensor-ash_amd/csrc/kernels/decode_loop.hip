@@ -115,16 +115,15 @@ template <int DH, bool KV16> struct AttnDecode {
       }
     }
 
-    for (uint32_t blk = p0; blk < p1; blk += 64) {
+    // Stage one block: wave w loads K^T rows w * KPW .. (lane = position)
+    // and V rows w * VPW .. (lane = head dimension), all in one batch.
+    // Loads past the chunk end re-read an in-range element and are zeroed
+    // when staged, so no load is predicated.  The next block's loads are
+    // issued as soon as this one is in LDS, so they run under its compute.
+    float kl[KPW], vl[VPW][DPL];
+    auto load_block = [&](uint32_t blk) {
       const uint32_t pos = blk + lane;
-      const bool valid = pos < p1;
-      // Stage the block: wave w loads K^T rows w * KPW .. (lane = position)
-      // and V rows w * VPW .. (lane = head dimension), all in one batch;
-      // positions past the chunk end are never read (zeros are staged).
-      // (Loads past the end re-read an in-range element, zeroed after the
-      // load, so no load is predicated.)
-      float kl[KPW], vl[VPW][DPL];
-      const uint32_t kpos = valid ? pos : blk;
+      const uint32_t kpos = pos < p1 ? pos : blk;
 #pragma unroll
       for (int u = 0; u < KPW; ++u)
         kl[u] = load_kv<KV16>(p.kt, kt_base + (uint64_t)(wave * KPW + u) * p.t_max + kpos);
@@ -135,24 +134,24 @@ template <int DH, bool KV16> struct AttnDecode {
         for (int c = 0; c < DPL; ++c)
           vl[u][c] = load_kv<KV16>(p.v, v_base + (uint64_t)row * DH + lane + 64 * c);
       }
-#pragma unroll
-      for (int u = 0; u < KPW; ++u)
-        kl[u] = valid ? kl[u] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < VPW; ++u)
-#pragma unroll
-        for (int c = 0; c < DPL; ++c)
-          vl[u][c] = blk + wave * VPW + u < p1 ? vl[u][c] : 0.0f;
+    };
+    if (p0 < p1)
+      load_block(p0);
+    for (uint32_t blk = p0; blk < p1; blk += 64) {
+      const uint32_t pos = blk + lane;
+      const bool valid = pos < p1;
       __syncthreads(); // the previous block's reads are done
 #pragma unroll
       for (int u = 0; u < KPW; ++u)
-        sm.k[wave * KPW + u][lane] = kl[u];
+        sm.k[wave * KPW + u][lane] = valid ? kl[u] : 0.0f;
 #pragma unroll
       for (int u = 0; u < VPW; ++u)
 #pragma unroll
         for (int c = 0; c < DPL; ++c)
-          sm.v[wave * VPW + u][lane + 64 * c] = vl[u][c];
+          sm.v[wave * VPW + u][lane + 64 * c] = blk + wave * VPW + u < p1 ? vl[u][c] : 0.0f;
       __syncthreads();
+      if (blk + 64 < p1)
+        load_block(blk + 64);
       if (!rows)
         continue;
       // Scores of this lane's position: q[r][d] from lane d % 64 of its
