@@ -47,6 +47,33 @@ def test_packed_gemv(ta, ex, oracle, m, k, n):
     check_f16(ex.download(ty), oracle.cpu_bmm(x, wr, None, 1, m, n, k), k, oracle)
 
 
+@pytest.mark.parametrize("m", [4, 5, 8])
+def test_packed_gemv_matrix_core_row_scales(ta, ex, oracle, m):
+    """4-8 rows on 64-column tiles run on f16 MFMA with each X row scaled
+    by a power of two and split into three f16 pieces.  Rows of very
+    different magnitude (1e-20, 1, 1e20, 0) in one launch, with K ragged
+    against the 256-row load groups, must each stay f32-accurate: per-row
+    normwise rel err <= 1e-5 against the oracle on the same f16 weights
+    (f16 would give ~5e-4; f32 accumulation over K = 1000 ~1e-6)."""
+    k, n = 1000, 2048
+    tile = ta.f16w_row_tile_n(k, n)
+    assert tile == 64, f"expected 64-column tiles for {k}x{n}, got {tile}"
+    w, wr = f16_weights(oracle, k, n, 70 + m)
+    scales = np.array([1e-20, 1.0, 1e20, 0.0, 3.0, 1e-3, 7e5, 1.0][:m], np.float64)
+    x = (oracle.fill_det(m * k, 71).reshape(m, k) * scales[:, None]).astype(np.float32).reshape(-1)
+    tw = ex.tensor_from(ta.pack_f16w_row_tiles(w, k, n, tile), shape=[k, n], f16=True)
+    tx, ty = ex.tensor_from(x, shape=[m, k]), ex.tensor([m, n])
+    ex.run_ops([ta.MatmulOp(tx, tw, ty, packed_b=True)])
+    got = np.asarray(ex.download(ty), np.float64).reshape(m, n)
+    ref = np.asarray(oracle.cpu_bmm(x, wr, None, 1, m, n, k), np.float64).reshape(m, n)
+    for r in range(m):
+        if scales[r] == 0.0:
+            assert not got[r].any(), f"row {r}: zero input gave nonzero output"
+            continue
+        e = np.linalg.norm(got[r] - ref[r]) / np.linalg.norm(ref[r])
+        assert e <= 1e-5, f"row {r} (scale {scales[r]:g}): rel err {e}"
+
+
 @pytest.mark.parametrize("m", [1, 4, 8])
 @pytest.mark.parametrize("epi", [dict(bias=True, act=2), dict(act=3, binary=1, beta=1.0),
                                  dict(binary=2), dict(alpha=0.5, accumulate=True)])
