@@ -654,7 +654,9 @@ struct Gemv {
       const uint32_t off = ((((kk >> 6) * 16u + (kk & 15u)) * MR + m) * 4u) + ((kk >> 4) & 3u);
       const float v = xr[j] * s;
       const _Float16 h = (_Float16)v;
-      const float r = v - (float)h;
+      // An infinite x keeps hi = inf and zero residuals, so the output is
+      // +-inf (or NaN against a zero weight) as with f32 FMAs.
+      const float r = __builtin_isinf((float)h) ? 0.0f : v - (float)h;
       const _Float16 md = (_Float16)r;
       xa[off] = h;
       xa[XROWS * MR + off] = md;
