@@ -176,7 +176,7 @@ def _mlp_layer_ops(ta, x, wts, up, h, y, res):
     ]
 
 
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 4, 6, 8])
 def test_decode_mlp_chain(ta, ex, oracle, m, monkeypatch):
     """Three config-3 decode layers in one op graph (layer l+1 reads layer
     l's y as x and as residual) run as one persistent MLP-chain launch.
