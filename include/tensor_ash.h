@@ -217,6 +217,24 @@ int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a,
                        const ta_tensor *b, const ta_tensor *c, float alpha,
                        uint32_t splits, ta_run_stats *stats);
 
+/* No counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): ta_matmul_split_k2 with the same
+ * kernels and bit-identical results, but its partial planes live in a
+ * fixed per-device array of TA_NOALLOC_SCRATCH_BYTES that the library
+ * holds until the process ends, so the call allocates nothing.  Fails
+ * (-1, ta_last_error) when the planes would exceed that size: batch * M *
+ * N * splits * sub-windows * 4 bytes, where the library adds sub-windows
+ * to fill the device (64x256 and 32x128 outputs use 16 MiB and 4 MiB at
+ * any split count).  Calls on one device share the array; the library
+ * serialises them within a process, and the array keeps the last call's
+ * partials. */
+#define TA_NOALLOC_SCRATCH_BYTES (32u << 20)
+int ta_matmul_split_k2_noalloc(const ta_executor *exec, const ta_tensor *a,
+                               const ta_tensor *b, const ta_tensor *c,
+                               float alpha, uint32_t splits,
+                               ta_run_stats *stats);
+
 /* MatmulOp::with_packed_b (src/matmul/api.rs:260-265): B holds the packed
  * decode layout produced by ta_pack_f16w_row_tiles with
  * ta_f16w_row_tile_n(K, N).  Packed ops take M <= 8, batch 1, f16 B. */

@@ -65,10 +65,20 @@ def build_host(jobs: int = 4) -> Path:
     srcs = sorted((CSRC / "runtime").glob("*.cpp"))
     objs = [obj_dir / (s.stem + ".o") for s in srcs]
     cxx = shutil.which("g++") or "g++"
+    # runtime/*.hip hold device data of the library itself (the fixed
+    # scratch array): compiled by hipcc into objects with an embedded
+    # gfx950 fat binary, linked like the host objects.
+    dev_srcs = sorted((CSRC / "runtime").glob("*.hip"))
+    dev_objs = [obj_dir / (s.stem + ".hip.o") for s in dev_srcs]
+    dev_flags = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+                 "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         futs = [pool.submit(_run, [cxx, *HOST_FLAGS, "-c", str(s), "-o", str(o)]) for s, o in zip(srcs, objs)]
+        futs += [pool.submit(_run, [HIPCC, *dev_flags, "-c", str(s), "-o", str(o)])
+                 for s, o in zip(dev_srcs, dev_objs)]
         for f in futs:
             f.result()
+    objs += dev_objs
     LIB.mkdir(exist_ok=True)
     so = LIB / "libtensor_ash.so"
     _run([cxx, "-shared", "-o", str(so), *map(str, objs), f"-L{ROCM / 'lib'}",

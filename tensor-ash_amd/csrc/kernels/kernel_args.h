@@ -20,6 +20,11 @@ enum {
   TA_GEMV_PACKED = 1u << 2,     // GEMV weights in the [N/TW][K][TW] layout
 };
 
+// Bytes of the fixed device scratch that the allocation-free split-K
+// entry point keeps its partial planes in (one array per device, held
+// until the process ends).  Config 4's largest plane set is 16 MiB.
+#define TA_NOALLOC_SCRATCH_BYTES (32u << 20)
+
 // Activation codes (shaders/matmul_epilogue_common.glsl:24-26 numbering).
 enum { TA_ACT_NONE = 0, TA_ACT_RELU = 1, TA_ACT_SILU = 2, TA_ACT_GELU = 3 };
 // Binary codes: 1 = += beta * D, 2 = *= D.

@@ -430,6 +430,17 @@ int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a, const ta_ten
   });
 }
 
+int ta_matmul_split_k2_noalloc(const ta_executor *exec, const ta_tensor *a, const ta_tensor *b,
+                               const ta_tensor *c, float alpha, uint32_t splits,
+                               ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_matmul_split_k2_noalloc: exec is null");
+    ta_matmul_call raw{a, b, c, alpha, 0};
+    write_stats(stats, e.exec->run_matmuls_split_k2_noalloc(
+                           checked_call(e, raw, "ta_matmul_split_k2_noalloc"), splits));
+  });
+}
+
 namespace {
 FlashAttentionDesc flash_desc(const ta_flash_desc &d, const std::string &fn) {
   if (d.reserved)

@@ -788,14 +788,20 @@ struct ExecutorImpl {
     ScratchNeed need = total_need(res, plans);
     slot->scratch.ensure(need.splitk, need.partial, need.counters);
     slot->scratch.ensure_mlp(need.mlp);
+    return submit_on(slot, ops, res, plans, slot->scratch);
+  }
+  // Submit with the given scratch, which already holds what the plans need.
+  uint64_t submit_on(Slot *slot, const std::vector<MatmulOp> &ops,
+                     const std::vector<ResolvedMatmul> &res, const std::vector<OpPlan> &plans,
+                     Scratch &scratch) const {
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
-    record(ops, res, plans, slot->scratch, slot->host_status, slot->stream);
+    record(ops, res, plans, scratch, slot->host_status, slot->stream);
     hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
     hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
     float ms = 0.f;
     hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
     if (has_mlp(plans))
-      check_host_status(slot->host_status, slot->scratch.mlp, slot->scratch.mlp_bytes);
+      check_host_status(slot->host_status, scratch.mlp, scratch.mlp_bytes);
     return (uint64_t)((double)ms * 1e6);
   }
 
@@ -1103,12 +1109,13 @@ struct ExecutorImpl {
   }
 
   // ---- split-K (src/executor/reduction.rs:21-70) ----
-  RunStats run_split_k2(const MatmulCall &call, uint32_t num_k_splits) {
-    ctx->make_current();
+  // Validates the call and resolves the split count (0 = default).
+  uint32_t split_k2_splits(const MatmulCall &call, uint32_t num_k_splits,
+                           ResolvedMatmul &d) const {
     validate_call(call);
     if (call.accumulate)
       fail("run_matmuls_split_k2: accumulate=true is not supported");
-    ResolvedMatmul d = ResolvedMatmul::from_call(call);
+    d = ResolvedMatmul::from_call(call);
     if (num_k_splits > 0xFFFF)
       fail("run_matmuls_split_k2: num_k_splits=" + std::to_string(num_k_splits) +
            " out of range [1, 65535]");
@@ -1120,17 +1127,59 @@ struct ExecutorImpl {
     const uint32_t splits =
         num_k_splits == 0 ? default_num_k_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k)
                           : num_k_splits;
+    if (splits > 1) {
+      validate_scratch_geometry(d.batch, d.m, d.n, d.k, splits);
+      if ((uint64_t)d.batch * splits > 65535)
+        fail("split-K2 dispatch grid Z (" + std::to_string((uint64_t)d.batch * splits) +
+             ") exceeds 65535");
+    }
+    return splits;
+  }
+
+  RunStats run_split_k2(const MatmulCall &call, uint32_t num_k_splits) {
+    ctx->make_current();
+    ResolvedMatmul d;
+    const uint32_t splits = split_k2_splits(call, num_k_splits, d);
     if (splits <= 1)
       return run_ops_impl({MatmulOp(call)}, false);
-    validate_scratch_geometry(d.batch, d.m, d.n, d.k, splits);
-    if ((uint64_t)d.batch * splits > 65535)
-      fail("split-K2 dispatch grid Z (" + std::to_string((uint64_t)d.batch * splits) +
-           ") exceeds 65535");
     OpPlan p;
     p.kernel = registry_index(splitk_stage1_spec(d.m, d.n).name);
     p.splitk2 = splits;
     Lease lease(this);
     const uint64_t ns = submit_and_wait(lease.s, {MatmulOp(call)}, {d}, {p});
+    return RunStats{ns, 1, d.total_flops};
+  }
+
+  // The same two launches with the partial planes in the device's fixed
+  // scratch array instead of slot memory: nothing is allocated, on the
+  // device or pinned.  A single split runs the stage-1 kernel straight
+  // into C (no scratch).  Calls on one device are serialised here, from
+  // the first launch until the stream has drained, because they share
+  // the array; the planes need no clearing (every element is stored
+  // before the reduce reads it).
+  RunStats run_split_k2_noalloc(const MatmulCall &call, uint32_t num_k_splits) {
+    ctx->make_current();
+    ResolvedMatmul d;
+    const uint32_t splits = split_k2_splits(call, num_k_splits, d);
+    OpPlan p;
+    p.kernel = registry_index(splitk_stage1_spec(d.m, d.n).name);
+    if (splits > 1)
+      p.splitk2 = splits;
+    const uint64_t need = scratch_need(d, p).splitk;
+    if (need > TA_NOALLOC_SCRATCH_BYTES)
+      fail("run_matmuls_split_k2_noalloc: partial planes need " + std::to_string(need) +
+           " bytes (B=" + std::to_string(d.batch) + " " + std::to_string(d.m) + "x" +
+           std::to_string(d.n) + ", " + std::to_string(splits) +
+           " splits) > the fixed scratch of " + std::to_string(TA_NOALLOC_SCRATCH_BYTES) +
+           " bytes");
+    void *base = nullptr;
+    hip_check(fixed_scratch_address(ctx->device(), &base), "hipGetSymbolAddress (fixed scratch)");
+    Scratch fixed;
+    fixed.splitk = base;
+    fixed.splitk_bytes = TA_NOALLOC_SCRATCH_BYTES;
+    std::lock_guard<std::mutex> serial(fixed_scratch_mutex(ctx->device()));
+    Lease lease(this);
+    const uint64_t ns = submit_on(lease.s, {MatmulOp(call)}, {d}, {p}, fixed);
     return RunStats{ns, 1, d.total_flops};
   }
 
@@ -1306,6 +1355,11 @@ RunStats Executor::run_gemv_chain(const std::vector<MatmulOp> &jobs) const {
 
 RunStats Executor::run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const {
   return impl_->run_split_k2(call, num_k_splits);
+}
+
+RunStats Executor::run_matmuls_split_k2_noalloc(const MatmulCall &call,
+                                                uint32_t num_k_splits) const {
+  return impl_->run_split_k2_noalloc(call, num_k_splits);
 }
 
 // ---- model ops (src/executor/elementwise/ops.rs) ----

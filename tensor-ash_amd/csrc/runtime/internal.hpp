@@ -108,4 +108,10 @@ std::string tune_header_line(const Context &ctx);
 std::map<TuneKey, TuneEntry> parse_tune_store(const std::string &text, const std::string &header);
 std::string format_tune_store(const std::map<TuneKey, TuneEntry> &map, const std::string &header);
 
+// Fixed device scratch (fixed_scratch.hip): the array's address on
+// `device` (the current device), resolved once per device, and the mutex
+// that serialises its users on that device.
+hipError_t fixed_scratch_address(int device, void **out);
+std::mutex &fixed_scratch_mutex(int device);
+
 } // namespace tensor_ash

@@ -585,6 +585,10 @@ public:
   // earlier jobs' writes) on the decode GEMV launches.
   RunStats run_gemv_chain(const std::vector<MatmulOp> &jobs) const;
   RunStats run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const;
+  // run_matmuls_split_k2 without allocating: partial planes live in a
+  // fixed per-device array of TA_NOALLOC_SCRATCH_BYTES (no reference
+  // counterpart; for callers that cannot allocate device memory).
+  RunStats run_matmuls_split_k2_noalloc(const MatmulCall &call, uint32_t num_k_splits) const;
 
   // Model ops (src/executor/elementwise/ops.rs); in-place (input ==
   // output) is allowed except for the copy.

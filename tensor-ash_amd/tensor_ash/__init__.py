@@ -150,6 +150,7 @@ _sig("ta_run_op_graph", C.c_int, P, C.POINTER(_Op), sz, C.POINTER(RunStats))
 _sig("ta_run_ops_v2", C.c_int, P, C.POINTER(_OpV2), sz, C.POINTER(RunStats))
 _sig("ta_run_op_graph_v2", C.c_int, P, C.POINTER(_OpV2), sz, C.POINTER(RunStats))
 _sig("ta_matmul_split_k2", C.c_int, P, P, P, P, f32, u32, C.POINTER(RunStats))
+_sig("ta_matmul_split_k2_noalloc", C.c_int, P, P, P, P, f32, u32, C.POINTER(RunStats))
 _sig("ta_prepared_create", P, P, C.POINTER(_Op), sz, u32)
 _sig("ta_prepared_create_v2", P, P, C.POINTER(_OpV2), sz, u32)
 _sig("ta_run_ops_v3", C.c_int, P, C.POINTER(_OpV3), sz, C.POINTER(RunStats))
@@ -756,6 +757,15 @@ class Executor:
     def run_matmuls_split_k2(self, a: Tensor, b: Tensor, c: Tensor, splits: int, alpha: float = 1.0) -> RunStats:
         st = RunStats()
         _check(_lib.ta_matmul_split_k2(self._h, a.handle, b.handle, c.handle, alpha, splits, C.byref(st)))
+        return st
+
+    def run_matmuls_split_k2_noalloc(self, a: Tensor, b: Tensor, c: Tensor, splits: int,
+                                     alpha: float = 1.0) -> RunStats:
+        """run_matmuls_split_k2 with the partial planes in the library's fixed
+        per-device scratch (no device allocation; raises when they do not fit)."""
+        st = RunStats()
+        _check(_lib.ta_matmul_split_k2_noalloc(self._h, a.handle, b.handle, c.handle, alpha, splits,
+                                               C.byref(st)))
         return st
 
     def prepare_ops(self, ops: Sequence[MatmulOp]) -> Prepared:

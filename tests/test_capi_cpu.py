@@ -46,6 +46,8 @@ def test_null_op_entry_points(ta):
     assert L.ta_matmul(None, None, None, None, 1.0, 0, None) == -1 and "ta_matmul: exec is null" in last(ta)
     assert L.ta_matmul_split_k2(None, None, None, None, 1.0, 4, None) == -1
     assert "ta_matmul_split_k2: exec is null" in last(ta)
+    assert L.ta_matmul_split_k2_noalloc(None, None, None, None, 1.0, 4, None) == -1
+    assert "ta_matmul_split_k2_noalloc: exec is null" in last(ta)
 
 
 def test_null_elementwise_and_diagnostics(ta):
