@@ -168,9 +168,8 @@ int ta_run_ops(const ta_executor *exec, const ta_matmul_op *ops, size_t n_ops,
 int ta_run_op_graph(const ta_executor *exec, const ta_matmul_op *ops,
                     size_t n_ops, ta_run_stats *stats);
 
-/* ref tensor_ash.h:172-208: model ops.  Outside this build's scope (the
- * fused-epilogue GEMM path): they validate exec and return -1 with an
- * "unsupported" error. */
+/* ref tensor_ash.h:172-208: model ops (src/executor/elementwise/ops.rs),
+ * with the reference's validations and error texts. */
 int ta_softmax_rows(const ta_executor *exec, const ta_tensor *input,
                     const ta_tensor *output, float scale, uint32_t mask_kind,
                     uint32_t valid_or_prefix, uint32_t rows_per_group,

@@ -37,8 +37,8 @@
 
 namespace {
 
-template <int DH> constexpr int flash_parts() { return DH == 64 ? 4 : 2; }   // KP
-template <int DH> constexpr int flash_qblocks() { return 2; }               // QB
+template <int DH> constexpr int flash_parts() { return ta_flash_parts(DH); }     // KP
+template <int DH> constexpr int flash_qblocks() { return ta_flash_qblocks(DH); } // QB
 constexpr float kNegMax = -3.402823466e38f;
 
 template <bool F16> TA_DEVICE f32x4 load4(const void *base, uint64_t i) {

@@ -328,7 +328,8 @@ TA_ATTN_DECODE(ta_attn_decode_kv16_dh128, 128, true)
 // merge costs one memory round trip.  The chunk weights go to LDS; the
 // normaliser and each output sum over the chunks in chunk order.
 extern "C" __global__ __launch_bounds__(64) void ta_attn_decode_combine(AttnCombineArgs p) {
-  constexpr int MAXC = 32; // TA_ATTN_DECODE_MAX_CHUNKS
+  constexpr int MAXC = TA_ATTN_DECODE_MAX_CHUNKS;
+  static_assert(MAXC <= 64, "one chunk weight per lane of the wave");
   __shared__ float wsh[64], lsh[64];
   const uint32_t row_id = blockIdx.x, lane = threadIdx.x;
   const uint32_t kvh = row_id / p.group, r = row_id % p.group;

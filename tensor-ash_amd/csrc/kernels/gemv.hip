@@ -40,13 +40,6 @@
 // Y = act(alpha * X @ W + bias) * U to y.
 #include "common.h"
 
-// Compile-time phase-timing hook for offline analysis; expands to nothing
-// in the library build.
-#ifndef TA_GEMV_TRACE
-#define TA_GEMV_TRACE(point)
-#define TA_GEMV_TRACE_ROLE(role)
-#endif
-
 // Row counts from which the matrix-core route and the hand-off sentinel
 // pre-poll apply (compile-time, for measurement builds).
 #ifndef TA_GEMV_MFMA_MIN_ROWS
@@ -97,12 +90,13 @@ TA_DEVICE void store_word(uint64_t *p, uint64_t v) {
 // Every thread reads N tagged words (address at(j), needed when need(j));
 // the workgroup re-reads them all until every needed word of every thread
 // carries `tag`, sleeping ~0.05 us between rounds.  out[] holds the values
-// of the last round.  Bounded: after spin_limit rounds the wait gives up
-// and raises the host-visible status word (the launch's results are then
-// invalid).
+// of the last round.  Bounded: after spin_limit rounds in all (`polls`
+// counts rounds a pre-poll already spent) the wait gives up and raises the
+// host-visible status word (the launch's results are then invalid).
 template <int N, class At, class Need>
-TA_DEVICE void poll_words(At at, Need need, uint32_t tag, float (&out)[N], const MlpArgs &m) {
-  for (uint32_t polls = 0;;) {
+TA_DEVICE void poll_words(At at, Need need, uint32_t tag, float (&out)[N], const MlpArgs &m,
+                          uint32_t polls = 0) {
+  for (;;) {
     uint64_t w[N];
 #pragma unroll
     for (int j = 0; j < N; ++j)
@@ -133,16 +127,19 @@ TA_DEVICE void poll_words(At at, Need need, uint32_t tag, float (&out)[N], const
 // their tags checked as before (poll_words), so a sentinel seen early
 // costs another round, never a wrong value.  Used from M = 4 up: with
 // fewer rows the window's words are few enough that the extra round trip
-// costs more than the re-reads it saves.  Bounded like poll_words; on the
-// limit the word poll that follows raises the status word.
-TA_DEVICE void poll_sentinels(const uint64_t *words, uint32_t first_tile, uint32_t ntiles,
-                              uint32_t mr, uint32_t row, uint32_t tag, const MlpArgs &m) {
+// costs more than the re-reads it saves.  Returns the rounds it spent, which
+// the word poll that follows counts against the same spin_limit (so a lost
+// hand-off is reported after one bound, not two).
+TA_DEVICE uint32_t poll_sentinels(const uint64_t *words, uint32_t first_tile, uint32_t ntiles,
+                                  uint32_t mr, uint32_t row, uint32_t tag, const MlpArgs &m) {
   const uint32_t tid = threadIdx.x;
   const uint64_t *f = words + ((uint64_t)(first_tile + tid) * 64u + 63u) * mr + row;
   for (uint32_t polls = 0;;) {
     const bool ok = tid >= ntiles || (uint32_t)(load_word(f) >> 32) == tag;
-    if (__syncthreads_and(ok) || ++polls >= m.spin_limit)
-      return;
+    if (__syncthreads_and(ok))
+      return polls;
+    if (++polls >= m.spin_limit)
+      return polls - 1u; // the word poll still takes its one round
     __builtin_amdgcn_s_sleep(2);
   }
 }
@@ -214,7 +211,6 @@ struct Gemv {
     uint32_t tag = 0;
     if constexpr (MODE != kStandalone)
       tag = __hip_atomic_load(mlp->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + layer + 1u;
-    TA_GEMV_TRACE(0);
 
     const uint32_t cp = lane % LPR, r0 = lane / LPR;
     // Lanes past N (row-major, ragged last tile) read column 0 of the tile
@@ -283,8 +279,10 @@ struct Gemv {
       // words of the window ([k][MR] order) until all carry this launch's
       // tag; vmcnt retires in order, so the first poll lands after them.
       issue(0, cur);
+      uint32_t spent = 0;
       if constexpr (MR >= TA_GEMV_SENTINEL_MIN_ROWS)
-        poll_sentinels(mlp->tag_h, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag, *mlp);
+        spent = poll_sentinels(mlp->tag_h, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag,
+                               *mlp);
       poll_words<XPT>(
           [&](int j) {
             bool ok;
@@ -297,7 +295,7 @@ struct Gemv {
             (void)x_index(j, ok);
             return ok;
           },
-          tag, xr, *mlp);
+          tag, xr, *mlp, spent);
 #pragma unroll
       for (int j = 0; j < XPT; ++j) {
         bool ok;
@@ -308,8 +306,10 @@ struct Gemv {
       // Chained layer: weights first, then X = the previous layer's y from
       // its tagged words ([k][MR] order, the previous layer's tag).
       issue(0, cur);
+      uint32_t spent = 0;
       if constexpr (MR >= TA_GEMV_SENTINEL_MIN_ROWS)
-        poll_sentinels(mlp->tag_y, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag - 1u, *mlp);
+        spent = poll_sentinels(mlp->tag_y, k0 / 64u, (kend - k0) / 64u, MR, p.rows - 1u, tag - 1u,
+                               *mlp);
       poll_words<XPT>(
           [&](int j) {
             bool ok;
@@ -322,7 +322,7 @@ struct Gemv {
             (void)x_index(j, ok);
             return ok;
           },
-          tag - 1u, xr, *mlp);
+          tag - 1u, xr, *mlp, spent);
 #pragma unroll
       for (int j = 0; j < XPT; ++j) {
         bool ok;
@@ -353,7 +353,6 @@ struct Gemv {
         sm.xs[tid + j * kThreads] = xr[j];
     }
     __syncthreads();
-    TA_GEMV_TRACE(1);
 
     float acc[WAYS][MR][CPL];
 #pragma unroll
@@ -482,7 +481,6 @@ struct Gemv {
         consume(kb, cur);
       }
     }
-    TA_GEMV_TRACE(2);
 
     if constexpr (MF) {
       // D rows 4*(lane/16)+i below MR, unscaled by the row's power of two.
@@ -558,7 +556,6 @@ struct Gemv {
           if (o < OUTS)
             store_word(mine + o, tag_word(part[i], tag));
         }
-        TA_GEMV_TRACE(3);
         return;
       }
       if (p.kchunks > 1) {
@@ -596,7 +593,6 @@ struct Gemv {
         for (int i = 0; i < OPT; ++i)
           part[i] = sum[i] + part[i];
       }
-      TA_GEMV_TRACE(5);
       epilogue(p, tile, part, sm, MODE == kProducer ? mlp->tag_h : mlp->tag_y, tag);
       if constexpr (MODE == kConsumer) {
         // The last down tile of the last layer advances the generation past
@@ -627,10 +623,13 @@ struct Gemv {
     constexpr int XPT = XROWS * MR / kThreads;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t m = tid % MR;
+    // Row scale from the finite values only: an infinite x must not push
+    // the row's finite values past the f16 range (their hi pieces would
+    // turn into +-inf and the column sums into inf - inf = NaN).
     float mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < XPT; ++j)
-      mx = fmaxf(mx, fabsf(xr[j]));
+      mx = __builtin_isfinite(xr[j]) ? fmaxf(mx, fabsf(xr[j])) : mx;
 #pragma unroll
     for (int off = MR; off < 64; off <<= 1)
       mx = fmaxf(mx, __shfl_xor(mx, off));
@@ -763,14 +762,12 @@ struct Gemv {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    TA_GEMV_TRACE(3);
     if (tid == 0) {
       const uint32_t seen =
           __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       sm.last_flag = (seen == p.kchunks - 1) ? 1u : 0u;
     }
     __syncthreads();
-    TA_GEMV_TRACE(4);
     if (!sm.last_flag)
       return false;
     // Sum the windows in order 0..kchunks-1.  A batch of NB windows is
@@ -935,7 +932,6 @@ template <int MR> struct DecodeMlp {
     __shared__ __attribute__((aligned(16))) Smem sm;
     const uint32_t per_layer = p.units_a + p.units_b;
     const uint32_t layer = blockIdx.x / per_layer, r = blockIdx.x % per_layer;
-    TA_GEMV_TRACE_ROLE(blockIdx.x);
     if (r < p.units_a)
       A::unit(p.layer[layer].a, r % p.tiles_a, r / p.tiles_a, sm.a, &p, layer);
     else

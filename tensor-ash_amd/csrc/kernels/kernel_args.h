@@ -25,6 +25,11 @@ enum {
 // until the process ends).  Config 4's largest plane set is 16 MiB.
 #define TA_NOALLOC_SCRATCH_BYTES (32u << 20)
 
+// Most chunks a split-K decode-attention launch uses per kv head: stage 2
+// (ta_attn_decode_combine) keeps one register slot per chunk and one LDS
+// weight per lane, so the cap must stay <= 64 (the wave width).
+#define TA_ATTN_DECODE_MAX_CHUNKS 32
+
 // Activation codes (shaders/matmul_epilogue_common.glsl:24-26 numbering).
 enum { TA_ACT_NONE = 0, TA_ACT_RELU = 1, TA_ACT_SILU = 2, TA_ACT_GELU = 3 };
 // Binary codes: 1 = += beta * D, 2 = *= D.
@@ -339,4 +344,15 @@ typedef struct MlpArgs {
 
 #ifdef __cplusplus
 }
+#endif
+
+#ifdef __cplusplus
+// Work split of the causal prefill attention kernels, shared with the host
+// launch (threads = 64 * QB * KP, query tiles of 32 * QB rows).
+//   KP: key parts per query block (head dim 64: 4, head dim 128: 2)
+//   QB: 32-row query blocks per workgroup
+constexpr int ta_flash_parts(int dh) { return dh == 64 ? 4 : 2; }
+constexpr int ta_flash_qblocks(int /*dh*/) { return 2; }
+constexpr int ta_flash_threads(int dh) { return 64 * ta_flash_qblocks(dh) * ta_flash_parts(dh); }
+constexpr int ta_flash_rows(int dh) { return 32 * ta_flash_qblocks(dh); }
 #endif

@@ -1659,7 +1659,8 @@ ElemLaunch plan_flash(ExecutorImpl &e, const Tensor &q, const Tensor &kt, const 
   a.o_head_stride = o_hs;
   a.o_row_stride = o_rs;
   a.heads = heads;
-  a.q_tiles = (t_q + 63) / 64; // query rows per workgroup: the kernel's 32 * QB
+  const uint32_t rows = ta_flash_rows((int)dh); // query rows per workgroup
+  a.q_tiles = (t_q + rows - 1) / rows;
   const uint64_t groups = (uint64_t)a.q_tiles * heads;
   if (groups == 0 || groups > UINT32_MAX)
     fail(op + ": empty or oversized launch (T_q " + std::to_string(t_q) + ", H " +
@@ -1670,7 +1671,7 @@ ElemLaunch plan_flash(ExecutorImpl &e, const Tensor &q, const Tensor &kt, const 
                                       : "ta_flash_attention_kv16_dh128")
                           : (dh == 64 ? "ta_flash_attention_dh64" : "ta_flash_attention_dh128");
   ElemLaunch l = elem(sym, (uint32_t)groups, a);
-  l.threads = dh == 64 ? 512 : 256; // QB query blocks x KP key parts: 2 x 4 at dh 64, 2 x 2 at 128
+  l.threads = (uint32_t)ta_flash_threads((int)dh); // QB query blocks x KP key parts, 64 lanes each
   return l;
 }
 
@@ -1882,6 +1883,8 @@ ElemLaunch plan_prefill_qkv_pack(ExecutorImpl &e, const Tensor &qkv, const Tenso
 // Decode-attention chunk count (elementwise/mod.rs:233-241): about 64
 // positions (one wave block) per chunk, at least 8 and at most
 // kAttnDecodeMaxChunks chunks; position-driven launches always use the cap.
+static_assert(kAttnDecodeMaxChunks == TA_ATTN_DECODE_MAX_CHUNKS,
+              "the combine kernel's chunk slots and the host cap must agree");
 uint32_t attn_decode_num_chunks(uint32_t kv_len) {
   return std::min(kAttnDecodeMaxChunks, std::max(8u, (kv_len + 63) / 64));
 }
@@ -1930,6 +1933,9 @@ ElemLaunches plan_attn_decode(ExecutorImpl &e, const Tensor &q, const Tensor &kt
          std::to_string(t_max));
   const uint32_t num_chunks =
       desc.pos_addr ? kAttnDecodeMaxChunks : attn_decode_num_chunks(desc.kv_len);
+  if (num_chunks == 0 || num_chunks > TA_ATTN_DECODE_MAX_CHUNKS)
+    fail(op + ": internal: " + std::to_string(num_chunks) + " chunks outside 1..=" +
+         std::to_string(TA_ATTN_DECODE_MAX_CHUNKS));
   const uint64_t needed = (uint64_t)kv_heads * num_chunks * group * (dh + 2);
   if (scratch.len() < needed)
     fail(op + ": scratch length " + std::to_string(scratch.len()) + " < required " +

@@ -73,15 +73,23 @@ def test_packed_gemv_matrix_core_row_scales(ta, ex, oracle, m):
         e = np.linalg.norm(got[r] - ref[r]) / np.linalg.norm(ref[r])
         assert e <= 1e-5, f"row {r} (scale {scales[r]:g}): rel err {e}"
     # an infinite X element gives +-inf (not NaN) where every weight of its
-    # column is nonzero, as with f32 FMAs
+    # column is nonzero, as with f32 FMAs -- also in a row whose finite
+    # values reach 7e5 (the row scale comes from the finite values only, so
+    # they do not overflow the f16 pieces)
     xi = x.reshape(m, k).copy()
-    xi[1, 5] = np.inf
+    inf_rows = [1] + ([6] if m > 6 else [])
+    for r in inf_rows:
+        xi[r, 5] = np.inf
     ex.upload(tx, xi.reshape(-1))
     ex.run_ops([ta.MatmulOp(tx, tw, ty, packed_b=True)])
     got = np.asarray(ex.download(ty), np.float32).reshape(m, n)
     want = np.where(wr.reshape(k, n)[5] > 0, np.inf, -np.inf)
     nz = wr.reshape(k, n)[5] != 0
-    np.testing.assert_array_equal(got[1][nz], want[nz])
+    for r in inf_rows:
+        np.testing.assert_array_equal(got[r][nz], want[nz])
+    for r in range(m):
+        if r not in inf_rows and scales[r] != 0.0:
+            assert np.all(np.isfinite(got[r])), f"row {r} without inf went non-finite"
 
 
 @pytest.mark.parametrize("m", [1, 4, 8])
