@@ -192,34 +192,56 @@ struct GemmH16 {
 
 // ---------------------------------------------------------------------
 // Pipelined f16 x f16 GEMM (both operands f16 in memory), the fast path
-// for K % BK == 0 and N % 8 == 0.  The f16w route gets its f16 A from
+// for K % 64 == 0 and N % 8 == 0.  The f16w route gets its f16 A from
 // ta_cvt_f32_f16 (RNE, the same rounding as staging-time conversion), the
-// a16 route reads its A directly.
+// a16 route reads its A directly.  Serves the plain tiles
+// (ta_gemm_{h16,a16}_<tile>_lds, k_splits = 1) and the split-K tiles
+// (ta_gemm_h16sk_<tile>).
 //
-//  * Global -> LDS with gfx950's direct loads (global_load_lds_dwordx4):
-//    no register staging; NS stages of BK k-values, NS - 1 of them in
-//    flight, one barrier per stage.  The loads are issued from inline asm
-//    with explicit vmcnt waits: the compiler would otherwise wait for every
-//    outstanding direct load before each LDS read, serialising the
-//    pipeline.
-//  * A stage: As[m][BK] f16, B stage: Bs[BK][BN] f16 exactly as B lies in
+//  * Two pipeline levels (DBUF; the 256 x 256 tile has room for two LDS
+//    stages only and runs the one-level loop).  Global -> LDS: gfx950's direct loads
+//    (global_load_lds_dwordx4, no register staging), NS stages of 64 k,
+//    one barrier per stage.  LDS -> registers: the MFMA fragments of stage
+//    kt + 1 are read into a second register set while the MFMAs of stage
+//    kt run, so a stage costs about max(MFMA chain, LDS reads + barrier)
+//    rather than their sum.  At iteration kt a wave waits until stage
+//    kt + 1 has landed (NS - 3 newer stages may still be in flight), joins
+//    the barrier, refills the buffer of stage kt - 1 (its fragments were
+//    consumed in iteration kt - 1) with stage kt + NS - 1, reads stage kt +
+//    1's fragments and runs stage kt's MFMAs.  The loads are issued from
+//    inline asm with explicit vmcnt waits: the compiler would otherwise
+//    wait for every outstanding direct load before each LDS read.
+//  * A stage: As[m][64] f16, B stage: Bs[64][BN] f16 exactly as B lies in
 //    memory (n contiguous).  A wave instruction writes 1 KiB of LDS
 //    contiguously (lane l at +16 l), so the bank-conflict swizzles are
 //    applied to which 16-byte global chunk a lane fetches: LDS slot c of
 //    row r holds global chunk c ^ swz(r).
 //  * Waves: WGM x WGN, each owning a WTM x WTN sub-tile of FM x FN MFMA
-//    blocks of 32x32.
+//    blocks of 32x32 (v_mfma_f32_32x32x16_f16).  8 waves (two per SIMD)
+//    for tiles of 128 x 64 and larger.
 //  * A operand: one ds_read_b128 per 32x32x16 MFMA (row, 8 k).  B operand:
 //    two ds_read_b64_tr_b16 (the CDNA4 LDS transpose read): in each group
 //    of 16 lanes, lane i receives element i % 4 of the 8-byte pieces the
 //    group's lanes 4j + i / 4 address (j = 0..3), so addressing row
 //    k0 + t / 4, columns nb + 4 (t % 4) from lane t hands lane i the
 //    column nb + i over rows k0..k0+3 - the MFMA's B layout, read from a
-//    row-major tile.  All reads of a stage are issued before its MFMAs.
+//    row-major tile.
 //  * Rows past M and column chunks past N read clamped (valid) addresses:
 //    their products only reach outputs the store guards drop.
-template <int BM, int BN, int BK, int WGM, int WGN, int NS, bool C_F16>
-struct GemmH16Lds {
+//  * Split-K (k_splits = S > 1, blockIdx.y = split s): split s takes K
+//    stages [lo, hi), lo = s * (steps / S) + min(s, steps % S) (the split
+//    window rule of the reference's split-K, in whole stages).  Every split
+//    stores its raw f32 accumulators to its slot of `partial` (lane-major,
+//    8-byte agent-scope stores, visible across the XCD L2s), waits for
+//    them, and increments the tile's counter.  The workgroup that brings
+//    the count to S sums the S partials in split order 0..S-1 (its own
+//    from registers, the others with agent-scope loads), so the result does
+//    not depend on which split finished last; then it runs the fused
+//    epilogue and clears the counter.  Nothing waits on another workgroup,
+//    so any residency order completes.  Used for deep K, where a tile's
+//    chain of stages is long and the grid small.
+template <int BM, int BN, int BK, int WGM, int WGN, int NS, bool C_F16, bool SPLIT, bool DBUF>
+struct GemmH16Pipe {
   static constexpr int T = 64 * WGM * WGN;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;
   static constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -230,12 +252,13 @@ struct GemmH16Lds {
   static constexpr int A_LD = A_BYTES / 16 / T, B_LD = B_BYTES / 16 / T;
   static constexpr int LD = A_LD + B_LD; // direct loads per thread per stage
   static_assert(A_LD * T * 16 == A_BYTES && B_LD * T * 16 == B_BYTES, "stages split evenly");
-  static_assert(CPA == 8 || CPA == 16, "BK is 64 or 128");
   static_assert(CPR >= 8, "B swizzle needs >= 8 chunks per row");
+  static_assert(BK == 32 || BK == 64, "A rows of 4 or 8 chunks");
   static_assert(FM >= 1 && FN >= 1, "wave tile must be a multiple of 32");
   static constexpr int SMEM_BYTES = NS * STAGE;
+  static_assert(SMEM_BYTES <= 160 * 1024 - 256, "LDS");
   static_assert(WGM * WGN * 32 * (WTN + 4) * 4 <= SMEM_BYTES, "C staging fits in LDS");
-  static_assert(NS >= 2 && (NS - 2) * LD <= 63, "vmcnt range");
+  static_assert(NS >= (DBUF ? 3 : 2) && (NS - 2) * LD <= 63, "vmcnt range");
 
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -249,8 +272,11 @@ struct GemmH16Lds {
   // per cycle on 4 consecutive rows x 2 or 4 chunks): row j of the four
   // is XORed with a pattern that separates the rows in chunk bits (b1,b2)
   // and in (b2,b3) - for 8-chunk rows, bit b2 together with the row parity.
+  // BK = 32 (4-chunk A rows, 4 rows per 256-byte bank line): the slot is
+  // c ^ (((row >> 1) ^ (row >> 3)) & 3), distinct in (row & 3, slot) over
+  // 16 consecutive rows and in (row & 1, slot) over 8.
   static TA_DEVICE uint32_t swz_a(uint32_t row) {
-    return CPA == 8 ? (row & 7u) ^ ((row >> 3) & 1u) : row & 15u;
+    return CPA == 8 ? (row & 7u) ^ ((row >> 3) & 1u) : ((row >> 1) ^ (row >> 3)) & 3u;
   }
   static TA_DEVICE uint32_t swz_b(uint32_t row) {
     return CPR >= 16 ? (0xACA60u >> (4u * (row & 3u))) & 15u : 2u * (row & 3u);
@@ -261,18 +287,58 @@ struct GemmH16Lds {
                  : "memory", "m0");
   }
 
+  struct Frags {
+    f16x8 a[KS][FM], b[KS][FN];
+  };
+
+  static TA_DEVICE void read_frags(uint32_t st, const uint32_t (&a_off)[KS][FM],
+                                   const uint32_t (&b_off)[KS][FN][2], Frags &f) {
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+        f.a[j][fm] = *(lds_f16x8 *)(uintptr_t)(st + a_off[j][fm]);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][0]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][1]));
+        f.b[j][fn] =
+            __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    }
+  }
+
+  static TA_DEVICE void mfmas(const Frags &f, f32x16 (&acc)[FM][FN]) {
+#pragma unroll
+    for (int j = 0; j < KS; ++j)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[j][fm], f.b[j][fn], acc[fm][fn],
+                                                               0, 0, 0);
+  }
+
   static TA_DEVICE void run(const GemmArgs &p) {
     __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
+    __shared__ uint32_t last_flag;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WGN, wn = wave % WGN;
     uint32_t tm, tn;
     ta_tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const uint32_t batch = blockIdx.z;
+    const uint32_t batch = blockIdx.z, split = blockIdx.y;
+    const uint32_t S = SPLIT && p.k_splits > 1 ? p.k_splits : 1u;
     const _Float16 *A = static_cast<const _Float16 *>(p.a) + (uint64_t)batch * p.stride_a;
     const _Float16 *B = static_cast<const _Float16 *>(p.b) + (uint64_t)batch * p.stride_b;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+
+    const uint32_t steps = p.k / BK, per = steps / S, extra = steps % S;
+    const uint32_t klo = split * per + min(split, extra);
+    const uint32_t kts = per + (split < extra ? 1u : 0u);
 
     // Per-thread source pointers of its direct loads (advanced per stage).
     const char *asrc[A_LD];
@@ -281,13 +347,13 @@ struct GemmH16Lds {
     for (int i = 0; i < A_LD; ++i) {
       const uint32_t q = i * T + tid, row = q / CPA, c = (q % CPA) ^ swz_a(row);
       const uint32_t gm = min(m0 + row, p.m - 1);
-      asrc[i] = reinterpret_cast<const char *>(A + (uint64_t)gm * p.k + 8 * c);
+      asrc[i] = reinterpret_cast<const char *>(A + (uint64_t)gm * p.k + (uint64_t)klo * BK + 8 * c);
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
       const uint32_t q = i * T + tid, row = q / CPR, c = (q % CPR) ^ swz_b(row);
       const uint32_t gn = min(n0 + 8 * c, p.n - 8);
-      bsrc[i] = reinterpret_cast<const char *>(B + (uint64_t)row * p.n + gn);
+      bsrc[i] = reinterpret_cast<const char *>(B + ((uint64_t)klo * BK + row) * p.n + gn);
     }
     const uint64_t b_step = (uint64_t)BK * p.n * 2;
 
@@ -338,47 +404,121 @@ struct GemmH16Lds {
         for (int r = 0; r < 16; ++r)
           acc[fm][fn][r] = 0.0f;
 
-    const uint32_t kts = p.k / BK;
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
       if (s < (int)kts)
         issue(s);
 
-    for (uint32_t kt = 0; kt < kts; ++kt) {
-      if (kt + NS - 2 < kts)
+    if constexpr (!DBUF) {
+      // One register set: wait for stage kt, barrier, refill, read, MFMAs
+      // (the 256 x 256 tile: two 64 KiB stages leave no room for a third).
+      for (uint32_t kt = 0; kt < kts; ++kt) {
+        if (kt + NS - 2 < kts)
+          asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * LD) : "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (kt + NS - 1 < kts)
+          issue((kt + NS - 1) % NS);
+        Frags f;
+        read_frags(lds0 + (kt % NS) * STAGE, a_off, b_off, f);
+        mfmas(f, acc);
+      }
+    } else {
+    Frags fr[2];
+    if (kts > 0) {
+      // stage 0 landed: min(NS - 2, kts - 1) newer stages may be in flight
+      if (kts >= NS - 1)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * LD) : "memory");
       else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      read_frags(lds0, a_off, b_off, fr[0]);
+    }
+    // Two iterations per trip so the register sets are fixed (no dynamic
+    // indexing of fr).
+    auto step = [&](uint32_t kt, Frags &cur, Frags &nxt) __attribute__((always_inline)) {
+      if (kt + 1 < kts) {
+        if (kt + NS - 2 < kts)
+          asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 3) * LD) : "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();
       if (kt + NS - 1 < kts)
         issue((kt + NS - 1) % NS);
-      const uint32_t st = lds0 + (kt % NS) * STAGE;
-      f16x8 a[KS][FM], b[KS][FN];
-#pragma unroll
-      for (int j = 0; j < KS; ++j) {
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-          a[j][fm] = *(lds_f16x8 *)(uintptr_t)(st + a_off[j][fm]);
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][0]));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][1]));
-          b[j][fn] = __builtin_bit_cast(
-              f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < KS; ++j)
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-          for (int fn = 0; fn < FN; ++fn)
-            acc[fm][fn] =
-                __builtin_amdgcn_mfma_f32_32x32x16_f16(a[j][fm], b[j][fn], acc[fm][fn], 0, 0, 0);
+      if (kt + 1 < kts)
+        read_frags(lds0 + ((kt + 1) % NS) * STAGE, a_off, b_off, nxt);
+      mfmas(cur, acc);
+    };
+    uint32_t kt = 0;
+    for (; kt + 1 < kts; kt += 2) {
+      step(kt, fr[0], fr[1]);
+      step(kt + 1, fr[1], fr[0]);
+    }
+    if (kt < kts)
+      step(kt, fr[0], fr[1]);
     }
     __syncthreads();
+
+    if (SPLIT && S > 1) {
+      const uint64_t tile_id = (uint64_t)batch * p.tiles_m * p.tiles_n + blockIdx.x;
+      uint64_t *slots = reinterpret_cast<uint64_t *>(p.partial) + tile_id * S * (BM * BN / 2);
+      uint64_t *mine = slots + (uint64_t)split * (BM * BN / 2);
+#pragma unroll
+      for (int f = 0; f < FM * FN; ++f)
+#pragma unroll
+        for (int r2 = 0; r2 < 8; ++r2) {
+          // Element values are copied out first: a bit cast of a vector
+          // element lvalue reads the vector's first element in this clang.
+          const float lo = acc[f / FN][f % FN][2 * r2], hi = acc[f / FN][f % FN][2 * r2 + 1];
+          const uint64_t w = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+          __hip_atomic_store(mine + (uint64_t)(f * 8 + r2) * T + tid, w, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      uint32_t *counter = p.counters + tile_id * TA_GEMV_COUNTER_STRIDE;
+      if (tid == 0)
+        last_flag =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+      __syncthreads();
+      if (!last_flag)
+        return;
+      // Fixed split order: acc = ((p0 + p1) + p2) + ...
+      f32x16 tot[FM][FN];
+      for (uint32_t j = 0; j < S; ++j) {
+        f32x16 src[FM][FN];
+        if (j == split) {
+#pragma unroll
+          for (int f = 0; f < FM * FN; ++f)
+            src[f / FN][f % FN] = acc[f / FN][f % FN];
+        } else {
+          const uint64_t *from = slots + (uint64_t)j * (BM * BN / 2);
+#pragma unroll
+          for (int f = 0; f < FM * FN; ++f)
+#pragma unroll
+            for (int r2 = 0; r2 < 8; ++r2) {
+              const uint64_t w =
+                  __hip_atomic_load(const_cast<uint64_t *>(from) + (uint64_t)(f * 8 + r2) * T + tid,
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              src[f / FN][f % FN][2 * r2] = __uint_as_float((uint32_t)w);
+              src[f / FN][f % FN][2 * r2 + 1] = __uint_as_float((uint32_t)(w >> 32));
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < FM * FN; ++f)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            tot[f / FN][f % FN][r] = j == 0 ? src[f / FN][f % FN][r]
+                                            : tot[f / FN][f % FN][r] + src[f / FN][f % FN][r];
+      }
+#pragma unroll
+      for (int f = 0; f < FM * FN; ++f)
+        acc[f / FN][f % FN] = tot[f / FN][f % FN];
+      if (tid == 0)
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     ta_store_tile<WTM, WTN, FM, FN, T, C_F16>(reinterpret_cast<float *>(smem), SMEM_BYTES / 4, acc,
                                               p, lane, wave, wm, wn, m0, n0, batch, 0);
   }
@@ -403,28 +543,36 @@ TA_GEMM_H16_FAMILY(m64n128, 64, 128, 2, 2)
 TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
 
 // Pipelined kernels: ta_gemm_h16_<tile>_lds (A pre-rounded to f16 by
-// ta_cvt_f32_f16, f32 C with the fused epilogue) and ta_gemm_a16_<tile>_lds
-// (f16 A, f16 C).
-#define TA_GEMM_LDS(TAG, BM, BN, BK, WGM, WGN, NS)                                        \
-  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void ta_gemm_h16_##TAG##_lds(   \
-      GemmArgs p) {                                                                       \
-    GemmH16Lds<BM, BN, BK, WGM, WGN, NS, false>::run(p);                                  \
-  }                                                                                       \
-  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void ta_gemm_a16_##TAG##_lds(   \
-      GemmArgs p) {                                                                       \
-    GemmH16Lds<BM, BN, BK, WGM, WGN, NS, true>::run(p);                                   \
+// ta_cvt_f32_f16, f32 C with the fused epilogue), ta_gemm_a16_<tile>_lds
+// (f16 A, f16 C) and the split-K ta_gemm_h16sk_<tile> (as h16, k_splits
+// workgroups per tile).
+#define TA_GEMM_PIPE(NAME, BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF)                      \
+  extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(GemmArgs p) {             \
+    static_assert(64 * WGM * WGN == ta_h16_lds_threads(BM, BN), "host launch width");         \
+    GemmH16Pipe<BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF>::run(p);                        \
   }
+#define TA_GEMM_LDS(TAG, BM, BN, BK, WGM, WGN, NS, DBUF)                                      \
+  TA_GEMM_PIPE(ta_gemm_h16_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, false, false, DBUF)         \
+  TA_GEMM_PIPE(ta_gemm_a16_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, true, false, DBUF)
+#define TA_GEMM_SK(TAG, BM, BN, BK, WGM, WGN, NS)                                             \
+  TA_GEMM_PIPE(ta_gemm_h16sk_##TAG, BM, BN, BK, WGM, WGN, NS, false, true, true)
 
-#ifndef TA_LDS_TILES
-TA_GEMM_LDS(m256n256, 256, 256, 64, 2, 4, 2)
-TA_GEMM_LDS(m128n128, 128, 128, 64, 2, 2, 3)
-TA_GEMM_LDS(m128n64, 128, 64, 64, 2, 2, 4)
-TA_GEMM_LDS(m64n128, 64, 128, 64, 2, 2, 4)
-TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4)
+// Stage counts and loop forms as measured fastest on the config-5 shapes
+// and 4096^3 (64 x 64: 11.9 us for 512x2048x2048; 128 x 64: 14.4 us for
+// 512x2560x2048; 128 x 128: 21.7 us for 512x5632x2048; split 128 x 64,
+// S = 2: 22.1 us for 512x2048x5632; 256 x 256: 110 us for 4096^3).
+#ifndef TA_PIPE_TILES
+TA_GEMM_LDS(m256n256, 256, 256, 64, 2, 4, 2, false)
+TA_GEMM_LDS(m128n128, 128, 128, 64, 2, 4, 4, true)
+TA_GEMM_LDS(m128n64, 128, 64, 64, 4, 2, 4, true)
+TA_GEMM_LDS(m64n128, 64, 128, 64, 2, 4, 4, true)
+TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4, true)
+TA_GEMM_SK(m64n128, 64, 128, 64, 2, 4, 4)
+TA_GEMM_SK(m128n64, 128, 64, 64, 4, 2, 4)
+TA_GEMM_SK(m128n128, 128, 128, 64, 2, 4, 4)
 #else
-TA_LDS_TILES
+TA_PIPE_TILES
 #endif
-
 // f32 -> f16 (RNE) of n elements, 8 per thread: the A pre-pass of the
 // pipelined f16w kernels.
 extern "C" __global__ __launch_bounds__(256) void ta_cvt_f32_f16(CvtArgs p) {

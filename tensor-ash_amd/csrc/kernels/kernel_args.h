@@ -65,7 +65,15 @@ typedef struct GemmArgs {
   // rule; plane (batch * num_splits + s * sub_splits + t) holds window t of
   // split s.
   uint32_t sub_splits;
-  uint32_t pad;
+  // In-kernel split-K (ta_gemm_h16sk_*): k_splits workgroups share each
+  // output tile, each over its K window (blockIdx.y = split); they store
+  // their f32 partial tiles to `partial` ((batch tile * k_splits + split)
+  // * BM * BN floats), count themselves in counters[batch tile *
+  // TA_GEMV_COUNTER_STRIDE], and the last to arrive sums the partials in
+  // split order, applies the epilogue and resets the counter to zero.
+  uint32_t k_splits;
+  float *partial;
+  uint32_t *counters;
 } GemmArgs;
 
 // Fixed-order reduction of split-K partial planes:
@@ -355,4 +363,9 @@ constexpr int ta_flash_parts(int dh) { return dh == 64 ? 4 : 2; }
 constexpr int ta_flash_qblocks(int /*dh*/) { return 2; }
 constexpr int ta_flash_threads(int dh) { return 64 * ta_flash_qblocks(dh) * ta_flash_parts(dh); }
 constexpr int ta_flash_rows(int dh) { return 32 * ta_flash_qblocks(dh); }
+
+// Threads of the pipelined f16-MFMA kernels (ta_gemm_{h16,a16}_<tile>_lds,
+// ta_gemm_h16sk_<tile>): 8 waves (two per SIMD) for tiles of 128 x 64 and
+// larger, 4 waves for 64 x 64.
+constexpr int ta_h16_lds_threads(int bm, int bn) { return bm * bn >= 128 * 64 ? 512 : 256; }
 #endif

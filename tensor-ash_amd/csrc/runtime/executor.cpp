@@ -318,6 +318,15 @@ struct ExecutorImpl {
       need.counters = (uint64_t)g.tiles * TA_GEMV_COUNTER_STRIDE;
     } else if (s.kind == KernelKind::GemmF16Mfma && gemm_lds_ok(d)) {
       need.splitk = a16_bytes(d);
+    } else if (s.kind == KernelKind::GemmF16Sk) {
+      need.splitk = a16_bytes(d);
+      const uint32_t splits = h16sk_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, s.tile_m, s.tile_n);
+      if (splits > 1) {
+        const uint64_t tiles =
+            (uint64_t)d.batch * div_ceil(d.m, s.tile_m) * div_ceil(d.n, s.tile_n);
+        need.partial = tiles * splits * s.tile_m * s.tile_n * 4;
+        need.counters = tiles * TA_GEMV_COUNTER_STRIDE;
+      }
     }
     return need;
   }
@@ -329,8 +338,19 @@ struct ExecutorImpl {
     return (planes * d.m * d.k * 2 + 255) / 256 * 256;
   }
 
+  // The f16 copy of A that the last pre-pass of a submission left in the
+  // split-K region: a later f16w GEMM with the same A (same buffer, same
+  // elements) reuses it unless an op in between wrote that buffer or the
+  // region (record() clears it).
+  struct CvtCache {
+    const void *buffer = nullptr;
+    const void *src = nullptr;
+    uint64_t n = 0;
+  };
+
   void launch_gemm(const KernelSpec &s, const ResolvedMatmul &d, const MatmulOp &op,
-                   uint32_t splits, void *splitk_scratch, hipStream_t stream) const {
+                   uint32_t splits, Scratch &scratch, CvtCache &cvt, hipStream_t stream) const {
+    void *splitk_scratch = scratch.splitk;
     GemmArgs a{};
     a.a = op.call.a->device_ptr();
     a.b = op.call.b->device_ptr();
@@ -366,9 +386,10 @@ struct ExecutorImpl {
     if (gz > 65535 || gx > 0x7fffffffull)
       fail("matmul grid (" + std::to_string(gx) + ", 1, " + std::to_string(gz) +
            ") exceeds the HIP launch limits");
-    const bool lds = (s.kind == KernelKind::GemmF16Mfma || s.kind == KernelKind::GemmA16) &&
+    const bool lds = (s.kind == KernelKind::GemmF16Mfma || s.kind == KernelKind::GemmA16 ||
+                      s.kind == KernelKind::GemmF16Sk) &&
                      gemm_lds_ok(d);
-    if (lds && s.kind == KernelKind::GemmF16Mfma) {
+    if (lds && s.kind != KernelKind::GemmA16) {
       // A -> f16 (RNE) pre-pass into scratch; the GEMM then reads f16 A.
       CvtArgs cv{};
       cv.src = static_cast<const float *>(a.a);
@@ -377,14 +398,37 @@ struct ExecutorImpl {
       const uint64_t blocks = (cv.n + 8 * 256 - 1) / (8 * 256);
       if (blocks > 0x7fffffffull)
         fail("f16 conversion grid exceeds the HIP launch limits");
-      launch("ta_cvt_f32_f16", (uint32_t)blocks, 1, 1, 256, &cv, stream);
+      const void *buf = op.call.a->buffer_id();
+      if (!(cvt.buffer == buf && cvt.src == cv.src && cvt.n == cv.n)) {
+        launch("ta_cvt_f32_f16", (uint32_t)blocks, 1, 1, 256, &cv, stream);
+        cvt = CvtCache{buf, cv.src, cv.n};
+      }
       a.a = splitk_scratch;
+    } else if (splits > 1) {
+      cvt = CvtCache{}; // the partial planes overwrite the f16 copy
+    }
+    const uint32_t lds_threads = (uint32_t)ta_h16_lds_threads((int)s.tile_m, (int)s.tile_n);
+    if (s.kind == KernelKind::GemmF16Sk) {
+      a.k_splits = h16sk_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, s.tile_m, s.tile_n);
+      if (a.k_splits > 1) {
+        const uint64_t tiles = (uint64_t)d.batch * a.tiles_m * a.tiles_n;
+        if (scratch.partial_bytes < tiles * a.k_splits * s.tile_m * s.tile_n * 4 ||
+            scratch.counters_len < tiles * TA_GEMV_COUNTER_STRIDE)
+          fail("internal: split-K f16 GEMM scratch not reserved");
+        a.partial = static_cast<float *>(scratch.partial);
+        a.counters = scratch.counters;
+      }
+      if (gz > 65535 || a.k_splits > 65535)
+        fail("matmul grid exceeds the HIP launch limits");
+      launch(s.symbol, (uint32_t)gx, a.k_splits, (uint32_t)gz, lds_threads, &a, stream);
+      return;
     }
     const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
     const bool mi16 = s.kind == KernelKind::GemmF32 && f32_mi16_ok(d, s.tile_m, s.tile_n,
                                                                    a.num_splits);
-    const uint32_t threads =
-        mi16 ? (s.tile_m == 256 ? 256u : s.tile_m == 64 ? 256u : 128u) : gemm_threads(s);
+    const uint32_t threads = mi16  ? (s.tile_m == 256 ? 256u : s.tile_m == 64 ? 256u : 128u)
+                             : lds ? lds_threads
+                                   : gemm_threads(s);
     launch(std::string(s.symbol) + (mi16 ? "_mi16" : lds ? "_lds" : vec ? "_vec" : "_gen"),
            (uint32_t)gx, 1, (uint32_t)gz, threads, &a, stream);
     if (splits > 1) {
@@ -761,8 +805,14 @@ struct ExecutorImpl {
   void record(const std::vector<MatmulOp> &ops, const std::vector<ResolvedMatmul> &res,
               const std::vector<OpPlan> &plans, Scratch &scratch, uint32_t *host_status,
               hipStream_t stream) const {
+    CvtCache cvt;
     for (size_t i = 0; i < ops.size(); ++i) {
       const OpPlan &p = plans[i];
+      // the cached f16 copy of A is stale once an op writes A's buffer
+      if (i > 0 && cvt.buffer &&
+          (ops[i - 1].call.c->buffer_id() == cvt.buffer ||
+           (ops[i - 1].store.dst && ops[i - 1].store.dst->buffer_id() == cvt.buffer)))
+        cvt = CvtCache{};
       if (p.role == 1 || p.role == 4)
         continue; // produced by the dual launch of op i+1 / the MLP launch
       if (p.role == 3) {
@@ -777,7 +827,7 @@ struct ExecutorImpl {
       if (s.is_gemv())
         launch_gemv(s, res[i], ops[i], p.role == 2 ? &ops[i - 1] : nullptr, scratch, stream);
       else
-        launch_gemm(s, res[i], ops[i], p.splitk2.value_or(1), scratch.splitk, stream);
+        launch_gemm(s, res[i], ops[i], p.splitk2.value_or(1), scratch, cvt, stream);
     }
   }
 

@@ -71,6 +71,8 @@ constexpr uint32_t kReduceThreads = 256;
 constexpr uint64_t kAutoScratchCapBytes = 256ull << 20;
 const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n);
 uint32_t gemm_threads(const KernelSpec &s);
+uint32_t h16sk_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                      uint32_t tile_m, uint32_t tile_n);
 uint32_t splitk_sub_splits(uint32_t cus, const ResolvedMatmul &dims, uint32_t splits);
 std::optional<uint32_t> heuristic_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
                                          uint32_t k);

@@ -36,6 +36,9 @@ const KernelSpec KERNEL_SPECS[] = {
      "f16w_coopmat_m64n128"},
     {"f16w_mfma_m64n64", 64, 64, 64, KernelKind::GemmF16Mfma, "ta_gemm_h16_m64n64",
      "f16w_coopmat_m64n64"},
+    {"f16w_sk_m128n128", 128, 128, 64, KernelKind::GemmF16Sk, "ta_gemm_h16sk_m128n128", ""},
+    {"f16w_sk_m128n64", 128, 64, 64, KernelKind::GemmF16Sk, "ta_gemm_h16sk_m128n64", ""},
+    {"f16w_sk_m64n128", 64, 128, 64, KernelKind::GemmF16Sk, "ta_gemm_h16sk_m64n128", ""},
     {"f16w_a16_m256n256", 256, 256, 64, KernelKind::GemmA16, "ta_gemm_a16_m256n256", ""},
     {"f16w_a16_m128n128", 128, 128, 64, KernelKind::GemmA16, "ta_gemm_a16_m128n128",
      "f16w_a16_coopmat_aligned"},
@@ -139,6 +142,8 @@ bool kernel_supports(const KernelSpec &s, const ResolvedMatmul &d) {
     return d.b_f16;
   case KernelKind::GemmA16:
     return false;
+  case KernelKind::GemmF16Sk:
+    return d.b_f16 && !d.a_f16 && gemm_lds_ok(d);
   case KernelKind::GemvF16Row:
     return d.b_f16 && d.batch == 1 && d.m <= kGemvMaxRows && d.n % 4 == 0;
   case KernelKind::GemvF32Row:
@@ -161,10 +166,14 @@ static size_t pick_tile(const char *const *names, int count, uint32_t cus, uint3
   return registry_index(names[count - 1]);
 }
 
-// f16-MFMA tile: pipelined shapes take 256x256 when that grid still covers
-// every CU, 128x128 when it covers them twice, else 64x64 (measured on
-// M = 512 prefill shapes: smaller tiles win while the grid is small);
-// other shapes take the largest register-staged tile covering every CU.
+// f16-MFMA tile.  Pipelined shapes: 256x256 when that grid covers every
+// CU; else the largest of 128x128 and 128x64 (8 waves) whose grid still
+// covers 60% of the CUs; else, for f16 weights with deep K (>= 64 stages)
+// whose 128x64 grid fits the CUs twice over, the split-K kernel; else
+// 64x64 (4 waves).  Measured on the M = 512 prefill shapes (a K step of
+// these kernels costs latency, so a tile's time follows its K steps: small
+// tiles win while the grid is small, and a deep K is best split).  Other
+// shapes take the largest register-staged tile covering every CU.
 static size_t pick_f16_mfma(bool a16, uint32_t cus, uint32_t batch, uint32_t m, uint32_t n,
                             uint32_t k) {
   static const char *mfma16_tiles[] = {"f16w_mfma_m128n128", "f16w_mfma_m128n64",
@@ -178,9 +187,16 @@ static size_t pick_f16_mfma(bool a16, uint32_t cus, uint32_t batch, uint32_t m, 
   if (!gemm_lds_ok(d))
     return pick_tile(a16 ? a16_tiles : mfma16_tiles, 4, cus, batch, m, n);
   const std::string pre = a16 ? "f16w_a16_" : "f16w_mfma_";
-  const uint64_t t256 = (uint64_t)batch * div_ceil(m, 256) * div_ceil(n, 256);
-  const uint64_t t128 = (uint64_t)batch * div_ceil(m, 128) * div_ceil(n, 128);
-  const char *tile = t256 >= cus ? "m256n256" : t128 >= 2ull * cus ? "m128n128" : "m64n64";
+  auto tiles = [&](uint32_t bm, uint32_t bn) {
+    return (uint64_t)batch * div_ceil(m, bm) * div_ceil(n, bn);
+  };
+  const uint64_t most = cus * 6ull / 10;
+  const char *tile = tiles(256, 256) >= cus   ? "m256n256"
+                     : tiles(128, 128) >= most ? "m128n128"
+                     : tiles(128, 64) >= most  ? "m128n64"
+                                               : "m64n64";
+  if (!a16 && std::string(tile) == "m64n64" && k / 64 >= 64 && 2 * tiles(128, 64) <= cus)
+    return registry_index("f16w_sk_m128n64");
   return registry_index((pre + tile).c_str());
 }
 
@@ -227,6 +243,33 @@ const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n) {
                      : m <= 64 && n >= 256 ? "f32_m64n256"
                                            : "f32_m64n64";
   return KERNEL_SPECS[registry_index(name)];
+}
+
+// K splits per output tile of the ta_gemm_h16sk_* kernels (one workgroup
+// per CU at a time, LDS-bound): the count in 1..8 (at least 4 K stages
+// per split) minimising rounds x stages per split, where a round is one
+// pass of workgroups over the CUs; ties go to fewer splits (less partial
+// traffic).  TA_H16_SPLITS fixes the count (route control for
+// measurements).
+uint32_t h16sk_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
+                      uint32_t tile_m, uint32_t tile_n) {
+  const uint64_t tiles = (uint64_t)batch * div_ceil(m, tile_m) * div_ceil(n, tile_n);
+  const uint32_t steps = std::max(1u, k / 64);
+  if (const char *env = std::getenv("TA_H16_SPLITS"))
+    return std::clamp<uint32_t>((uint32_t)std::strtoul(env, nullptr, 10), 1u, std::min(steps, 64u));
+  uint32_t best = 1;
+  uint64_t best_cost = UINT64_MAX;
+  for (uint32_t s = 1; s <= 8 && s <= steps; ++s) {
+    if (s > 1 && steps / s < 4)
+      break;
+    const uint64_t rounds = (tiles * s + cus - 1) / cus;
+    const uint64_t cost = rounds * ((steps + s - 1) / s);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = s;
+    }
+  }
+  return best;
 }
 
 uint32_t gemm_threads(const KernelSpec &s) {

@@ -461,6 +461,7 @@ enum class KernelKind : uint32_t {
   GemmF16w,      // f32 A, f16 B widened to f32, FP32 MFMA
   GemmF16Mfma,   // f32 A rounded to f16, f16 B, f16 MFMA, f32 accumulation
   GemmA16,       // f16 A, f16 B, f16 C (RNE store), f16 MFMA
+  GemmF16Sk,     // f32 A rounded to f16 at fragment read, f16 B, f16 MFMA, split-K in the launch
   GemvF16Packed, // M <= 8 decode GEMV, f16 B packed [N/TW][K][TW]
   GemvF16Row,    // M <= 8 decode GEMV, f16 B row-major
   GemvF32Row,    // M <= 8 decode GEMV, f32 B row-major
@@ -473,7 +474,8 @@ struct KernelSpec {
   const char *aliases; // extra ML_KERNEL spellings, comma separated
   bool weights_f16() const {
     return kind == KernelKind::GemmF16w || kind == KernelKind::GemmF16Mfma ||
-           kind == KernelKind::GemmA16 || kind == KernelKind::GemvF16Packed ||
+           kind == KernelKind::GemmA16 || kind == KernelKind::GemmF16Sk ||
+           kind == KernelKind::GemvF16Packed ||
            kind == KernelKind::GemvF16Row;
   }
   bool is_gemv() const {

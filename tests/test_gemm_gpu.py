@@ -218,7 +218,8 @@ def test_f16_mfma_gemm(ta, ctx, ex, oracle, shape):
     for name in [None] + names:
         kex = ex if name is None else ta.Executor(ctx, kernel_selection=name, tune=False)
         if name is None:
-            assert "mfma" in kex.dispatch_info_for(1, m, n, k, True)["kernel"]
+            routed = kex.dispatch_info_for(1, m, n, k, True)["kernel"]
+            assert "mfma" in routed or "_sk_" in routed, routed
         a = kex.tensor_from(ha, shape=[m, k])
         b = kex.tensor_from(hb, shape=[k, n], f16=True)
         bias, c = kex.tensor_from(hbias, shape=[n]), kex.tensor([m, n])
@@ -226,7 +227,8 @@ def test_f16_mfma_gemm(ta, ctx, ex, oracle, shape):
         check_f16_mfma(kex.download(c), refs, k, oracle)
 
 
-@pytest.mark.parametrize("name", ["f16w_mfma_m64n64", "f16w_mfma_m128n128", "f16w_mfma_m256n256"])
+@pytest.mark.parametrize("name", ["f16w_mfma_m64n64", "f16w_mfma_m128n64", "f16w_mfma_m64n128",
+                                  "f16w_mfma_m128n128", "f16w_mfma_m256n256"])
 @pytest.mark.parametrize("epi", ["bias_bn_gelu", "add_scaled", "mul", "broadcast_a"])
 def test_f16_mfma_pipelined_epilogues(ta, ctx, oracle, name, epi):
     """Pipelined f16-MFMA kernels (K % 64 == 0, N % 8 == 0): ragged M and N
@@ -303,3 +305,93 @@ def test_leaves_no_pending_hip_error(ta, ctx, oracle):
     kex.run_ops([ta.MatmulOp(a, b, c)])
     kex.run_matmuls_split_k2(kex.tensor([64, 2048]), kex.tensor([2048, 64]), kex.tensor([64, 64]), 4)
     assert hip.hipGetLastError() == 0
+
+
+@pytest.mark.parametrize("name", ["f16w_sk_m128n128", "f16w_sk_m128n64", "f16w_sk_m64n128"])
+@pytest.mark.parametrize("splits", ["1", "3", "5"])
+def test_f16_split_k_kernels(ta, ctx, oracle, monkeypatch, name, splits):
+    """ta_gemm_h16sk_*: f32 A rounded to f16 (RNE) by the pre-pass, K split
+    over `splits` workgroups per tile and summed in split order inside the
+    launch.  Ragged M/N tiles, a batched [B, N] bias with SiLU, a broadcast
+    B, D (ADD_SCALED); f32 tolerance against the dual-rounded oracle, 2e-3
+    against f32 A; bit-identical over repeated runs (fixed split order),
+    and the tile counters left at zero (a second, different launch reusing
+    them is still right)."""
+    monkeypatch.setenv("TA_H16_SPLITS", splits)
+    kex = ta.Executor(ctx, kernel_selection=name, tune=False)
+    bt, m, n, k = 2, 300, 264, 640
+    ha = oracle.fill_det(bt * m * k, 7200)
+    hb = oracle.fill_normal(k * n, 7201, 0.05)
+    hbias, hd = oracle.fill_det(bt * n, 7202), oracle.fill_det(bt * m * n, 7203)
+    a, b = kex.tensor_from(ha, shape=[bt, m, k]), kex.tensor_from(hb, shape=[k, n], f16=True)
+    bias, d, c = kex.tensor_from(hbias, shape=[bt, n]), kex.tensor_from(hd, shape=[bt, m, n]), kex.tensor([bt, m, n])
+    epi = ta.Epilogue(bias=bias, activation=ta.ACTIVATION_SILU, binary=ta.BINARY_ADD_SCALED, d=d, beta=0.5)
+    print(f"{name} splits={splits} B={bt} {m}x{n}x{k}", flush=True)
+    kex.run_ops([ta.MatmulOp(a, b, c, alpha=0.75, epilogue=epi)])
+    got = kex.download(c)
+    refs = f16_mfma_refs(ha, hb, bt, m, n, k, oracle, alpha=0.75, bias=hbias, bias_batch_stride=n, act=2,
+                         binary=1, d=hd, beta=0.5)
+    check_f16_mfma(got, refs, k, oracle)
+    for _ in range(3):
+        kex.run_ops([ta.MatmulOp(a, b, c, alpha=0.75, epilogue=epi)])
+        np.testing.assert_array_equal(kex.download(c), got)
+    # a smaller plain launch after: counters must be back at zero
+    m2, n2, k2 = 130, 72, 384
+    ha2, hb2 = oracle.fill_det(m2 * k2, 7204), oracle.fill_normal(k2 * n2, 7205, 0.05)
+    a2, b2, c2 = kex.tensor_from(ha2, shape=[m2, k2]), kex.tensor_from(hb2, shape=[k2, n2], f16=True), kex.tensor([m2, n2])
+    kex.run_ops([ta.MatmulOp(a2, b2, c2)])
+    check_f16_mfma(kex.download(c2), f16_mfma_refs(ha2, hb2, 1, m2, n2, k2, oracle), k2, oracle)
+
+
+@pytest.mark.parametrize("shape", [(512, 2560, 2048), (512, 2048, 5632)])
+def test_f16_split_k_prefill_shapes(ta, ctx, oracle, shape):
+    """The split-K f16w kernels at config-5 shapes with their default split
+    counts, against the oracle (the down projection 512x2048x5632 routes to
+    f16w_sk_m128n64 by default)."""
+    m, n, k = shape
+    ha, hb = oracle.fill_det(m * k, 7210), oracle.fill_normal(k * n, 7211, 0.02)
+    refs = f16_mfma_refs(ha, hb, 1, m, n, k, oracle)
+    for name in ("f16w_sk_m128n128", "f16w_sk_m128n64"):
+        kex = ta.Executor(ctx, kernel_selection=name, tune=False)
+        a, b, c = kex.tensor_from(ha, shape=[m, k]), kex.tensor_from(hb, shape=[k, n], f16=True), kex.tensor([m, n])
+        print(f"{name} {m}x{n}x{k}", flush=True)
+        kex.run_ops([ta.MatmulOp(a, b, c)])
+        check_f16_mfma(kex.download(c), refs, k, oracle)
+
+
+def test_f16w_a_conversion_reused_only_while_valid(ta, ex, oracle):
+    """Within one submission, f16w GEMMs with the same f32 A share one f16
+    pre-pass copy; an op that writes A in between, or split-K planes that
+    reuse the scratch, force a fresh conversion.  Results equal separate
+    launches bit for bit."""
+    m, k, n = 256, 512, 320
+    hx, hw1, hw2 = oracle.fill_det(m * k, 7300), oracle.fill_normal(k * n, 7301, 0.05), oracle.fill_normal(k * n, 7302, 0.05)
+    hwx = oracle.fill_normal(k * k, 7303, 0.05)
+    x, w1, w2 = ex.tensor_from(hx, shape=[m, k]), ex.tensor_from(hw1, shape=[k, n], f16=True), ex.tensor_from(hw2, shape=[k, n], f16=True)
+    wx = ex.tensor_from(hwx, shape=[k, k], f16=True)
+    y0 = ex.tensor_from(oracle.fill_det(m * k, 7304), shape=[m, k])
+    c1, c2, c3 = ex.tensor([m, n]), ex.tensor([m, n]), ex.tensor([m, n])
+    # separate launches: the reference bits
+    ex.run_ops([ta.MatmulOp(x, w1, c1)])
+    ref1 = ex.download(c1)
+    ex.run_ops([ta.MatmulOp(x, w2, c2)])
+    ref2 = ex.download(c2)
+    ex.run_ops([ta.MatmulOp(x, w1, c1), ta.MatmulOp(x, w2, c2)])  # shared conversion
+    np.testing.assert_array_equal(ex.download(c1), ref1)
+    np.testing.assert_array_equal(ex.download(c2), ref2)
+    # A rewritten in the middle of a graph: x <- y0 @ wx, then x @ w1 again
+    ex.upload(x, hx)
+    ex.run_op_graph([ta.MatmulOp(x, w1, c1), ta.MatmulOp(y0, wx, x), ta.MatmulOp(x, w1, c3)])
+    np.testing.assert_array_equal(ex.download(c1), ref1)
+    new_x = ex.download(x)
+    x2 = ex.tensor_from(new_x, shape=[m, k])
+    ex.run_ops([ta.MatmulOp(x2, w1, c2)])
+    np.testing.assert_array_equal(ex.download(c3), ex.download(c2))
+    # split-K planes between two uses of the same A
+    ex.upload(x, hx)
+    a32, b32, cs = ex.tensor_from(oracle.fill_det(64 * 8192, 7305), shape=[64, 8192]), \
+        ex.tensor_from(oracle.fill_det(8192 * 64, 7306), shape=[8192, 64]), ex.tensor([64, 64])
+    assert ex.dispatch_info_for(1, 64, 64, 8192)["split_k2"], "expected a split-K route"
+    ex.run_op_graph([ta.MatmulOp(x, w1, c1), ta.MatmulOp(a32, b32, cs), ta.MatmulOp(x, w2, c3)])
+    np.testing.assert_array_equal(ex.download(c1), ref1)
+    np.testing.assert_array_equal(ex.download(c3), ref2)
