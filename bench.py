@@ -38,6 +38,44 @@ METRIC = "fused-GEMM TFLOP/s at 4096^3 f32 + decode-GEMV HBM GB/s (f16 W), 1 MI3
 LLC_BYTES = 256 << 20
 
 
+def roofline(bound: str, achieved: float, peak: float, unit: str, traffic=None, **extra) -> dict:
+    """The roofline block of one measured kernel or step: `achieved` is
+    algorithmic work (flops or bytes, each tensor once) per second."""
+    out = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+           "frac": round(achieved / peak, 4), "traffic": traffic}
+    out.update(extra)
+    return out
+
+
+def time_roofline(flops: float, nbytes: float, seconds: float, peak_tflops: float, traffic=None) -> dict:
+    """Roofline of a shape that is compute- or bandwidth-bound depending on
+    its balance: the bound is the larger of flops / peak and bytes / HBM
+    peak; frac = that time / the measured time."""
+    t_c, t_m = flops / (peak_tflops * 1e12), nbytes / (PEAK_HBM * 1e9)
+    if t_c >= t_m:
+        return roofline("mfma", flops / seconds / 1e12, peak_tflops, "TFLOP/s", traffic,
+                        floor_us=round(t_c * 1e6, 3))
+    return roofline("hbm", nbytes / seconds / 1e9, PEAK_HBM, "GB/s", traffic, floor_us=round(t_m * 1e6, 3))
+
+
+def load_pmc_traffic() -> dict:
+    """HBM bytes per launch of the secondary kernels, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE per dispatch, each
+    scaled by the same counter on a plain copy): `key traffic_bytes=N`."""
+    out = {}
+    try:
+        for line in (ROOT / "profiles" / "secondary_pmc.txt").read_text().splitlines():
+            parts = line.split()
+            if len(parts) >= 2 and parts[1].startswith("traffic_bytes="):
+                out[parts[0]] = int(parts[1].split("=", 1)[1])
+    except OSError:
+        pass
+    return out
+
+
+PMC = {}
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -46,7 +84,7 @@ def median_ns(stats_list):
     return statistics.median([s.gpu_time_ns for s in stats_list])
 
 
-def headline(ta, ex, steps: int, warmup: int):
+def headline(ta, ex, steps: int, warmup: int, settle_ms: float):
     m = n = k = 4096
     rng = np.random.default_rng(31)
     ha = rng.uniform(-1, 1, (m, k)).astype(np.float32)
@@ -55,6 +93,14 @@ def headline(ta, ex, steps: int, warmup: int):
     a, b = ex.tensor_from(ha), ex.tensor_from(hb)
     bias, c = ex.tensor_from(hbias), ex.tensor([m, n])
     op = ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_RELU))
+    # Untimed clock settling (declared in the JSON line, not counted as
+    # warm-up): a cold process needs ~20 ms of MFMA load before the chip
+    # holds its steady clock.
+    settled = 0.0
+    t_settle = time.perf_counter()
+    while settle_ms > 0 and (time.perf_counter() - t_settle) * 1e3 < settle_ms:
+        ex.run_ops([op])
+    settled = (time.perf_counter() - t_settle) * 1e3 if settle_ms > 0 else 0.0
     for _ in range(warmup):
         ex.run_ops([op])
     stats = []
@@ -71,6 +117,7 @@ def headline(ta, ex, steps: int, warmup: int):
     rel = float(np.max(np.abs(got[rows] - ref)) / np.max(np.abs(ref)))
     info = ex.dispatch_info_for(1, m, n, k)
     return dict(
+        settle_ms=settled,
         wall_s=wall, ms_per_step=wall / steps * 1e3, value=flops / (wall / steps) / 1e12,
         kernel_ms=kernel_ns / 1e6, achieved=flops / kernel_ns / 1e3, kernel=info["kernel"],
         rel_err=rel, inputs=(ha, hb),
@@ -128,10 +175,13 @@ def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=30, layers=10):
         single_ns = median_ns([single.run() for _ in range(iters)])
         bytes_step = w_bytes + 4 * m * (hdim + 2 * ffn + 2 * hdim)
         step_ns = median_ns(stats) / layers
+        traffic = PMC.get(f"decode_M{m}")
         out[f"M{m}"] = dict(step_us=step_ns / 1e3, gbps=bytes_step / step_ns,
                             frac_hbm=bytes_step / step_ns / PEAK_HBM, bytes_per_step=bytes_step,
                             layers_per_graph=layers, launch_us=single_ns / 1e3,
-                            wall_us_per_step=wall / iters / layers * 1e6)
+                            wall_us_per_step=wall / iters / layers * 1e6,
+                            roofline=roofline("hbm", bytes_step / step_ns, PEAK_HBM, "GB/s",
+                                              traffic // layers if traffic else None))
         chain.close()
         single.close()
     return out
@@ -152,7 +202,9 @@ def batched_gelu(ta, ex, iters=10):
     ns = median_ns([ex.run_ops([op]) for _ in range(iters)])
     flops = 2.0 * bt * m * n * k
     return dict(kernel_ms=ns / 1e6, tflops=flops / ns / 1e3, frac=flops / ns / 1e3 / PEAK_FP32_MFMA,
-                kernel=ex.dispatch_info_for(bt, m, n, k)["kernel"])
+                kernel=ex.dispatch_info_for(bt, m, n, k)["kernel"],
+                roofline=roofline("mfma", flops / ns / 1e3, PEAK_FP32_MFMA, "TFLOP/s",
+                                  PMC.get("gelu_8x2048")))
 
 
 def splitk(ta, ex, iters=10):
@@ -172,7 +224,9 @@ def splitk(ta, ex, iters=10):
                             for i in range(iters)])
             key = f"{m}x{n}x{k}_S{s if s else 'auto'}"
             out[key] = dict(us=ns / 1e3, tflops=flops / ns / 1e3, gbps=bytes_ / ns,
-                            frac_mfma=flops / ns / 1e3 / PEAK_FP32_MFMA, frac_hbm=bytes_ / ns / PEAK_HBM)
+                            frac_mfma=flops / ns / 1e3 / PEAK_FP32_MFMA, frac_hbm=bytes_ / ns / PEAK_HBM,
+                            roofline=time_roofline(flops, bytes_, ns * 1e-9, PEAK_FP32_MFMA,
+                                                   PMC.get(f"splitk_{m}x{n}x{k}") if s == 0 else None))
     return out
 
 
@@ -195,16 +249,34 @@ def prefill_layer(ta, ex, iters=10):
     out = {}
     total_ns = 0.0
     total_flops = 0.0
+    total_bytes = 0.0
     for name, ops in cases.items():
         for _ in range(3):
             ex.run_ops(ops)
         ns = median_ns([ex.run_ops(ops) for _ in range(iters)])
-        dims = [int(v) for v in name.split("_")[-1].split("x")]
-        flops = 2.0 * dims[0] * dims[1] * dims[2]
-        out[name] = dict(us=ns / 1e3, tflops=flops / ns / 1e3)
+        mm, nn, kk = [int(v) for v in name.split("_")[-1].split("x")]
+        flops = 2.0 * mm * nn * kk
+        # A f32, W f16, C f32 (+ D f32 for the binary epilogues)
+        nbytes = 4.0 * mm * kk + 2.0 * kk * nn + 4.0 * mm * nn * (2 if ops[0].epilogue.binary else 1)
+        out[name] = dict(us=ns / 1e3, tflops=flops / ns / 1e3,
+                         kernel=ex.dispatch_info_for(1, mm, nn, kk, True)["kernel"],
+                         roofline=time_roofline(flops, nbytes, ns * 1e-9, PEAK_FP16_MFMA,
+                                                PMC.get(f"prefill_{name.split('_')[0]}")))
         total_ns += ns
         total_flops += flops
-    out["layer_gemms"] = dict(us=total_ns / 1e3, tflops=total_flops / total_ns / 1e3)
+        total_bytes += nbytes
+    out["layer_gemms"] = dict(us=total_ns / 1e3, tflops=total_flops / total_ns / 1e3,
+                              note="sum of the five GEMMs, each its own ta_run_ops call",
+                              roofline=time_roofline(total_flops, total_bytes, total_ns * 1e-9, PEAK_FP16_MFMA))
+    # The layer as a prefill runs it: the five GEMMs in one submission (one
+    # event pair; the f16 copy of x is made once for QKV, up and gate).
+    layer = [op for ops in cases.values() for op in ops]
+    for _ in range(3):
+        ex.run_op_graph(layer)
+    ns = median_ns([ex.run_op_graph(layer) for _ in range(iters)])
+    out["layer_gemms_one_submission"] = dict(
+        us=ns / 1e3, tflops=total_flops / ns / 1e3,
+        roofline=time_roofline(total_flops, total_bytes, ns * 1e-9, PEAK_FP16_MFMA))
     return out
 
 
@@ -358,7 +430,9 @@ def cpu_baseline(inputs, target_s: float = 12.0):
     ha, hb = inputs
     m, k = ha.shape
     n = hb.shape[1]
-    threads = max(1, min(os.cpu_count() or 1, 16))
+    # The GPU box gives one GPU a 16-thread CPU share (OMP_NUM_THREADS=16
+    # there); the host may show more logical CPUs.
+    threads = max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16))
     a = np.ascontiguousarray(ha).reshape(-1)
     b = np.ascontiguousarray(hb).reshape(-1)
     out = np.zeros(m * n, np.float32)
@@ -374,7 +448,17 @@ def cpu_baseline(inputs, target_s: float = 12.0):
         dt += time.perf_counter() - t1
         rows += more
     flops = 2.0 * rows * n * k
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                cpu_model=model, host_logical_cpus=os.cpu_count(),
+                cores_note="threads capped at the one-GPU CPU share (16) of the GPU box",
                 sample=f"cpu_bmm (f64-accumulate i-j-k oracle) on {rows} of 4096 output rows of the "
                        f"4096^3 GEMM, {dt:.1f} s on {threads} threads, extrapolation-free rate")
 
@@ -396,11 +480,15 @@ def load_traffic():
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=50,
-                    help="untimed steps first; the chip needs ~20 ms of MFMA load to reach its steady clock")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=10, help="untimed steps after clock settling")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--no-headline", action="store_true",
+                    help="skip the headline (profiling runs of single sections)")
+    ap.add_argument("--clock-settle-ms", type=float, default=50.0,
+                    help="untimed headline GEMMs before warm-up until this many ms passed "
+                         "(declared in the JSON line as clock_settle_ms)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (rocprof counter calibration)")
     ap.add_argument("--sections", default="decode,gelu,splitk,prefill,attention,token_loop,vendor",
@@ -429,10 +517,13 @@ def main() -> int:
         return 0
     import tensor_ash as ta
 
+    PMC.update(load_pmc_traffic())
     ctx = ta.Context()
     ex = ta.Executor(ctx, tune=False)
-    log("headline 4096^3 f32 fused GEMM ...")
-    hl = headline(ta, ex, args.steps, args.warmup)
+    hl = None
+    if not args.no_headline:
+        log("headline 4096^3 f32 fused GEMM ...")
+        hl = headline(ta, ex, args.steps, args.warmup, args.clock_settle_ms)
     secondary = {}
     if "decode" in sections:
         log("decode SwiGLU MLP ...")
@@ -455,6 +546,9 @@ def main() -> int:
     if "vendor" in sections:
         log("vendor library reference ...")
         secondary["vendor_reference"] = vendor_reference()
+    if hl is None:
+        print(json.dumps({"secondary": secondary}), flush=True)
+        return 0
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
@@ -468,6 +562,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(hl["ms_per_step"], 4),
+        "clock_settle_ms": round(hl["settle_ms"], 1),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
