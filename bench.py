@@ -280,6 +280,53 @@ def prefill_layer(ta, ex, iters=10):
     return out
 
 
+def concurrency(ta, ex, iters=20):
+    """Independent ops in one ta_run_ops call may run concurrently on
+    several streams; the same ops as a dependent op graph run back to back
+    on one.  Cases: TinyLlama decode Q/K/V projections (three packed f16
+    GEMVs, M = 1), four independent 512x1024x2048 f16w GEMMs, and four
+    long underfilled f32 GEMMs with a fused bias + GELU (256x256x16384,
+    16 tiles each; the epilogue rules out split-K)."""
+    rng = np.random.default_rng(91)
+
+    def packed(k, n):
+        w = (rng.standard_normal(k * n, dtype=np.float32) * 0.02).astype(np.float32)
+        return ex.tensor_from(ta.pack_f16w_row_tiles(w, k, n, ta.f16w_row_tile_n(k, n)), shape=[k, n], f16=True)
+
+    x = ex.tensor_from(rng.uniform(-1, 1, (1, 2048)).astype(np.float32))
+    qkv = [ta.MatmulOp(x, packed(2048, n), ex.tensor([1, n]), packed_b=True) for n in (2048, 256, 256)]
+    a = ex.tensor_from(rng.uniform(-1, 1, (512, 2048)).astype(np.float32))
+    gemms = [ta.MatmulOp(a, ex.tensor_from((rng.standard_normal((2048, 1024), dtype=np.float32) * 0.02),
+                                           f16=True), ex.tensor([512, 1024])) for _ in range(4)]
+    bias = ex.tensor_from(rng.uniform(-1, 1, 256).astype(np.float32))
+    big = [ta.MatmulOp(ex.tensor_from(rng.uniform(-1, 1, (256, 16384)).astype(np.float32)),
+                       ex.tensor_from(rng.uniform(-1, 1, (16384, 256)).astype(np.float32)),
+                       ex.tensor([256, 256]), epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_GELU))
+           for _ in range(4)]
+    out = {"note": "run_ops spreads independent ops over 4 streams only when the work beyond the "
+                   "longest op is well above the ~40 us fork/join cost; one_lane_us forces one stream "
+                   "(same routes); op_graph_us runs the same ops as a dependent graph"}
+    def serial_run_ops(ops):
+        os.environ["TA_RUN_OPS_LANES"] = "1"
+        try:
+            return ex.run_ops(ops)
+        finally:
+            del os.environ["TA_RUN_OPS_LANES"]
+
+    for name, ops in (("decode_qkv_gemv_m1", qkv), ("four_512x1024x2048_f16w", gemms),
+                      ("four_256x256x16384_f32_bias_gelu", big)):
+        for _ in range(3):
+            ex.run_ops(ops)
+            serial_run_ops(ops)
+            ex.run_op_graph(ops)
+        auto = median_ns([ex.run_ops(ops) for _ in range(iters)])
+        serial = median_ns([serial_run_ops(ops) for _ in range(iters)])
+        graph = median_ns([ex.run_op_graph(ops) for _ in range(iters)])
+        out[name] = dict(run_ops_us=auto / 1e3, one_lane_us=serial / 1e3, speedup=serial / auto,
+                         op_graph_us=graph / 1e3)
+    return out
+
+
 ATTN_CASES = (  # name, H, H_kv, T, dh
     ("tinyllama_prefill_t512_dh64", 32, 4, 512, 64),
     ("llama_prefill_t2048_dh128", 32, 8, 2048, 128),
@@ -491,7 +538,7 @@ def main() -> int:
                          "(declared in the JSON line as clock_settle_ms)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (rocprof counter calibration)")
-    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,attention,token_loop,vendor",
+    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,concurrency,attention,token_loop,vendor",
                     help="comma list of secondary sections to run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -537,6 +584,9 @@ def main() -> int:
     if "prefill" in sections:
         log("prefill layer GEMMs ...")
         secondary["prefill_tinyllama_m512_f16w"] = prefill_layer(ta, ex)
+    if "concurrency" in sections:
+        log("independent ops in one submission ...")
+        secondary["run_ops_concurrency"] = concurrency(ta, ex)
     if "attention" in sections:
         log("causal prefill attention ...")
         secondary["causal_prefill_attention"] = attention(ta, ex)

@@ -101,11 +101,25 @@ struct Scratch {
   }
 };
 
+// Extra stream of a slot for run_ops' independent ops: its own scratch,
+// so ops on different lanes never share partial planes or counters.
+struct SideLane {
+  hipStream_t stream = nullptr;
+  hipEvent_t done = nullptr;
+  Scratch scratch;
+};
+
+// Streams a submission of independent ops is spread over (the slot's own
+// plus three side lanes): GPU_MAX_HW_QUEUES is 4 per process by default.
+constexpr size_t kRunOpsLanes = 4;
+
 struct Slot {
   hipStream_t stream = nullptr;
   hipEvent_t start = nullptr, end = nullptr;
   Scratch scratch;
   uint32_t *host_status = nullptr; // mapped pinned word (decode-MLP status)
+  hipEvent_t fork = nullptr;       // created with the side lanes
+  std::vector<SideLane> side;      // created on first use
 };
 
 // Mapped pinned word the decode-MLP kernel reports its wait status into.
@@ -840,6 +854,77 @@ struct ExecutorImpl {
     slot->scratch.ensure_mlp(need.mlp);
     return submit_on(slot, ops, res, plans, slot->scratch);
   }
+  // run_ops with several independent ops (src/executor/dispatch.rs:55-60:
+  // no barriers between them): ops are spread over the slot's stream and
+  // its side lanes (largest first, each to the lane with the least work so
+  // far, in a deterministic order), forked from and joined back into the
+  // slot's stream with events.  Each lane has its own scratch; an op's
+  // result does not depend on the lane it ran on.
+  uint64_t submit_concurrent(Slot *slot, const std::vector<MatmulOp> &ops,
+                             const std::vector<ResolvedMatmul> &res,
+                             const std::vector<OpPlan> &plans) const {
+    const size_t lanes = std::min(kRunOpsLanes, ops.size());
+    if (slot->side.size() + 1 < lanes) {
+      if (!slot->fork)
+        hip_check(hipEventCreateWithFlags(&slot->fork, hipEventDisableTiming), "hipEventCreate");
+      while (slot->side.size() + 1 < lanes) {
+        SideLane l;
+        hip_check(hipStreamCreateWithFlags(&l.stream, hipStreamNonBlocking), "hipStreamCreate");
+        hip_check(hipEventCreateWithFlags(&l.done, hipEventDisableTiming), "hipEventCreate");
+        slot->side.push_back(std::move(l));
+      }
+    }
+    std::vector<size_t> order(ops.size());
+    for (size_t i = 0; i < order.size(); ++i)
+      order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](size_t x, size_t y) {
+      return res[x].total_flops > res[y].total_flops;
+    });
+    std::vector<uint64_t> load(lanes, 0);
+    std::vector<std::vector<size_t>> members(lanes);
+    for (size_t i : order) {
+      const size_t l = std::min_element(load.begin(), load.end()) - load.begin();
+      load[l] += std::max<uint64_t>(res[i].total_flops, 1);
+      members[l].push_back(i);
+    }
+    struct Part {
+      std::vector<MatmulOp> ops;
+      std::vector<ResolvedMatmul> res;
+      std::vector<OpPlan> plans;
+    };
+    std::vector<Part> parts(lanes);
+    for (size_t l = 0; l < lanes; ++l) {
+      std::sort(members[l].begin(), members[l].end());
+      for (size_t i : members[l]) {
+        parts[l].ops.push_back(ops[i]);
+        parts[l].res.push_back(res[i]);
+        parts[l].plans.push_back(plans[i]);
+      }
+      const ScratchNeed need = total_need(parts[l].res, parts[l].plans);
+      Scratch &sc = l == 0 ? slot->scratch : slot->side[l - 1].scratch;
+      sc.ensure(need.splitk, need.partial, need.counters);
+      sc.ensure_mlp(need.mlp);
+    }
+    hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
+    hip_check(hipEventRecord(slot->fork, slot->stream), "hipEventRecord");
+    for (size_t l = 1; l < lanes; ++l)
+      hip_check(hipStreamWaitEvent(slot->side[l - 1].stream, slot->fork, 0), "hipStreamWaitEvent");
+    for (size_t l = 0; l < lanes; ++l) {
+      hipStream_t st = l == 0 ? slot->stream : slot->side[l - 1].stream;
+      Scratch &sc = l == 0 ? slot->scratch : slot->side[l - 1].scratch;
+      record(parts[l].ops, parts[l].res, parts[l].plans, sc, slot->host_status, st);
+    }
+    for (size_t l = 1; l < lanes; ++l) {
+      hip_check(hipEventRecord(slot->side[l - 1].done, slot->side[l - 1].stream), "hipEventRecord");
+      hip_check(hipStreamWaitEvent(slot->stream, slot->side[l - 1].done, 0), "hipStreamWaitEvent");
+    }
+    hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
+    hip_check(hipEventSynchronize(slot->end), "hipEventSynchronize");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, slot->start, slot->end), "hipEventElapsedTime");
+    return (uint64_t)((double)ms * 1e6);
+  }
+
   // Submit with the given scratch, which already holds what the plans need.
   uint64_t submit_on(Slot *slot, const std::vector<MatmulOp> &ops,
                      const std::vector<ResolvedMatmul> &res, const std::vector<OpPlan> &plans,
@@ -1142,10 +1227,14 @@ struct ExecutorImpl {
       }
     }
 
+    // Split-K eligibility: plain ops (src/executor/mod.rs:125-139).  The
+    // reference also excludes multi-op run_ops submissions, whose ops share
+    // one scratch with no barriers between them; here each stream lane has
+    // its own scratch and runs in stream order, so every plain op may take
+    // the split-K route.
     std::vector<OpPlan> plans;
     for (size_t i = 0; i < ops.size(); ++i) {
-      const bool eligible = !ops[i].call.accumulate && ops[i].epilogue.is_none() &&
-                            (graph || ops.size() == 1);
+      const bool eligible = !ops[i].call.accumulate && ops[i].epilogue.is_none();
       plans.push_back(plan_op(ops[i], res[i], eligible));
     }
     if (graph)
@@ -1154,8 +1243,51 @@ struct ExecutorImpl {
       return run_split_k2(ops[0].call, *plans[0].splitk2);
 
     Lease lease(this);
-    const uint64_t ns = submit_and_wait(lease.s, ops, res, plans);
+    const uint64_t ns = !graph && run_ops_lanes(res, plans) > 1
+                            ? submit_concurrent(lease.s, ops, res, plans)
+                            : submit_and_wait(lease.s, ops, res, plans);
     return RunStats{ns, ops.size(), flops};
+  }
+
+  // Lanes for a run_ops submission of independent ops.  Forking onto side
+  // streams and joining back costs ~40 us on this platform (measured with
+  // four 28 us kernels: 114 us serial, 71 us over four streams), and an op
+  // whose grid covers the CUs (split-K, decode GEMV and large-tile routes
+  // are planned that way) gains nothing from company.  So the ops are
+  // spread only when those whose grids leave most CUs idle would, run
+  // back to back, take well over that beyond the longest of them; an op's
+  // time is estimated from flops and bytes at sustained rates, scaled by
+  // the share of the CUs its grid occupies.  TA_RUN_OPS_LANES fixes the
+  // lane count (1 = serial; route control).
+  uint32_t run_ops_lanes(const std::vector<ResolvedMatmul> &res,
+                         const std::vector<OpPlan> &plans) const {
+    if (res.size() < 2)
+      return 1;
+    if (const char *env = std::getenv("TA_RUN_OPS_LANES"))
+      return (uint32_t)std::clamp<unsigned long>(std::strtoul(env, nullptr, 10), 1, kRunOpsLanes);
+    const double cus = ctx->cu_count();
+    double total = 0.0, longest = 0.0;
+    size_t small = 0;
+    for (size_t i = 0; i < res.size(); ++i) {
+      const ResolvedMatmul &d = res[i];
+      const KernelSpec &s = KERNEL_SPECS[plans[i].kernel];
+      if (plans[i].splitk2 || s.is_gemv())
+        continue;
+      const double tiles = (double)d.batch * div_ceil(d.m, s.tile_m) * div_ceil(d.n, s.tile_n);
+      if (tiles >= cus / 2)
+        continue;
+      const double bytes = (d.a_f16 ? 2.0 : 4.0) * d.batch * d.m * d.k +
+                           (d.b_f16 ? 2.0 : 4.0) * (d.batch_stride_b ? d.batch : 1) * d.k * d.n +
+                           4.0 * d.batch * d.m * d.n;
+      const double rate = d.b_f16 ? 300e12 : 80e12; // sustained flop/s on the whole chip
+      const double us =
+          std::max((double)d.total_flops / rate, bytes / 4e12) * 1e6 * cus / tiles + 5.0;
+      total += us;
+      longest = std::max(longest, us);
+      ++small;
+    }
+    return small >= 2 && total - longest > 60.0 ? (uint32_t)std::min(kRunOpsLanes, res.size())
+                                                : 1u;
   }
 
   // ---- split-K (src/executor/reduction.rs:21-70) ----
@@ -1366,6 +1498,14 @@ Executor::~Executor() {
   (void)hipSetDevice(impl_->ctx->device());
   for (Slot *s : impl_->all_slots) {
     (void)hipStreamSynchronize(s->stream);
+    for (SideLane &l : s->side) {
+      (void)hipStreamSynchronize(l.stream);
+      l.scratch.release();
+      (void)hipEventDestroy(l.done);
+      (void)hipStreamDestroy(l.stream);
+    }
+    if (s->fork)
+      (void)hipEventDestroy(s->fork);
     s->scratch.release();
     (void)hipEventDestroy(s->start);
     (void)hipEventDestroy(s->end);

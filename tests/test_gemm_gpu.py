@@ -395,3 +395,64 @@ def test_f16w_a_conversion_reused_only_while_valid(ta, ex, oracle):
     ex.run_op_graph([ta.MatmulOp(x, w1, c1), ta.MatmulOp(a32, b32, cs), ta.MatmulOp(x, w2, c3)])
     np.testing.assert_array_equal(ex.download(c1), ref1)
     np.testing.assert_array_equal(ex.download(c3), ref2)
+
+
+@pytest.mark.parametrize("lanes", ["4", "2", None])
+def test_run_ops_independent_ops_run_concurrently_with_serial_bits(ta, ex, oracle, monkeypatch, lanes):
+    """ta_run_ops takes independent ops with no barriers between them
+    (src/executor/dispatch.rs:55-60): they are spread over several streams,
+    each with its own scratch.  Every output equals its own single-op
+    launch bit for bit, over two submissions (lane scratch reused).  The
+    lane count is forced (TA_RUN_OPS_LANES) or left to the heuristic."""
+    if lanes:
+        monkeypatch.setenv("TA_RUN_OPS_LANES", lanes)
+    ops, outs = [], []
+
+    def f32(shape, seed):
+        return ex.tensor_from(oracle.fill_det(int(np.prod(shape)), seed), shape=list(shape))
+
+    def f16w(k, n, seed, packed=False):
+        w = oracle.fill_normal(k * n, seed, 0.05)
+        if packed:
+            w = ta.pack_f16w_row_tiles(w, k, n, ta.f16w_row_tile_n(k, n))
+        return ex.tensor_from(w, shape=[k, n], f16=True)
+
+    cases = [  # (A shape, B, out shape, epilogue kwargs, packed)
+        ((256, 512), f32((512, 384), 7401), (256, 384), dict(bias=f32((384,), 7402), activation=ta.ACTIVATION_GELU), False),
+        ((512, 1024), f16w(1024, 640, 7403), (512, 640), dict(activation=ta.ACTIVATION_SILU), False),
+        ((1, 2048), f16w(2048, 1024, 7404, packed=True), (1, 1024), {}, True),
+        ((4, 2048), f16w(2048, 512, 7405, packed=True), (4, 512), {}, True),
+        ((128, 4096), f32((4096, 128), 7406), (128, 128), {}, False),  # split-K route
+        ((96, 320), f32((320, 200), 7407), (96, 200), dict(binary=ta.BINARY_ADD_SCALED, d=f32((96, 200), 7408), beta=0.5), False),
+    ]
+    for i, (ashape, b, oshape, epi, packed) in enumerate(cases):
+        a = f32(ashape, 7410 + i)
+        c = ex.tensor(list(oshape))
+        ops.append(ta.MatmulOp(a, b, c, epilogue=ta.Epilogue(**epi), packed_b=packed))
+        outs.append(c)
+    refs = []
+    for op, c in zip(ops, outs):
+        ex.run_ops([op])
+        refs.append(ex.download(c).copy())
+    if lanes is None:
+        # long underfilled GEMMs with an epilogue (no split-K): the heuristic spreads these
+        bias = f32((256,), 7440)
+        big = [ta.MatmulOp(f32((256, 16384), 7420 + i), f32((16384, 256), 7430 + i), ex.tensor([256, 256]),
+                           epilogue=ta.Epilogue(bias=bias, activation=ta.ACTIVATION_RELU)) for i in range(4)]
+        monkeypatch.setenv("TA_RUN_OPS_LANES", "1")  # serial reference, same (non-split-K) routes
+        ex.run_ops(big)
+        big_refs = [ex.download(op.c).copy() for op in big]
+        monkeypatch.delenv("TA_RUN_OPS_LANES")
+        for op in big:
+            ex.upload(op.c, np.zeros(256 * 256, np.float32))
+        ex.run_ops(big)
+        for op, r in zip(big, big_refs):
+            np.testing.assert_array_equal(ex.download(op.c), r)
+    for rep in range(2):
+        for c in outs:
+            ex.upload(c, np.full(int(np.prod(c.shape)), np.nan, np.float32))
+        print(f"concurrent run_ops of {len(ops)} ops, round {rep}", flush=True)
+        st = ex.run_ops(ops)
+        assert st.n_calls == len(ops)
+        for i, c in enumerate(outs):
+            np.testing.assert_array_equal(ex.download(c), refs[i], err_msg=f"op {i}")
