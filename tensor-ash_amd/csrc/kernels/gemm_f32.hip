@@ -267,7 +267,10 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 //  * v_mfma_f32_16x16x4_f32; FM x FN blocks of 16x16 accumulators per wave
 //    (256 registers per lane at 128x128, kept in the AGPRs).  MFMA step s
 //    of a 16-deep stage takes k = (lane / 16) * 4 + s from both operands.
-//  * NS = 4 stages of 16-deep A [BM][16] and B [16][BN] slabs in LDS,
+//  * NS stages (ta_mi16_stages: 8 for the 32x128 tile, whose two waves
+//    per CU need the deeper look-ahead to cover the loaded memory latency;
+//    4 elsewhere, where 8 measured slower) of 16-deep A [BM][16] and
+//    B [16][BN] slabs in LDS,
 //    filled by direct global -> LDS loads (global_load_lds_dwordx4) with
 //    16-byte chunks XOR-swizzled per row on the global side:
 //      A rows (64 bytes): chunk ^ ((b1 ^ b3) | b2 << 1) of the row index, so
@@ -304,7 +307,7 @@ template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
   static constexpr int MFMAS = 4 * FM * FN; // per stage
   static constexpr int SIDE = LD + READS;   // side operations per stage
   static constexpr int RU = BN / 64;        // a B row in 256-byte ds_read2st64 units
-  static_assert(NS == 4, "the loop is unrolled by four stages, two LDS base groups");
+  static_assert(NS >= 4 && NS % 2 == 0, "the loop is unrolled by NS stages, NS / 2 LDS base groups");
   static_assert((NS - 3) * LD <= 63, "vmcnt range");
   static_assert(A_LD * T * 16 == A_BYTES && B_LD * T * 16 == B_BYTES, "stages split evenly");
   static_assert(SIDE <= MFMAS && 2 * LD <= SIDE, "side operations fit between the MFMAs");
@@ -370,11 +373,11 @@ template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
     const char *bbase0 = reinterpret_cast<const char *>(B + n0);
     const uint64_t b_stage = (uint64_t)BK * p.n * 4;
     const uint32_t lr = lane & 15u, lg = lane >> 4;
-    // LDS read bases for stages {0, 1} (group 0) and {2, 3} (group 1); the
-    // stage within a group is the instruction's immediate offset.
-    uint32_t a_off[2][FM], b_off[2][FN];
+    // LDS read bases for stage pairs {2g, 2g + 1} (group g); the stage
+    // within a group is the instruction's immediate offset.
+    uint32_t a_off[NS / 2][FM], b_off[NS / 2][FN];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
+    for (int g = 0; g < NS / 2; ++g) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         const uint32_t row = wm * WTM + fm * 16 + lr;
@@ -474,10 +477,9 @@ template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
     for (uint32_t kt = 0; kt < kts; kt += NS) {
-      body(std::integral_constant<int, 0>{}, kt);
-      body(std::integral_constant<int, 1>{}, kt + 1);
-      body(std::integral_constant<int, 2>{}, kt + 2);
-      body(std::integral_constant<int, 3>{}, kt + 3);
+      ta_static_for<NS>([&](auto sc) __attribute__((always_inline)) {
+        body(sc, kt + decltype(sc)::value);
+      });
       // The MFMAs are inline asm, so the compiler does not know their result
       // latency: wait states after each iteration's last MFMAs, so copies
       // the compiler places at the loop exit read settled accumulators.
@@ -536,11 +538,11 @@ TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2, 16)
 // (see GemmF32Mi16): the 256x256 data-parallel tile and the two skinny
 // split-K stage-1 tiles.
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m256n256_mi16(GemmArgs p) {
-  GemmF32Mi16<256, 256, 2, 2, 4>::run(p);
+  GemmF32Mi16<256, 256, 2, 2, ta_mi16_stages(256)>::run(p);
 }
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m64n256_mi16(GemmArgs p) {
-  GemmF32Mi16<64, 256, 1, 4, 4>::run(p);
+  GemmF32Mi16<64, 256, 1, 4, ta_mi16_stages(64)>::run(p);
 }
 extern "C" __global__ __launch_bounds__(128) void ta_gemm_f32_m32n128_mi16(GemmArgs p) {
-  GemmF32Mi16<32, 128, 1, 2, 4>::run(p);
+  GemmF32Mi16<32, 128, 1, 2, ta_mi16_stages(32)>::run(p);
 }

@@ -440,7 +440,7 @@ struct ExecutorImpl {
     const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
     const bool mi16 = s.kind == KernelKind::GemmF32 && f32_mi16_ok(d, s.tile_m, s.tile_n,
                                                                    a.num_splits);
-    const uint32_t threads = mi16  ? (s.tile_m == 256 ? 256u : s.tile_m == 64 ? 256u : 128u)
+    const uint32_t threads = mi16  ? mi16_threads(s.tile_m)
                              : lds ? lds_threads
                                    : gemm_threads(s);
     launch(std::string(s.symbol) + (mi16 ? "_mi16" : lds ? "_lds" : vec ? "_vec" : "_gen"),

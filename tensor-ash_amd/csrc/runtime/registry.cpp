@@ -110,17 +110,21 @@ uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 // Shapes the pipelined f16-MFMA kernels (`_lds` code objects) take: whole
 // 64-deep K stages and 16-byte B rows.
 bool gemm_lds_ok(const ResolvedMatmul &d) { return d.k > 0 && d.k % 64 == 0 && d.n % 8 == 0; }
+// Threads of the _mi16 kernel of a tile height (32: 128, else 256).
+uint32_t mi16_threads(uint32_t tile_m) { return tile_m == 32 ? 128u : 256u; }
+
 // The ta_gemm_f32_<tile>_mi16 kernels (256x256, and the split-K stage-1
 // tiles 64x256 and 32x128) take whole tiles of f32 A and B and walk each
-// K window four 16-deep stages at a time; `planes` K windows of equal
-// length (the split window rule gives that when K is a multiple of
-// 64 * planes); 32-bit per-lane load offsets span a tile's A rows and 16
-// rows of B.
+// K window ta_mi16_stages(tile_m) 16-deep stages at a time; `planes` K
+// windows of equal length holding whole loops (the split window rule gives
+// that when K is a multiple of 16 * stages * planes); 32-bit per-lane load
+// offsets span a tile's A rows and 16 rows of B.
 bool f32_mi16_ok(const ResolvedMatmul &d, uint32_t tile_m, uint32_t tile_n, uint32_t planes) {
   const bool tile = (tile_m == 256 && tile_n == 256) || (tile_m == 64 && tile_n == 256) ||
                     (tile_m == 32 && tile_n == 128);
+  const uint64_t loop = 16ull * ta_mi16_stages((int)tile_m);
   return tile && planes >= 1 && !d.a_f16 && !d.b_f16 && d.m % tile_m == 0 && d.n % tile_n == 0 &&
-         d.k > 0 && d.k % (64ull * planes) == 0 && (uint64_t)tile_m * d.k * 4 < (1ull << 32) &&
+         d.k > 0 && d.k % (loop * planes) == 0 && (uint64_t)tile_m * d.k * 4 < (1ull << 32) &&
          16ull * d.n * 4 < (1ull << 32);
 }
 

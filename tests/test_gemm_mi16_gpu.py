@@ -1,6 +1,7 @@
 """GPU parity of the aligned FP32 route (256x256, 64x256 and 32x128 tiles
 on v_mfma_f32_16x16x4_f32, taken when M and N are multiples of the tile
-and K of 64) against the CPU oracle, with every epilogue, alpha / accumulate and
+and K of one pipeline loop: 64, or 128 for the eight-stage 32x128 tile)
+against the CPU oracle, with every epilogue, alpha / accumulate and
 the batch-broadcast forms; shapes just off the alignment take the other
 kernels and must agree too.  Tolerances as in test_gemm_gpu.check_f32.
 """
@@ -23,7 +24,7 @@ EPIS = [dict(), dict(bias=True), dict(act=1), dict(act=2, bias=True), dict(act=3
         dict(binary=2), dict(alpha=0.25, accumulate=True, act=3), dict(bias=True, act=2, binary=2)]
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 64), (512, 768, 192), (768, 512, 1024)])
+@pytest.mark.parametrize("shape", [(256, 256, 64), (256, 256, 128), (512, 768, 192), (768, 512, 1024)])
 @pytest.mark.parametrize("epi", EPIS)
 def test_aligned_epilogues(ta, kex, oracle, shape, epi):
     m, n, k = shape
