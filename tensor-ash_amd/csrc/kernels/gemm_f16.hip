@@ -240,17 +240,20 @@ struct GemmH16 {
 //    epilogue and clears the counter.  Nothing waits on another workgroup,
 //    so any residency order completes.  Used for deep K, where a tile's
 //    chain of stages is long and the grid small.
-template <int BM, int BN, int BK, int WGM, int WGN, int NS, bool C_F16, bool SPLIT, bool DBUF>
+template <int BM, int BN, int BK, int WGM, int WGN, int NS, bool C_F16, bool SPLIT, bool DBUF,
+          bool DUAL = false>
 struct GemmH16Pipe {
   static constexpr int T = 64 * WGM * WGN;
+  static constexpr int WAYS = DUAL ? 2 : 1; // weight matrices streamed per stage
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;
   static constexpr int FM = WTM / 32, FN = WTN / 32;
   static constexpr int KS = BK / 16; // MFMA k-steps per stage
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
-  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int STAGE = A_BYTES + WAYS * B_BYTES;
   static constexpr int CPA = BK / 8, CPR = BN / 8; // 16-byte chunks per A / B row
   static constexpr int A_LD = A_BYTES / 16 / T, B_LD = B_BYTES / 16 / T;
-  static constexpr int LD = A_LD + B_LD; // direct loads per thread per stage
+  static constexpr int LD = A_LD + WAYS * B_LD; // direct loads per thread per stage
+  static_assert(!DUAL || (!SPLIT && !C_F16), "dual: f32 C, no split-K");
   static_assert(A_LD * T * 16 == A_BYTES && B_LD * T * 16 == B_BYTES, "stages split evenly");
   static_assert(CPR >= 8, "B swizzle needs >= 8 chunks per row");
   static_assert(BK == 32 || BK == 64, "A rows of 4 or 8 chunks");
@@ -288,7 +291,7 @@ struct GemmH16Pipe {
   }
 
   struct Frags {
-    f16x8 a[KS][FM], b[KS][FN];
+    f16x8 a[KS][FM], b[WAYS][KS][FN];
   };
 
   static TA_DEVICE void read_frags(uint32_t st, const uint32_t (&a_off)[KS][FM],
@@ -299,26 +302,34 @@ struct GemmH16Pipe {
       for (int fm = 0; fm < FM; ++fm)
         f.a[j][fm] = *(lds_f16x8 *)(uintptr_t)(st + a_off[j][fm]);
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][0]));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4 *)(uintptr_t)(st + b_off[j][fn][1]));
-        f.b[j][fn] =
-            __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
+      for (int w = 0; w < WAYS; ++w)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4 *)(uintptr_t)(st + w * B_BYTES + b_off[j][fn][0]));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4 *)(uintptr_t)(st + w * B_BYTES + b_off[j][fn][1]));
+          f.b[w][j][fn] =
+              __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
     }
   }
 
-  static TA_DEVICE void mfmas(const Frags &f, f32x16 (&acc)[FM][FN]) {
+  // acc2: the second weight matrix's accumulators (dual launches only).
+  static TA_DEVICE void mfmas(const Frags &f, f32x16 (&acc)[FM][FN],
+                              f32x16 (&acc2)[DUAL ? FM : 1][DUAL ? FN : 1]) {
 #pragma unroll
     for (int j = 0; j < KS; ++j)
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-          acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[j][fm], f.b[j][fn], acc[fm][fn],
-                                                               0, 0, 0);
+        for (int fn = 0; fn < FN; ++fn) {
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[j][fm], f.b[0][j][fn],
+                                                               acc[fm][fn], 0, 0, 0);
+          if constexpr (DUAL)
+            acc2[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[j][fm], f.b[1][j][fn],
+                                                                  acc2[fm][fn], 0, 0, 0);
+        }
   }
 
   static TA_DEVICE void run(const GemmArgs &p) {
@@ -342,7 +353,7 @@ struct GemmH16Pipe {
 
     // Per-thread source pointers of its direct loads (advanced per stage).
     const char *asrc[A_LD];
-    const char *bsrc[B_LD];
+    const char *bsrc[WAYS][B_LD];
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       const uint32_t q = i * T + tid, row = q / CPA, c = (q % CPA) ^ swz_a(row);
@@ -353,7 +364,11 @@ struct GemmH16Pipe {
     for (int i = 0; i < B_LD; ++i) {
       const uint32_t q = i * T + tid, row = q / CPR, c = (q % CPR) ^ swz_b(row);
       const uint32_t gn = min(n0 + 8 * c, p.n - 8);
-      bsrc[i] = reinterpret_cast<const char *>(B + ((uint64_t)klo * BK + row) * p.n + gn);
+      const uint64_t off = ((uint64_t)klo * BK + row) * p.n + gn;
+      bsrc[0][i] = reinterpret_cast<const char *>(B + off);
+      if constexpr (DUAL)
+        bsrc[1][i] = reinterpret_cast<const char *>(
+            static_cast<const _Float16 *>(p.b2) + (uint64_t)batch * p.stride_b + off);
     }
     const uint64_t b_step = (uint64_t)BK * p.n * 2;
 
@@ -365,10 +380,12 @@ struct GemmH16Pipe {
         asrc[i] += BK * 2;
       }
 #pragma unroll
-      for (int i = 0; i < B_LD; ++i) {
-        load16(bsrc[i], base + A_BYTES + i * T * 16);
-        bsrc[i] += b_step;
-      }
+      for (int w = 0; w < WAYS; ++w)
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+          load16(bsrc[w][i], base + A_BYTES + w * B_BYTES + i * T * 16);
+          bsrc[w][i] += b_step;
+        }
     };
 
     // Per-lane LDS read offsets within a stage.
@@ -396,13 +413,17 @@ struct GemmH16Pipe {
         }
 
     f32x16 acc[FM][FN];
+    f32x16 acc2[DUAL ? FM : 1][DUAL ? FN : 1];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
+        for (int r = 0; r < 16; ++r) {
           acc[fm][fn][r] = 0.0f;
+          if constexpr (DUAL)
+            acc2[fm][fn][r] = 0.0f;
+        }
 
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
@@ -422,7 +443,7 @@ struct GemmH16Pipe {
           issue((kt + NS - 1) % NS);
         Frags f;
         read_frags(lds0 + (kt % NS) * STAGE, a_off, b_off, f);
-        mfmas(f, acc);
+        mfmas(f, acc, acc2);
       }
     } else {
     Frags fr[2];
@@ -449,7 +470,7 @@ struct GemmH16Pipe {
         issue((kt + NS - 1) % NS);
       if (kt + 1 < kts)
         read_frags(lds0 + ((kt + 1) % NS) * STAGE, a_off, b_off, nxt);
-      mfmas(cur, acc);
+      mfmas(cur, acc, acc2);
     };
     uint32_t kt = 0;
     for (; kt + 1 < kts; kt += 2) {
@@ -519,6 +540,19 @@ struct GemmH16Pipe {
       if (tid == 0)
         __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if constexpr (DUAL) {
+      // U = alpha * (A @ B2) first, to c2 with no epilogue; then the
+      // gate's fused epilogue, whose D = c2 reads U back.  Both stores map
+      // element (row, col) to the same thread, so each U value is read
+      // back by the thread that stored it.
+      GemmArgs pu = p;
+      pu.c = p.c2;
+      pu.flags = 0;
+      pu.act = TA_ACT_NONE;
+      pu.binary = TA_BIN_NONE;
+      ta_store_tile<WTM, WTN, FM, FN, T, false>(reinterpret_cast<float *>(smem), SMEM_BYTES / 4,
+                                                acc2, pu, lane, wave, wm, wn, m0, n0, batch, 0);
+    }
     ta_store_tile<WTM, WTN, FM, FN, T, C_F16>(reinterpret_cast<float *>(smem), SMEM_BYTES / 4, acc,
                                               p, lane, wave, wm, wn, m0, n0, batch, 0);
   }
@@ -546,16 +580,20 @@ TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
 // ta_cvt_f32_f16, f32 C with the fused epilogue), ta_gemm_a16_<tile>_lds
 // (f16 A, f16 C) and the split-K ta_gemm_h16sk_<tile> (as h16, k_splits
 // workgroups per tile).
-#define TA_GEMM_PIPE(NAME, BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF)                      \
+#define TA_GEMM_PIPE(NAME, BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF, DUAL)                \
   extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(GemmArgs p) {             \
     static_assert(64 * WGM * WGN == ta_h16_lds_threads(BM, BN), "host launch width");         \
-    GemmH16Pipe<BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF>::run(p);                        \
+    GemmH16Pipe<BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF, DUAL>::run(p);                  \
   }
 #define TA_GEMM_LDS(TAG, BM, BN, BK, WGM, WGN, NS, DBUF)                                      \
-  TA_GEMM_PIPE(ta_gemm_h16_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, false, false, DBUF)         \
-  TA_GEMM_PIPE(ta_gemm_a16_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, true, false, DBUF)
+  TA_GEMM_PIPE(ta_gemm_h16_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, false, false, DBUF, false)  \
+  TA_GEMM_PIPE(ta_gemm_a16_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, true, false, DBUF, false)
 #define TA_GEMM_SK(TAG, BM, BN, BK, WGM, WGN, NS)                                             \
-  TA_GEMM_PIPE(ta_gemm_h16sk_##TAG, BM, BN, BK, WGM, WGN, NS, false, true, true)
+  TA_GEMM_PIPE(ta_gemm_h16sk_##TAG, BM, BN, BK, WGM, WGN, NS, false, true, true, false)
+// SwiGLU pair in one pass: C = act(alpha * A @ B + bias) * U with
+// U = alpha * A @ B2 stored to c2 (A read once for both weight matrices).
+#define TA_GEMM_DUAL(TAG, BM, BN, BK, WGM, WGN, NS)                                           \
+  TA_GEMM_PIPE(ta_gemm_h16dual_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, false, false, true, true)
 
 // Stage counts and loop forms as measured fastest on the config-5 shapes
 // and 4096^3 (64 x 64: 11.9 us for 512x2048x2048; 128 x 64: 14.4 us for
@@ -570,6 +608,10 @@ TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4, true)
 TA_GEMM_SK(m64n128, 64, 128, 64, 2, 4, 4)
 TA_GEMM_SK(m128n64, 128, 64, 64, 4, 2, 4)
 TA_GEMM_SK(m128n128, 128, 128, 64, 2, 4, 4)
+TA_GEMM_DUAL(m128n128, 128, 128, 64, 2, 4, 3)
+TA_GEMM_DUAL(m128n64, 128, 64, 64, 4, 2, 4)
+TA_GEMM_DUAL(m64n128, 64, 128, 64, 2, 4, 3)
+TA_GEMM_DUAL(m64n64, 64, 64, 64, 2, 2, 4)
 #else
 TA_PIPE_TILES
 #endif

@@ -74,6 +74,11 @@ typedef struct GemmArgs {
   uint32_t k_splits;
   float *partial;
   uint32_t *counters;
+  // Dual SwiGLU launch (ta_gemm_h16dual_*): second weight matrix (same
+  // shape and strides as b) and the output U = alpha * A @ b2 goes to c2;
+  // the launch's own epilogue has binary Mul with d = c2.
+  const void *b2;
+  float *c2;
 } GemmArgs;
 
 // Fixed-order reduction of split-K partial planes:

@@ -362,8 +362,11 @@ struct ExecutorImpl {
     uint64_t n = 0;
   };
 
+  // `up` set: dual SwiGLU launch (ta_gemm_h16dual_*) computing `up`
+  // (plain) and `op` (gate with activation and Mul{d = up.C}) in one pass.
   void launch_gemm(const KernelSpec &s, const ResolvedMatmul &d, const MatmulOp &op,
-                   uint32_t splits, Scratch &scratch, CvtCache &cvt, hipStream_t stream) const {
+                   uint32_t splits, Scratch &scratch, CvtCache &cvt, hipStream_t stream,
+                   const MatmulOp *up = nullptr) const {
     void *splitk_scratch = scratch.splitk;
     GemmArgs a{};
     a.a = op.call.a->device_ptr();
@@ -435,6 +438,16 @@ struct ExecutorImpl {
       if (gz > 65535 || a.k_splits > 65535)
         fail("matmul grid exceeds the HIP launch limits");
       launch(s.symbol, (uint32_t)gx, a.k_splits, (uint32_t)gz, lds_threads, &a, stream);
+      return;
+    }
+    if (up) {
+      if (!lds || s.kind != KernelKind::GemmF16Mfma || !f16_dual_tile(s) || splits > 1)
+        fail("internal: dual f16w GEMM on an unsupported route");
+      a.b2 = up->call.b->device_ptr();
+      a.c2 = static_cast<float *>(up->call.c->device_ptr());
+      std::string sym = s.symbol;
+      sym.replace(0, std::strlen("ta_gemm_h16_"), "ta_gemm_h16dual_");
+      launch(sym + "_lds", (uint32_t)gx, 1, (uint32_t)gz, lds_threads, &a, stream);
       return;
     }
     const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
@@ -535,10 +548,15 @@ struct ExecutorImpl {
   // Dual SwiGLU fusion in a dependent graph: op i = x @ Wu (plain) and op
   // i+1 = act(x @ Wg [+ bias]) * C_i on the same decode GEMV route become
   // one launch that streams Wg and Wu together and writes both outputs.
+  // Same route for both ops: the decode GEMV (dual launch) or the
+  // pipelined f16w GEMM on a tile with a dual kernel (ta_gemm_h16dual_*).
   static bool fusable_pair(const MatmulOp &up, const OpPlan &pu, const MatmulOp &gate,
-                           const OpPlan &pg) {
-    if (pu.kernel != pg.kernel || !KERNEL_SPECS[pu.kernel].weights_f16() ||
-        !KERNEL_SPECS[pu.kernel].is_gemv() || pu.splitk2 || pg.splitk2)
+                           const OpPlan &pg, const ResolvedMatmul &d) {
+    if (pu.kernel != pg.kernel || !KERNEL_SPECS[pu.kernel].weights_f16() || pu.splitk2 ||
+        pg.splitk2)
+      return false;
+    const KernelSpec &s = KERNEL_SPECS[pu.kernel];
+    if (!s.is_gemv() && !(f16_dual_tile(s) && gemm_lds_ok(d)))
       return false;
     if (!up.epilogue.is_none() || up.call.accumulate || gate.call.accumulate ||
         up.has_decode_fusion() || gate.has_decode_fusion())
@@ -566,7 +584,7 @@ struct ExecutorImpl {
         continue;
       if (!std::getenv("TA_NO_MLP") && i + 2 < ops.size() && plans[i + 2].role == 0 &&
           res[i].batch == 1 && res[i].m <= mlp_max_rows() &&
-          fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1]) &&
+          fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1], res[i]) &&
           mlp_tail_ok(ops[i], ops[i + 1], plans[i + 1], ops[i + 2], plans[i + 2])) {
         plans[i].role = 3;
         plans[i].mlp_layers = 1;
@@ -575,7 +593,7 @@ struct ExecutorImpl {
         i += 2;
         continue;
       }
-      if (fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1])) {
+      if (fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1], res[i])) {
         plans[i].role = 1;
         plans[i + 1].role = 2;
         ++i;
@@ -841,7 +859,8 @@ struct ExecutorImpl {
       if (s.is_gemv())
         launch_gemv(s, res[i], ops[i], p.role == 2 ? &ops[i - 1] : nullptr, scratch, stream);
       else
-        launch_gemm(s, res[i], ops[i], p.splitk2.value_or(1), scratch, cvt, stream);
+        launch_gemm(s, res[i], ops[i], p.splitk2.value_or(1), scratch, cvt, stream,
+                    p.role == 2 ? &ops[i - 1] : nullptr);
     }
   }
 

@@ -64,6 +64,7 @@ bool kernel_supports(const KernelSpec &spec, const ResolvedMatmul &dims);
 bool gemm_lds_ok(const ResolvedMatmul &dims);
 bool f32_mi16_ok(const ResolvedMatmul &dims, uint32_t tile_m, uint32_t tile_n, uint32_t planes);
 uint32_t mi16_threads(uint32_t tile_m);
+bool f16_dual_tile(const KernelSpec &spec);
 std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims);
 size_t registry_index(const char *name);
 

@@ -110,6 +110,14 @@ uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 // Shapes the pipelined f16-MFMA kernels (`_lds` code objects) take: whole
 // 64-deep K stages and 16-byte B rows.
 bool gemm_lds_ok(const ResolvedMatmul &d) { return d.k > 0 && d.k % 64 == 0 && d.n % 8 == 0; }
+// Pipelined f16w tiles that also have a dual (SwiGLU pair) kernel,
+// ta_gemm_h16dual_<tile>_lds.
+bool f16_dual_tile(const KernelSpec &s) {
+  return s.kind == KernelKind::GemmF16Mfma &&
+         ((s.tile_m == 128 && (s.tile_n == 128 || s.tile_n == 64)) ||
+          (s.tile_m == 64 && (s.tile_n == 128 || s.tile_n == 64)));
+}
+
 // Threads of the _mi16 kernel of a tile height (32: 128, else 256).
 uint32_t mi16_threads(uint32_t tile_m) { return tile_m == 32 ? 128u : 256u; }
 

@@ -256,6 +256,50 @@ def test_f16_mfma_pipelined_epilogues(ta, ctx, oracle, name, epi):
     check_f16_mfma(kex.download(c), refs, k, oracle)
 
 
+@pytest.mark.parametrize("name", [None, "f16w_mfma_m128n128", "f16w_mfma_m128n64", "f16w_mfma_m64n128",
+                                  "f16w_mfma_m64n64"])
+@pytest.mark.parametrize("bt,m,n,k", [(1, 300, 264, 192), (2, 128, 256, 128), (1, 512, 5632, 2048)])
+def test_f16w_dual_swiglu_pair(ta, ctx, ex, oracle, monkeypatch, name, bt, m, n, k):
+    """A SwiGLU pair in an op graph, up = alpha * x @ Wu then
+    h = SiLU(alpha * x @ Wg + bias) * up, runs as one dual launch on the
+    pipelined f16w route (ta_gemm_h16dual_*: x read once for both weight
+    matrices).  Both outputs must equal the unfused ops' bits (same K order
+    per element), and match the oracle (h on the GPU's own up)."""
+    if name is not None and m * n * k > 1 << 26:
+        pytest.skip("forced tiles on the small shapes only")
+    kex = ex if name is None else ta.Executor(ctx, kernel_selection=name, tune=False)
+    hx = oracle.fill_det(bt * m * k, 7400)
+    hwu, hwg = oracle.fill_normal(k * n, 7401, 0.05), oracle.fill_normal(k * n, 7402, 0.05)
+    hbias = oracle.fill_det(n, 7403)
+    x = kex.tensor_from(hx, shape=[bt, m, k])
+    wu, wg = kex.tensor_from(hwu, shape=[k, n], f16=True), kex.tensor_from(hwg, shape=[k, n], f16=True)
+    bias = kex.tensor_from(hbias, shape=[n])
+    up, h, up2, h2 = (kex.tensor([bt, m, n]) for _ in range(4))
+    pair = lambda u, g: [ta.MatmulOp(x, wu, u, alpha=1.25),
+                         ta.MatmulOp(x, wg, g, alpha=1.25, epilogue=ta.Epilogue(
+                             bias=bias, activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=u))]
+    kex.run_op_graph(pair(up, h))
+    monkeypatch.setenv("TA_NO_FUSE", "1")
+    kex.run_op_graph(pair(up2, h2))
+    monkeypatch.delenv("TA_NO_FUSE")
+    got_up, got_h = kex.download(up), kex.download(h)
+    np.testing.assert_array_equal(got_up, kex.download(up2))
+    np.testing.assert_array_equal(got_h, kex.download(h2))
+    if m * n * k <= 1 << 26:  # the full config-5 shape: bits against the unfused ops only
+        _dual_oracle_check(oracle, hx, hwu, hwg, hbias, got_up, got_h, bt, m, n, k)
+    # the fused launch repeats its bits
+    kex.run_op_graph(pair(up, h))
+    np.testing.assert_array_equal(kex.download(h), got_h)
+
+
+def _dual_oracle_check(oracle, hx, hwu, hwg, hbias, got_up, got_h, bt, m, n, k):
+    hwb = np.tile(hwu, bt)
+    check_f16_mfma(got_up, f16_mfma_refs(hx, hwb, bt, m, n, k, oracle, alpha=1.25), k, oracle)
+    refs_h = f16_mfma_refs(hx, np.tile(hwg, bt), bt, m, n, k, oracle, alpha=1.25, bias=hbias, act=2,
+                           binary=2, d=got_up.reshape(-1))
+    check_f16_mfma(got_h, refs_h, k, oracle)
+
+
 def test_f16_mfma_batched_alpha_accumulate(ta, ex, oracle):
     """f16.rs:791-817: batched + alpha + accumulate."""
     bt, m, n, k = 2, 256, 384, 256
