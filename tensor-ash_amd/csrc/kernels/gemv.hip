@@ -48,6 +48,18 @@
 #ifndef TA_GEMV_SENTINEL_MIN_ROWS
 #define TA_GEMV_SENTINEL_MIN_ROWS 4
 #endif
+#ifndef TA_MLP_ISSUE_BATCH_M1
+#define TA_MLP_ISSUE_BATCH_M1 2
+#endif
+#ifndef TA_MLP_ISSUE_BATCH_M2
+#define TA_MLP_ISSUE_BATCH_M2 2
+#endif
+#ifndef TA_MLP_ISSUE_BATCH_M4
+#define TA_MLP_ISSUE_BATCH_M4 0
+#endif
+#ifndef TA_MLP_ISSUE_BATCH_M8
+#define TA_MLP_ISSUE_BATCH_M8 2
+#endif
 
 namespace {
 
@@ -153,6 +165,12 @@ struct Gemv {
   static constexpr int RPW = RPI * kWaves;  // rows per workgroup step
   static constexpr int EB = WF32 ? 4 : 2;   // bytes per weight element
   static constexpr int kUnroll = UNROLL;    // loads per weight matrix per group
+  // Decode-MLP units: weight loads per issue batch (at most two batches
+  // outstanding while the window is fetched; 0 = all at once).
+  static constexpr int kIssueBatch = MR == 1   ? TA_MLP_ISSUE_BATCH_M1
+                                     : MR == 2 ? TA_MLP_ISSUE_BATCH_M2
+                                     : MR == 4 ? TA_MLP_ISSUE_BATCH_M4
+                                               : TA_MLP_ISSUE_BATCH_M8;
   static constexpr int OUTS = WAYS * MR * TW; // outputs of one tile, all ways
   static constexpr int OPT = (OUTS + kThreads - 1) / kThreads;
   // The X window's LDS is reused to stage the partials of all K windows
@@ -244,12 +262,22 @@ struct Gemv {
     auto issue = [&](uint32_t kb, uint64_t (&raw)[WAYS][kUnroll]) {
       if constexpr (EXACT) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u)
+        for (int u = 0; u < kUnroll; ++u) {
 #pragma unroll
           for (int w = 0; w < WAYS; ++w)
             raw[w][u] = __builtin_nontemporal_load(
                 reinterpret_cast<__attribute__((address_space(1))) const uint64_t *>(
                     uniform_ptr(wbase[w] + (uint64_t)(k0 + kb + u * RPW) * row_stride) + lane_b));
+          // Decode-MLP units keep at most 2 * kIssueBatch of their loads
+          // outstanding: every resident unit fetching its whole window at
+          // once queues ~64 MB at the memory controllers, and each hand-off
+          // poll then waits behind that queue.  The window still lands in
+          // registers long before the unit's input is published.
+          const int issued = (u + 1) * WAYS;
+          if (kIssueBatch > 0 && issued % kIssueBatch == 0 && issued >= 2 * kIssueBatch &&
+              issued < kUnroll * WAYS)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kIssueBatch) : "memory");
+        }
         return;
       }
 #pragma unroll
