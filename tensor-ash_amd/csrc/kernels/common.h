@@ -144,9 +144,20 @@ TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &
           }
         }
         *reinterpret_cast<f32x4 *>(&p.c[base]) = o;
+        if (p.c16) {
+          f16x4 h;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            h[c] = (_Float16)o[c];
+          *reinterpret_cast<f16x4 *>(reinterpret_cast<_Float16 *>(p.c16) + base) = h;
+        }
       } else {
-        for (int c = 0; c < 4 && col + c < p.n; ++c)
-          p.c[base + c] = S > 1 ? p.alpha * v[c] : ta_epilogue(v[c], p, base + c, col + c, batch);
+        for (int c = 0; c < 4 && col + c < p.n; ++c) {
+          const float r = S > 1 ? p.alpha * v[c] : ta_epilogue(v[c], p, base + c, col + c, batch);
+          p.c[base + c] = r;
+          if (p.c16)
+            reinterpret_cast<_Float16 *>(p.c16)[base + c] = (_Float16)r;
+        }
       }
     }
     __syncthreads();

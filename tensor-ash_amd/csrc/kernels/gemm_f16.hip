@@ -547,6 +547,7 @@ struct GemmH16Pipe {
       // back by the thread that stored it.
       GemmArgs pu = p;
       pu.c = p.c2;
+      pu.c16 = nullptr;
       pu.flags = 0;
       pu.act = TA_ACT_NONE;
       pu.binary = TA_BIN_NONE;

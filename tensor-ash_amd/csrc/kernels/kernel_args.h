@@ -79,6 +79,10 @@ typedef struct GemmArgs {
   // the launch's own epilogue has binary Mul with d = c2.
   const void *b2;
   float *c2;
+  // Optional f16 (RNE) copy of the final C values, same layout as c (f32-C
+  // launches without split planes); null = none.  Lets a following f16w
+  // GEMM that reads this C as A skip its conversion pre-pass.
+  uint16_t *c16;
 } GemmArgs;
 
 // Fixed-order reduction of split-K partial planes:

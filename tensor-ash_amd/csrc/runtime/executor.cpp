@@ -42,6 +42,10 @@ struct Scratch {
   // no other kernel and zeroed when allocated or reset.
   void *mlp = nullptr;
   uint64_t mlp_bytes = 0;
+  // f16 copy of a dual SwiGLU launch's output for the next op's A (kept
+  // apart from the split-K region, which holds the dual launch's own A).
+  void *shadow = nullptr;
+  uint64_t shadow_bytes = 0;
 
   void release() {
     if (splitk)
@@ -52,9 +56,20 @@ struct Scratch {
       (void)hipFree(counters);
     if (mlp)
       (void)hipFree(mlp);
-    splitk = partial = mlp = nullptr;
+    if (shadow)
+      (void)hipFree(shadow);
+    splitk = partial = mlp = shadow = nullptr;
     counters = nullptr;
-    splitk_bytes = partial_bytes = counters_len = mlp_bytes = 0;
+    splitk_bytes = partial_bytes = counters_len = mlp_bytes = shadow_bytes = 0;
+  }
+  void ensure_shadow(uint64_t bytes) {
+    if (bytes <= shadow_bytes)
+      return;
+    if (shadow)
+      hip_check(hipFree(shadow), "hipFree");
+    shadow = nullptr;
+    hip_check(hipMalloc(&shadow, bytes), "hipMalloc (f16 output copy)");
+    shadow_bytes = bytes;
   }
   void ensure_mlp(uint64_t bytes) {
     if (bytes <= mlp_bytes)
@@ -153,8 +168,9 @@ struct OpPlan {
 };
 
 struct ScratchNeed {
-  uint64_t splitk = 0, partial = 0, counters = 0, mlp = 0;
+  uint64_t splitk = 0, partial = 0, counters = 0, mlp = 0, shadow = 0;
   void merge(const ScratchNeed &o) {
+    shadow = std::max(shadow, o.shadow);
     splitk = std::max(splitk, o.splitk);
     partial = std::max(partial, o.partial);
     counters = std::max(counters, o.counters);
@@ -360,13 +376,36 @@ struct ExecutorImpl {
     const void *buffer = nullptr;
     const void *src = nullptr;
     uint64_t n = 0;
+    void *base = nullptr;              // where the copy lives
+    size_t producer = SIZE_MAX;        // op whose epilogue wrote it, if any
   };
+
+  // Does op i (the gate of a dual SwiGLU launch) feed op i + 1 as A on the
+  // f16w pipelined route?  Then the dual launch also writes an f16 copy of
+  // its output (the conversion pre-pass's values: the same RNE rounding of
+  // the same f32 results) and op i + 1 reads that instead of converting.
+  static bool f16_copy_feeds_next(const std::vector<MatmulOp> &ops,
+                                  const std::vector<ResolvedMatmul> &res,
+                                  const std::vector<OpPlan> &plans, size_t i) {
+    const size_t j = i + 1;
+    if (j >= ops.size() || plans[i].role != 2 || plans[j].role != 0 || plans[j].splitk2 ||
+        KERNEL_SPECS[plans[i].kernel].is_gemv())
+      return false;
+    const KernelSpec &s = KERNEL_SPECS[plans[j].kernel];
+    if ((s.kind != KernelKind::GemmF16Mfma && s.kind != KernelKind::GemmF16Sk) ||
+        !gemm_lds_ok(res[j]))
+      return false;
+    const Tensor *c = ops[i].call.c, *a = ops[j].call.a;
+    const uint64_t a_elems = (res[j].batch_stride_a ? (uint64_t)res[j].batch : 1) * res[j].m * res[j].k;
+    return a->buffer_id() == c->buffer_id() && a->device_ptr() == c->device_ptr() &&
+           a_elems == (uint64_t)res[i].batch * res[i].m * res[i].n;
+  }
 
   // `up` set: dual SwiGLU launch (ta_gemm_h16dual_*) computing `up`
   // (plain) and `op` (gate with activation and Mul{d = up.C}) in one pass.
   void launch_gemm(const KernelSpec &s, const ResolvedMatmul &d, const MatmulOp &op,
                    uint32_t splits, Scratch &scratch, CvtCache &cvt, hipStream_t stream,
-                   const MatmulOp *up = nullptr) const {
+                   const MatmulOp *up = nullptr, uint16_t *c16 = nullptr) const {
     void *splitk_scratch = scratch.splitk;
     GemmArgs a{};
     a.a = op.call.a->device_ptr();
@@ -418,9 +457,9 @@ struct ExecutorImpl {
       const void *buf = op.call.a->buffer_id();
       if (!(cvt.buffer == buf && cvt.src == cv.src && cvt.n == cv.n)) {
         launch("ta_cvt_f32_f16", (uint32_t)blocks, 1, 1, 256, &cv, stream);
-        cvt = CvtCache{buf, cv.src, cv.n};
+        cvt = CvtCache{buf, cv.src, cv.n, splitk_scratch, SIZE_MAX};
       }
-      a.a = splitk_scratch;
+      a.a = cvt.base;
     } else if (splits > 1) {
       cvt = CvtCache{}; // the partial planes overwrite the f16 copy
     }
@@ -445,6 +484,7 @@ struct ExecutorImpl {
         fail("internal: dual f16w GEMM on an unsupported route");
       a.b2 = up->call.b->device_ptr();
       a.c2 = static_cast<float *>(up->call.c->device_ptr());
+      a.c16 = c16;
       std::string sym = s.symbol;
       sym.replace(0, std::strlen("ta_gemm_h16_"), "ta_gemm_h16dual_");
       launch(sym + "_lds", (uint32_t)gx, 1, (uint32_t)gz, lds_threads, &a, stream);
@@ -691,6 +731,11 @@ struct ExecutorImpl {
         need.merge(m);
       } else if (plans[i].role != 1 && plans[i].role != 4) {
         need.merge(scratch_need(res[i], plans[i]));
+        if (plans[i].role == 2 && !KERNEL_SPECS[plans[i].kernel].is_gemv()) {
+          ScratchNeed c; // f16 copy of a dual launch's output (f16_copy_feeds_next)
+          c.shadow = (uint64_t)res[i].batch * res[i].m * res[i].n * 2;
+          need.merge(c);
+        }
       }
     }
     return need;
@@ -841,7 +886,8 @@ struct ExecutorImpl {
     for (size_t i = 0; i < ops.size(); ++i) {
       const OpPlan &p = plans[i];
       // the cached f16 copy of A is stale once an op writes A's buffer
-      if (i > 0 && cvt.buffer &&
+      // (except the op whose epilogue wrote the copy)
+      if (i > 0 && cvt.buffer && cvt.producer != i - 1 &&
           (ops[i - 1].call.c->buffer_id() == cvt.buffer ||
            (ops[i - 1].store.dst && ops[i - 1].store.dst->buffer_id() == cvt.buffer)))
         cvt = CvtCache{};
@@ -858,7 +904,14 @@ struct ExecutorImpl {
       check_fusions(s, ops[i], res[i]);
       if (s.is_gemv())
         launch_gemv(s, res[i], ops[i], p.role == 2 ? &ops[i - 1] : nullptr, scratch, stream);
-      else
+      else if (p.role == 2 && f16_copy_feeds_next(ops, res, plans, i)) {
+        if (scratch.shadow_bytes < (uint64_t)res[i].batch * res[i].m * res[i].n * 2)
+          fail("internal: f16 output copy scratch not reserved");
+        uint16_t *c16 = static_cast<uint16_t *>(scratch.shadow);
+        launch_gemm(s, res[i], ops[i], 1, scratch, cvt, stream, &ops[i - 1], c16);
+        cvt = CvtCache{ops[i].call.c->buffer_id(), ops[i].call.c->device_ptr(),
+                       (uint64_t)res[i].batch * res[i].m * res[i].n, c16, i};
+      } else
         launch_gemm(s, res[i], ops[i], p.splitk2.value_or(1), scratch, cvt, stream,
                     p.role == 2 ? &ops[i - 1] : nullptr);
     }
@@ -871,6 +924,7 @@ struct ExecutorImpl {
     ScratchNeed need = total_need(res, plans);
     slot->scratch.ensure(need.splitk, need.partial, need.counters);
     slot->scratch.ensure_mlp(need.mlp);
+    slot->scratch.ensure_shadow(need.shadow);
     return submit_on(slot, ops, res, plans, slot->scratch);
   }
   // run_ops with several independent ops (src/executor/dispatch.rs:55-60:
@@ -923,6 +977,7 @@ struct ExecutorImpl {
       Scratch &sc = l == 0 ? slot->scratch : slot->side[l - 1].scratch;
       sc.ensure(need.splitk, need.partial, need.counters);
       sc.ensure_mlp(need.mlp);
+      sc.ensure_shadow(need.shadow);
     }
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
     hip_check(hipEventRecord(slot->fork, slot->stream), "hipEventRecord");
@@ -1063,6 +1118,7 @@ struct ExecutorImpl {
     const ScratchNeed need = exec_need(steps);
     slot->scratch.ensure(need.splitk, need.partial, need.counters);
     slot->scratch.ensure_mlp(need.mlp);
+    slot->scratch.ensure_shadow(need.shadow);
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
     record_exec(steps, slot->scratch, slot->host_status, slot->stream);
     hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
@@ -1435,7 +1491,8 @@ struct ExecutorImpl {
     Scratch scratch;
     scratch.ensure(need.splitk, need.partial, need.counters);
     scratch.ensure_mlp(need.mlp);
-    p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters, scratch.mlp};
+    scratch.ensure_shadow(need.shadow);
+    p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters, scratch.mlp, scratch.shadow};
     p->mlp_scratch_ = scratch.mlp;
     p->mlp_bytes_ = scratch.mlp_bytes;
     if (mlp)

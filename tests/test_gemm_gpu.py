@@ -263,8 +263,10 @@ def test_f16w_dual_swiglu_pair(ta, ctx, ex, oracle, monkeypatch, name, bt, m, n,
     """A SwiGLU pair in an op graph, up = alpha * x @ Wu then
     h = SiLU(alpha * x @ Wg + bias) * up, runs as one dual launch on the
     pipelined f16w route (ta_gemm_h16dual_*: x read once for both weight
-    matrices).  Both outputs must equal the unfused ops' bits (same K order
-    per element), and match the oracle (h on the GPU's own up)."""
+    matrices), which also leaves an f16 copy of h for the down-projection
+    that follows.  All outputs must equal the unfused ops' bits (same K
+    order per element, same rounding of h), and match the oracle (h on the
+    GPU's own up)."""
     if name is not None and m * n * k > 1 << 26:
         pytest.skip("forced tiles on the small shapes only")
     kex = ex if name is None else ta.Executor(ctx, kernel_selection=name, tune=False)
@@ -275,21 +277,32 @@ def test_f16w_dual_swiglu_pair(ta, ctx, ex, oracle, monkeypatch, name, bt, m, n,
     wu, wg = kex.tensor_from(hwu, shape=[k, n], f16=True), kex.tensor_from(hwg, shape=[k, n], f16=True)
     bias = kex.tensor_from(hbias, shape=[n])
     up, h, up2, h2 = (kex.tensor([bt, m, n]) for _ in range(4))
-    pair = lambda u, g: [ta.MatmulOp(x, wu, u, alpha=1.25),
-                         ta.MatmulOp(x, wg, g, alpha=1.25, epilogue=ta.Epilogue(
-                             bias=bias, activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=u))]
-    kex.run_op_graph(pair(up, h))
+    # down-projection reading h as A: takes the dual launch's f16 copy of h
+    # instead of converting h (same RNE rounding of the same values)
+    k2 = 2048 if n == 5632 else 128
+    wd = kex.tensor_from(oracle.fill_normal(n * k2, 7404, 0.05), shape=[n, k2], f16=True)
+    res = kex.tensor_from(oracle.fill_det(bt * m * k2, 7405), shape=[bt, m, k2])
+    y, y2 = kex.tensor([bt, m, k2]), kex.tensor([bt, m, k2])
+    pair = lambda u, g, yy: [ta.MatmulOp(x, wu, u, alpha=1.25),
+                             ta.MatmulOp(x, wg, g, alpha=1.25, epilogue=ta.Epilogue(
+                                 bias=bias, activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=u)),
+                             ta.MatmulOp(g, wd, yy, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=res,
+                                                                         beta=1.0))]
+    kex.run_op_graph(pair(up, h, y))
     monkeypatch.setenv("TA_NO_FUSE", "1")
-    kex.run_op_graph(pair(up2, h2))
+    kex.run_op_graph(pair(up2, h2, y2))
     monkeypatch.delenv("TA_NO_FUSE")
     got_up, got_h = kex.download(up), kex.download(h)
     np.testing.assert_array_equal(got_up, kex.download(up2))
     np.testing.assert_array_equal(got_h, kex.download(h2))
+    np.testing.assert_array_equal(kex.download(y), kex.download(y2))
     if m * n * k <= 1 << 26:  # the full config-5 shape: bits against the unfused ops only
         _dual_oracle_check(oracle, hx, hwu, hwg, hbias, got_up, got_h, bt, m, n, k)
     # the fused launch repeats its bits
-    kex.run_op_graph(pair(up, h))
+    got_y = kex.download(y)
+    kex.run_op_graph(pair(up, h, y))
     np.testing.assert_array_equal(kex.download(h), got_h)
+    np.testing.assert_array_equal(kex.download(y), got_y)
 
 
 def _dual_oracle_check(oracle, hx, hwu, hwg, hbias, got_up, got_h, bt, m, n, k):
