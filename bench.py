@@ -268,8 +268,10 @@ def prefill_layer(ta, ex, iters=10):
     out["layer_gemms"] = dict(us=total_ns / 1e3, tflops=total_flops / total_ns / 1e3,
                               note="sum of the five GEMMs, each its own ta_run_ops call",
                               roofline=time_roofline(total_flops, total_bytes, total_ns * 1e-9, PEAK_FP16_MFMA))
-    # The layer as a prefill runs it: the five GEMMs in one submission (one
-    # event pair; the f16 copy of x is made once for QKV, up and gate).
+    # The layer as a prefill runs it: the five GEMMs in one dependent op
+    # graph (one event pair).  up and gate run as one dual launch, which
+    # also leaves the f16 copy of h that down reads; x is converted for QKV
+    # and again for up/gate (O's conversion of attn sits between them).
     layer = [op for ops in cases.values() for op in ops]
     for _ in range(3):
         ex.run_op_graph(layer)
