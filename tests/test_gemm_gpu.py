@@ -305,6 +305,36 @@ def test_f16w_dual_swiglu_pair(ta, ctx, ex, oracle, monkeypatch, name, bt, m, n,
     np.testing.assert_array_equal(kex.download(y), got_y)
 
 
+def test_f16w_dual_swiglu_prepared_graph_replays(ta, ex, oracle):
+    """The prefill SwiGLU triple (dual up/gate launch leaving h's f16 copy,
+    down reading it) captured as one hipGraph and replayed five times, with
+    the outputs cleared and eager work between replays: every replay equals
+    the eager run."""
+    m, hid, ffn = 512, 512, 1408
+    x = ex.tensor_from(oracle.fill_det(m * hid, 7501), shape=[m, hid])
+    wu = ex.tensor_from(oracle.fill_normal(hid * ffn, 7502, 0.05), shape=[hid, ffn], f16=True)
+    wg = ex.tensor_from(oracle.fill_normal(hid * ffn, 7503, 0.05), shape=[hid, ffn], f16=True)
+    wd = ex.tensor_from(oracle.fill_normal(ffn * hid, 7504, 0.05), shape=[ffn, hid], f16=True)
+    res = ex.tensor_from(oracle.fill_det(m * hid, 7505), shape=[m, hid])
+    up, h, y = ex.tensor([m, ffn]), ex.tensor([m, ffn]), ex.tensor([m, hid])
+    ops = [ta.MatmulOp(x, wu, up),
+           ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up)),
+           ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=res, beta=1.0))]
+    ex.run_op_graph(ops)
+    eager = [ex.download(t).copy() for t in (up, h, y)]
+    p = ex.prepare_op_graph(ops)
+    other_a = ex.tensor_from(oracle.fill_det(m * hid, 7506), shape=[m, hid])
+    other_c = ex.tensor([m, ffn])
+    for _ in range(5):
+        for t, e in zip((up, h, y), eager):
+            ex.upload(t, np.zeros(e.size, np.float32))
+        p.run()
+        for t, e in zip((up, h, y), eager):
+            np.testing.assert_array_equal(ex.download(t), e)
+        ex.run_ops([ta.MatmulOp(other_a, wu, other_c)])  # eager work on the same executor between replays
+    p.close()
+
+
 def _dual_oracle_check(oracle, hx, hwu, hwg, hbias, got_up, got_h, bt, m, n, k):
     hwb = np.tile(hwu, bt)
     check_f16_mfma(got_up, f16_mfma_refs(hx, hwb, bt, m, n, k, oracle, alpha=1.25), k, oracle)
