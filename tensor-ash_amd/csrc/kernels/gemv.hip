@@ -156,7 +156,12 @@ TA_DEVICE uint32_t poll_sentinels(const uint64_t *words, uint32_t first_tile, ui
   }
 }
 
-template <int MR, bool DUAL, int TW, bool WF32, int MODE, int XROWS, int UNROLL = 16>
+// COH (persistent GEMV chain): X, the normed-A row and D are read, and Y
+// is written, with agent-scope accesses, so a job may read what an earlier
+// job of the same launch wrote on another XCD once a grid barrier (no
+// cache-wide fences) has passed.
+template <int MR, bool DUAL, int TW, bool WF32, int MODE, int XROWS, int UNROLL = 16,
+          bool COH = false>
 struct Gemv {
   static constexpr int WAYS = DUAL ? 2 : 1;
   static constexpr int CPL = WF32 ? 2 : 4;  // columns per lane (8-byte load)
@@ -364,7 +369,7 @@ struct Gemv {
       for (int j = 0; j < XPT; ++j) {
         bool ok;
         const uint64_t xi = x_index(j, ok);
-        xr[j] = p.x[xi];
+        xr[j] = COH ? coherent_load(p.x + xi) : p.x[xi];
         xr[j] = ok ? xr[j] : 0.0f;
       }
       issue(0, cur);
@@ -708,7 +713,7 @@ struct Gemv {
       const float *row = p.x + (uint64_t)m * p.k;
       float ss = 0.0f;
       for (uint32_t kk = tid; kk < p.k; kk += kThreads) {
-        const float a = row[kk];
+        const float a = COH ? coherent_load(row + kk) : row[kk];
         ss = fmaf(a, a, ss);
       }
       sm.xs[tid] = ss;
@@ -890,7 +895,7 @@ struct Gemv {
         if (o >= OUTS || m >= p.rows || c >= p.n)
           continue;
         const uint64_t yi = (uint64_t)m * p.n + c;
-        constexpr bool kCoherent = MODE == kConsumer;
+        constexpr bool kCoherent = MODE == kConsumer || COH;
         auto rd = [&](const float *q) { return kCoherent ? coherent_load(q) : *q; };
         float v = p.alpha * part[i];
         if (p.flags & TA_FLAG_ACCUMULATE)
@@ -969,6 +974,92 @@ template <int MR> struct DecodeMlp {
 };
 
 } // namespace
+
+namespace {
+// The row-major f16 decode GEMV at one row (ta_gemv_f16_t64_m1's unit).
+using ChainGemv =
+    Gemv<1, false, 64, false, kStandalone, standalone_rows<1>(), standalone_unroll<1>(), true>;
+
+// Grid barrier of the chain: every thread waits for its agent-scope
+// (write-through) output stores to complete, thread 0 reads the
+// generation, waits for that value, counts the workgroup in; the last to
+// arrive resets the count and advances the generation, the others poll it.
+// Readers use agent-scope loads, so no cache-wide fence is needed (an
+// agent-scope fence writes back and invalidates the whole L2 of the XCD,
+// which measured ~40 us per barrier here).  Every workgroup of the launch arrives (a workgroup not yet
+// resident waits only for CUs held by kernels that finish on their own),
+// so the bound is a safety net: past it the wait raises the host-visible
+// status word and the workgroup stops.
+TA_DEVICE bool chain_barrier(const GemvChainArgs &c, uint32_t &flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t *count = c.barrier, *gen = c.barrier + TA_GEMV_COUNTER_STRIDE;
+    uint32_t g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(g0) : : "memory");
+    uint32_t ok = 1;
+    if (__hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        gridDim.x - 1) {
+      __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gen, g0 + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      for (uint32_t polls = 0;
+           __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0;) {
+        if (++polls >= c.spin_limit) {
+          __hip_atomic_store(c.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    flag = ok;
+  }
+  __syncthreads();
+  return flag != 0;
+}
+} // namespace
+
+extern "C" __global__ __launch_bounds__(kThreads) void
+ta_gemv_chain_f16_m1(GemvChainArgs c) {
+  __shared__ __attribute__((aligned(16))) ChainGemv::Smem sm;
+  __shared__ uint32_t flag;
+  for (uint32_t j0 = 0; j0 < c.n_jobs;) {
+    uint32_t j1 = j0;
+    while (j1 + 1 < c.n_jobs && !((c.sync_after >> j1) & 1u))
+      ++j1;
+    // Units of the group's jobs, laid end to end (constant indices into
+    // the argument arrays: no private copy of them).
+    uint32_t first[TA_GEMV_CHAIN_MAX_JOBS], total = 0;
+#pragma unroll
+    for (int q = 0; q < TA_GEMV_CHAIN_MAX_JOBS; ++q) {
+      first[q] = total;
+      if ((uint32_t)q >= j0 && (uint32_t)q <= j1)
+        total += c.units[q];
+    }
+    for (uint32_t u = blockIdx.x; u < total; u += gridDim.x) {
+      uint32_t j = j0;
+#pragma unroll
+      for (int q = 1; q < TA_GEMV_CHAIN_MAX_JOBS; ++q)
+        if ((uint32_t)q > j0 && (uint32_t)q <= j1 && u >= first[q])
+          j = q;
+      uint32_t lu = u;
+#pragma unroll
+      for (int q = 0; q < TA_GEMV_CHAIN_MAX_JOBS; ++q)
+        if ((uint32_t)q == j)
+          lu = u - first[q];
+      const GemvArgs &p = c.job[j];
+      const uint32_t tiles = (p.n + 63) / 64;
+      ChainGemv::unit(p, lu % tiles, lu / tiles, sm, nullptr, 0, &c.fu[j]);
+      __syncthreads(); // the next unit reuses the LDS
+    }
+    if (j1 + 1 >= c.n_jobs)
+      break;
+    if (!chain_barrier(c, flag))
+      return;
+    j0 = j1 + 1;
+  }
+}
 
 #define TA_GEMV(NAME, MR, DUAL, TW, WF32)                                          \
   extern "C" __global__ __launch_bounds__(kThreads) void NAME(GemvArgs p,          \

@@ -165,6 +165,28 @@ typedef struct GemvFusion {
   uint64_t table_len, dst_len;
 } GemvFusion;
 
+// Persistent GEMV chain (ta_gemv_chain_f16_m1; the reference's GemvChain,
+// src/executor/elementwise/gemv_chain.rs): up to TA_GEMV_CHAIN_MAX_JOBS
+// M = 1 GEMVs with row-major f16 weights (64-column tiles) in one launch.  Jobs run in
+// groups: consecutive jobs without a data hazard share one grid-stride
+// space of units (tile, K window), and a group that a later job depends on
+// (bit j of sync_after: the group ending at job j) is followed by a grid
+// barrier.  A unit is exactly a standalone GEMV workgroup (same K windows,
+// same fixed-order window reduction through job[j].partial / .counters,
+// same epilogue), so the results equal the jobs' standalone launches.
+#define TA_GEMV_CHAIN_MAX_JOBS 8
+typedef struct GemvChainArgs {
+  GemvArgs job[TA_GEMV_CHAIN_MAX_JOBS];
+  GemvFusion fu[TA_GEMV_CHAIN_MAX_JOBS];
+  uint32_t units[TA_GEMV_CHAIN_MAX_JOBS]; // ceil(n / 64) tiles * kchunks
+  uint32_t n_jobs;
+  uint32_t sync_after;
+  uint32_t spin_limit; // barrier polls before a wait gives up
+  uint32_t pad;
+  uint32_t *barrier;   // [2 * TA_GEMV_COUNTER_STRIDE]: arrivals, generation (zeroed once)
+  uint32_t *status;    // host-mapped; set to 1 if a wait gave up (results invalid)
+} GemvChainArgs;
+
 // ---- model ops (ta_softmax_rows, ta_rms_norm, ta_layer_norm, ta_rope,
 // ta_copy_strided; src/executor/elementwise/ops.rs semantics) ----
 

@@ -9,6 +9,7 @@
 // sees every earlier op's writes.
 #include <algorithm>
 #include <atomic>
+#include <cctype>
 #include <chrono>
 #include <condition_variable>
 #include <cstdio>
@@ -46,6 +47,11 @@ struct Scratch {
   // apart from the split-K region, which holds the dual launch's own A).
   void *shadow = nullptr;
   uint64_t shadow_bytes = 0;
+  // Grid-barrier words of the persistent GEMV chain (arrival count,
+  // generation; zeroed once, the count returns to zero after every
+  // barrier).  Kept apart from `counters`, whose tile counters must all
+  // read zero between launches.
+  uint32_t *barrier = nullptr;
 
   void release() {
     if (splitk)
@@ -58,9 +64,18 @@ struct Scratch {
       (void)hipFree(mlp);
     if (shadow)
       (void)hipFree(shadow);
+    if (barrier)
+      (void)hipFree(barrier);
     splitk = partial = mlp = shadow = nullptr;
-    counters = nullptr;
+    counters = barrier = nullptr;
     splitk_bytes = partial_bytes = counters_len = mlp_bytes = shadow_bytes = 0;
+  }
+  void ensure_barrier(bool want) {
+    if (!want || barrier)
+      return;
+    hip_check(hipMalloc(reinterpret_cast<void **>(&barrier), 2 * TA_GEMV_COUNTER_STRIDE * 4),
+              "hipMalloc (GEMV chain barrier)");
+    hip_check(hipMemset(barrier, 0, 2 * TA_GEMV_COUNTER_STRIDE * 4), "hipMemset (GEMV chain barrier)");
   }
   void ensure_shadow(uint64_t bytes) {
     if (bytes <= shadow_bytes)
@@ -151,7 +166,8 @@ void check_host_status(uint32_t *word, void *mlp, uint64_t mlp_bytes) {
     *w = 0;
     if (mlp)
       hip_check(hipMemset(mlp, 0, mlp_bytes), "hipMemset (decode-MLP scratch)");
-    fail("decode MLP: a unit gave up waiting for its inputs");
+    fail("persistent launch (decode MLP or GEMV chain): a workgroup gave up waiting for its "
+         "inputs");
   }
 }
 
@@ -162,14 +178,18 @@ struct OpPlan {
   // Launch role: 0 = normal, 1 = fused into the next op's dual GEMV,
   // 2 = dual GEMV that also produces the previous op's output,
   // 3 = decode-MLP launch covering this op and the next 3 * mlp_layers - 1,
-  // 4 = covered.
+  // 4 = covered, 5 = persistent GEMV-chain launch covering this op and the
+  // next chain_jobs - 1, 6 = covered by it.
   int role = 0;
   uint32_t mlp_layers = 0;
+  uint32_t chain_jobs = 0;
 };
 
 struct ScratchNeed {
   uint64_t splitk = 0, partial = 0, counters = 0, mlp = 0, shadow = 0;
+  bool barrier = false;
   void merge(const ScratchNeed &o) {
+    barrier = barrier || o.barrier;
     shadow = std::max(shadow, o.shadow);
     splitk = std::max(splitk, o.splitk);
     partial = std::max(partial, o.partial);
@@ -729,6 +749,15 @@ struct ExecutorImpl {
         ScratchNeed m;
         m.mlp = g.bytes;
         need.merge(m);
+      } else if (plans[i].role == 5) {
+        const ChainGeom g = chain_geom(res, i, plans[i].chain_jobs);
+        ScratchNeed c;
+        c.partial = g.partial_bytes;
+        c.counters = g.counters;
+        c.barrier = true;
+        need.merge(c);
+      } else if (plans[i].role == 6) {
+        continue;
       } else if (plans[i].role != 1 && plans[i].role != 4) {
         need.merge(scratch_need(res[i], plans[i]));
         if (plans[i].role == 2 && !KERNEL_SPECS[plans[i].kernel].is_gemv()) {
@@ -872,9 +901,171 @@ struct ExecutorImpl {
            1, 256, &m, stream);
   }
 
+  // ---- persistent GEMV chain (src/executor/elementwise/gemv_chain.rs) ----
+  // Each job keeps the K windows its standalone row-GEMV launch would take
+  // (the same plan_gemv call), so its units, window reduction and epilogue
+  // are that launch's; the jobs' partial planes and tile counters sit end
+  // to end in the scratch regions.
+  struct ChainGeom {
+    std::vector<GemvPlan> plans;
+    std::vector<uint64_t> partial_off, counter_off;
+    uint64_t partial_bytes = 0, counters = 0;
+  };
+  ChainGeom chain_geom(const std::vector<ResolvedMatmul> &res, size_t i, uint32_t n) const {
+    ChainGeom g;
+    for (size_t j = i; j < i + n; ++j) {
+      const ResolvedMatmul &d = res[j];
+      g.plans.push_back(plan_gemv(ctx->cu_count(), d.m, d.n, d.k, 64, false,
+                                  gemv_unit(64, false, false, d.m)));
+      g.partial_off.push_back(g.partial_bytes);
+      g.counter_off.push_back(g.counters);
+      g.partial_bytes += (g.plans.back().partial_bytes + 255) / 256 * 256;
+      g.counters += (uint64_t)g.plans.back().tiles * TA_GEMV_COUNTER_STRIDE;
+    }
+    return g;
+  }
+
+  // gemv_chain.rs:200-240 (gemv_jobs_hazard): does job `next` read what an
+  // earlier job of the chain writes, or write what one reads or writes?
+  static bool chain_hazard(const std::vector<MatmulOp> &ops, size_t first, size_t next) {
+    auto reads = [](const MatmulOp &op) {
+      std::vector<const void *> v{op.call.a->buffer_id(), op.call.b->buffer_id()};
+      if (const Tensor *d = op.epilogue.d_tensor())
+        v.push_back(d->buffer_id());
+      if (op.normed_a)
+        v.push_back(op.normed_a->weight->buffer_id());
+      if (op.call.accumulate)
+        v.push_back(op.call.c->buffer_id());
+      return v;
+    };
+    const auto next_reads = reads(ops[next]);
+    const void *next_writes = ops[next].call.c->buffer_id();
+    for (size_t j = first; j < next; ++j) {
+      const void *writes = ops[j].call.c->buffer_id();
+      const auto prev_reads = reads(ops[j]);
+      if (std::find(next_reads.begin(), next_reads.end(), writes) != next_reads.end() ||
+          next_writes == writes ||
+          std::find(prev_reads.begin(), prev_reads.end(), next_writes) != prev_reads.end())
+        return true;
+    }
+    return false;
+  }
+
+  // Roles of a GEMV chain's ops: one persistent launch when it is enabled
+  // (ML_DEVICE_SCOPE=1, the reference's opt-in for its persistent chain,
+  // src/context/init.rs:292-307) and every job takes the row-major f16
+  // decode GEMV (M = 1, N % 4 == 0); otherwise the jobs run as separate
+  // launches in list order (with the graph fusions), which measured faster
+  // on this chip (a 7-job decode chain: 69 us against 78 us).  Both give
+  // the same bits.
+  static bool chain_enabled() {
+    const char *v = std::getenv("ML_DEVICE_SCOPE");
+    if (!v)
+      return false;
+    std::string t(v);
+    for (char &ch : t)
+      ch = (char)std::tolower((unsigned char)ch);
+    return t == "1" || t == "true";
+  }
+  static bool mark_chain(const std::vector<ResolvedMatmul> &res, std::vector<OpPlan> &plans) {
+    if (!chain_enabled() || plans.empty() || plans.size() > TA_GEMV_CHAIN_MAX_JOBS)
+      return false;
+    for (size_t j = 0; j < plans.size(); ++j)
+      if (KERNEL_SPECS[plans[j].kernel].kind != KernelKind::GemvF16Row || plans[j].splitk2 ||
+          res[j].m != 1 || res[j].batch != 1)
+        return false;
+    plans[0].role = 5;
+    plans[0].chain_jobs = (uint32_t)plans.size();
+    for (size_t j = 1; j < plans.size(); ++j)
+      plans[j].role = 6;
+    return true;
+  }
+
+  void launch_chain(const std::vector<MatmulOp> &ops, const std::vector<ResolvedMatmul> &res,
+                    size_t i, uint32_t n, Scratch &scratch, uint32_t *host_status,
+                    hipStream_t stream) const {
+    if (n < 1 || n > TA_GEMV_CHAIN_MAX_JOBS || i + n > ops.size())
+      fail("internal: bad GEMV chain length");
+    const ChainGeom g = chain_geom(res, i, n);
+    if (scratch.partial_bytes < g.partial_bytes || scratch.counters_len < g.counters ||
+        !scratch.barrier)
+      fail("internal: GEMV chain scratch not reserved");
+    if (!host_status)
+      fail("internal: GEMV chain status word missing");
+    GemvChainArgs c{};
+    for (uint32_t j = 0; j < n; ++j) {
+      const MatmulOp &op = ops[i + j];
+      const ResolvedMatmul &d = res[i + j];
+      const GemvPlan &gp = g.plans[j];
+      GemvArgs &a = c.job[j];
+      a.x = static_cast<const float *>(op.call.a->device_ptr());
+      a.w = static_cast<const uint16_t *>(op.call.b->device_ptr());
+      a.y = static_cast<float *>(op.call.c->device_ptr());
+      a.rows = d.m;
+      a.n = d.n;
+      a.k = d.k;
+      a.kchunk = gp.kchunk;
+      a.kchunks = gp.kchunks;
+      a.alpha = op.call.alpha;
+      a.flags = 0; // row-major weights (the chain's rules exclude bias and accumulate)
+      a.act = (uint32_t)op.epilogue.activation;
+      a.binary = (uint32_t)op.epilogue.binary.kind;
+      if (const Tensor *dt = op.epilogue.d_tensor())
+        a.d = static_cast<const float *>(dt->device_ptr());
+      a.beta = op.epilogue.binary.beta;
+      if (gp.kchunks > 1) {
+        a.partial = reinterpret_cast<float *>(static_cast<char *>(scratch.partial) + g.partial_off[j]);
+        a.counters = scratch.counters + g.counter_off[j];
+      }
+      if (op.normed_a) {
+        c.fu[j].norm_w = static_cast<const float *>(op.normed_a->weight->device_ptr());
+        c.fu[j].norm_eps = op.normed_a->eps;
+      }
+      c.units[j] = gp.tiles * gp.kchunks;
+      if (j + 1 < n && chain_hazard(ops, i, i + j + 1))
+        c.sync_after |= 1u << j;
+    }
+    uint64_t widest = 0, group = 0;
+    for (uint32_t j = 0; j < n; ++j) {
+      group += c.units[j];
+      if (j + 1 == n || ((c.sync_after >> j) & 1u)) {
+        widest = std::max(widest, group);
+        group = 0;
+      }
+    }
+    c.n_jobs = n;
+    c.spin_limit = 1u << 22; // ~seconds of polling: a safety net, see the kernel
+    c.barrier = scratch.barrier;
+    void *dev_status = nullptr;
+    hip_check(hipHostGetDevicePointer(&dev_status, host_status, 0), "hipHostGetDevicePointer");
+    c.status = static_cast<uint32_t *>(dev_status);
+    const uint64_t grid = std::max<uint64_t>(1, std::min<uint64_t>(widest, 2ull * ctx->cu_count()));
+    launch("ta_gemv_chain_f16_m1", (uint32_t)grid, 1, 1, 256, &c, stream);
+  }
+
+  // run_gemv_chain (gemv_chain.rs:181-193): one persistent launch.
+  RunStats run_chain_impl(const std::vector<MatmulOp> &jobs) {
+    ctx->make_current();
+    for (const auto &op : jobs)
+      validate_op(op);
+    std::vector<ResolvedMatmul> res;
+    for (const auto &op : jobs)
+      res.push_back(ResolvedMatmul::from_op(op));
+    std::vector<OpPlan> plans;
+    for (size_t i = 0; i < jobs.size(); ++i)
+      plans.push_back(plan_op(jobs[i], res[i], false));
+    if (!mark_chain(res, plans))
+      mark_fusions(jobs, res, plans);
+    Lease lease(this);
+    const uint64_t ns = submit_and_wait(lease.s, jobs, res, plans);
+    return RunStats{ns, jobs.size(), total_flops(res)};
+  }
+
+  // Launches that report through the host status word: the decode MLP
+  // and the persistent GEMV chain.
   static bool has_mlp(const std::vector<OpPlan> &plans) {
     for (const auto &p : plans)
-      if (p.role == 3)
+      if (p.role == 3 || p.role == 5)
         return true;
     return false;
   }
@@ -891,8 +1082,14 @@ struct ExecutorImpl {
           (ops[i - 1].call.c->buffer_id() == cvt.buffer ||
            (ops[i - 1].store.dst && ops[i - 1].store.dst->buffer_id() == cvt.buffer)))
         cvt = CvtCache{};
-      if (p.role == 1 || p.role == 4)
-        continue; // produced by the dual launch of op i+1 / the MLP launch
+      if (p.role == 1 || p.role == 4 || p.role == 6)
+        continue; // produced by the dual launch of op i+1 / the MLP / chain launch
+      if (p.role == 5) {
+        for (size_t j = i; j < i + p.chain_jobs; ++j)
+          check_supported(KERNEL_SPECS[plans[j].kernel], res[j]);
+        launch_chain(ops, res, i, p.chain_jobs, scratch, host_status, stream);
+        continue;
+      }
       if (p.role == 3) {
         for (size_t j = i; j < i + 3 * (size_t)p.mlp_layers; ++j)
           check_supported(KERNEL_SPECS[plans[j].kernel], res[j]);
@@ -925,6 +1122,7 @@ struct ExecutorImpl {
     slot->scratch.ensure(need.splitk, need.partial, need.counters);
     slot->scratch.ensure_mlp(need.mlp);
     slot->scratch.ensure_shadow(need.shadow);
+    slot->scratch.ensure_barrier(need.barrier);
     return submit_on(slot, ops, res, plans, slot->scratch);
   }
   // run_ops with several independent ops (src/executor/dispatch.rs:55-60:
@@ -978,6 +1176,7 @@ struct ExecutorImpl {
       sc.ensure(need.splitk, need.partial, need.counters);
       sc.ensure_mlp(need.mlp);
       sc.ensure_shadow(need.shadow);
+      sc.ensure_barrier(need.barrier);
     }
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
     hip_check(hipEventRecord(slot->fork, slot->stream), "hipEventRecord");
@@ -1041,6 +1240,7 @@ struct ExecutorImpl {
   // launch.  Stream order provides every op's dependency on earlier ones.
   struct ExecStep {
     bool matmul = false;
+    bool chain = false; // a GEMV chain's jobs (one persistent launch when eligible)
     std::vector<MatmulOp> ops;
     std::vector<ResolvedMatmul> res;
     std::vector<OpPlan> plans;
@@ -1055,9 +1255,12 @@ struct ExecutorImpl {
         const std::vector<MatmulOp> &list = op.kind == ExecOp::Kind::Matmul ? one : op.jobs;
         if (op.kind == ExecOp::Kind::GemvChain)
           check_gemv_chain(*this, op.jobs);
-        if (steps.empty() || !steps.back().matmul) {
+        // A chain is a step of its own; later matmuls start a new one.
+        if (steps.empty() || !steps.back().matmul || steps.back().chain ||
+            op.kind == ExecOp::Kind::GemvChain) {
           steps.emplace_back();
           steps.back().matmul = true;
+          steps.back().chain = op.kind == ExecOp::Kind::GemvChain;
         }
         for (const MatmulOp &m : list) {
           validate_op(m);
@@ -1075,10 +1278,11 @@ struct ExecutorImpl {
         continue;
       for (size_t i = 0; i < st.ops.size(); ++i)
         st.plans.push_back(plan_op(st.ops[i], st.res[i], false));
-      mark_fusions(st.ops, st.res, st.plans);
+      if (!st.chain || !mark_chain(st.res, st.plans))
+        mark_fusions(st.ops, st.res, st.plans);
       for (size_t i = 0; i < st.ops.size(); ++i) {
         check_supported(KERNEL_SPECS[st.plans[i].kernel], st.res[i]);
-        if (st.plans[i].role != 3 && st.plans[i].role != 4)
+        if (st.plans[i].role != 3 && st.plans[i].role != 4 && st.plans[i].role < 5)
           check_fusions(KERNEL_SPECS[st.plans[i].kernel], st.ops[i], st.res[i]);
       }
       flops += total_flops(st.res);
@@ -1119,6 +1323,7 @@ struct ExecutorImpl {
     slot->scratch.ensure(need.splitk, need.partial, need.counters);
     slot->scratch.ensure_mlp(need.mlp);
     slot->scratch.ensure_shadow(need.shadow);
+    slot->scratch.ensure_barrier(need.barrier);
     hip_check(hipEventRecord(slot->start, slot->stream), "hipEventRecord");
     record_exec(steps, slot->scratch, slot->host_status, slot->stream);
     hip_check(hipEventRecord(slot->end, slot->stream), "hipEventRecord");
@@ -1492,7 +1697,9 @@ struct ExecutorImpl {
     scratch.ensure(need.splitk, need.partial, need.counters);
     scratch.ensure_mlp(need.mlp);
     scratch.ensure_shadow(need.shadow);
-    p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters, scratch.mlp, scratch.shadow};
+    scratch.ensure_barrier(need.barrier);
+    p->scratch_ = {scratch.splitk, scratch.partial, scratch.counters, scratch.mlp, scratch.shadow,
+                   scratch.barrier};
     p->mlp_scratch_ = scratch.mlp;
     p->mlp_bytes_ = scratch.mlp_bytes;
     if (mlp)
@@ -1614,9 +1821,7 @@ RunStats Executor::run_op_graph(const std::vector<MatmulOp> &ops) const {
 }
 RunStats Executor::run_gemv_chain(const std::vector<MatmulOp> &jobs) const {
   check_gemv_chain(*impl_, jobs);
-  RunStats st = impl_->run_ops_impl(jobs, true);
-  st.n_calls = jobs.size();
-  return st;
+  return impl_->run_chain_impl(jobs);
 }
 
 RunStats Executor::run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const {

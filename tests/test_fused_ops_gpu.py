@@ -147,9 +147,15 @@ def _chain_ops(ta, x, attn, wo, w_up, w_gate, w_down, norm, o, up, gate, out):
     ]
 
 
-def test_gemv_chain_mlp_matches_composed_graph(ta, ex, oracle):
+@pytest.mark.parametrize("persistent", [True, False])
+def test_gemv_chain_mlp_matches_composed_graph(ta, ex, oracle, monkeypatch, persistent):
     """gemv_chain.rs:41-143: o-proj + normed SwiGLU MLP as one GEMV chain (and as
-    a graph op) gives the composed graph's bits."""
+    a graph op) gives the composed graph's bits, as one persistent launch
+    (ML_DEVICE_SCOPE=1) and as list-order launches."""
+    if persistent:
+        monkeypatch.setenv("ML_DEVICE_SCOPE", "1")
+    else:
+        monkeypatch.delenv("ML_DEVICE_SCOPE", raising=False)
     k, n_o, n_ff = 256, 256, 384
     f16w = lambda r, c, seed: ex.tensor_from(oracle.fill_det(r * c, seed), shape=[r, c], f16=True)
     x = ex.tensor_from(oracle.fill_det(k, 1), shape=[1, k])
@@ -166,6 +172,64 @@ def test_gemv_chain_mlp_matches_composed_graph(ta, ex, oracle):
     want = ex.download(composed[3])
     assert np.array_equal(ex.download(chained[3]), want)
     assert np.array_equal(ex.download(graphed[3]), want)
+
+
+@pytest.mark.parametrize("persistent", [True, False])
+def test_gemv_chain_persistent_groups_and_windows(ta, ex, oracle, monkeypatch, persistent):
+    """A chain with independent neighbours (one group: q, k, v reading the
+    same x), dependent jobs (grid barriers), ragged N (1000 = 15 full
+    64-column tiles + 40), deep K (several K windows per tile, reduced in
+    window order) and normed-A, as one persistent launch (ML_DEVICE_SCOPE=1)
+    and as list-order launches: every output equals the same ops run as
+    separate launches, and repeated launches (self-resetting barrier) and a
+    prepared graph's replays repeat the bits."""
+    if persistent:
+        monkeypatch.setenv("ML_DEVICE_SCOPE", "1")
+    else:
+        monkeypatch.delenv("ML_DEVICE_SCOPE", raising=False)
+    k, kd = 2048, 4096
+    f16w = lambda r, c, seed: ex.tensor_from(oracle.fill_normal(r * c, seed, 0.05), shape=[r, c], f16=True)
+    x = ex.tensor_from(oracle.fill_det(k, 11), shape=[1, k])
+    norm = ex.tensor_from(oracle.fill_det(k, 12), shape=[k])
+    wq, wk, wv = f16w(k, 2048, 13), f16w(k, 1000, 14), f16w(k, 256, 15)
+    w2 = f16w(2048, kd, 16)
+    w3 = f16w(kd, 512, 17)
+    res = ex.tensor_from(oracle.fill_det(512, 18), shape=[1, 512])
+    E = ta.Epilogue
+
+    def ops(q, kk, v, h, out):
+        return [ta.MatmulOp(x, wq, q, normed_a=(norm, 1e-5)),
+                ta.MatmulOp(x, wk, kk, alpha=0.5),
+                ta.MatmulOp(x, wv, v, epilogue=E(activation=ta.ACTIVATION_SILU)),
+                ta.MatmulOp(q, w2, h, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL,
+                                                 d=ex.tensor_from(oracle.fill_det(kd, 19), shape=[1, kd]))),
+                ta.MatmulOp(h, w3, out, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=res, beta=0.75))]
+
+    shapes = [[1, 2048], [1, 1000], [1, 256], [1, kd], [1, 512]]
+    chained = [ex.tensor(s_) for s_ in shapes]
+    composed = [ex.tensor(s_) for s_ in shapes]
+    st = ex.run_gemv_chain(ops(*chained))
+    assert st.n_calls == 5
+    ex.run_exec_ops([ta.ExecOp.matmul(op) for op in ops(*composed)])
+    first = [ex.download(t).copy() for t in chained]
+    for got, want in zip(first, composed):
+        np.testing.assert_array_equal(got, ex.download(want))
+    for _ in range(5):
+        for t in chained:
+            ex.upload(t, np.zeros(ex.download(t).size, np.float32))
+        ex.run_gemv_chain(ops(*chained))
+        for t, want in zip(chained, first):
+            np.testing.assert_array_equal(ex.download(t), want)
+    # as a graph op inside a prepared exec graph, replayed
+    graphed = [ex.tensor(s_) for s_ in shapes]
+    p = ex.prepare_exec_ops([ta.ExecOp.gemv_chain(ops(*graphed))])
+    for _ in range(3):
+        for t in graphed:
+            ex.upload(t, np.zeros(ex.download(t).size, np.float32))
+        p.run()
+        for t, want in zip(graphed, first):
+            np.testing.assert_array_equal(ex.download(t), want)
+    p.close()
 
 
 def test_gemv_chain_single_job_and_rejections(ta, ex, oracle):
