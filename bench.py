@@ -282,6 +282,47 @@ def prefill_layer(ta, ex, iters=10):
     return out
 
 
+def gemv_chain(ta, ex, iters=30):
+    """One TinyLlama decode step's seven GEMV jobs (q, k, v with normed-A;
+    o with the residual; up and gate with normed-A and SiLU*up; down with
+    the residual) as a GEMV chain: list-order launches (the default) and
+    one persistent launch with grid barriers between dependent groups
+    (ML_DEVICE_SCOPE=1).  Bytes = f16 weights plus the f32 activations read
+    and written."""
+    rng = np.random.default_rng(71)
+    hid, ffn, kv = 2048, 5632, 256
+    w = lambda k, n: ex.tensor_from((rng.standard_normal((k, n), dtype=np.float32) * 0.02), f16=True)
+    x = ex.tensor_from(rng.uniform(-1, 1, (1, hid)).astype(np.float32))
+    norm = ex.tensor_from(rng.uniform(0.5, 1.5, hid).astype(np.float32))
+    wq, wk, wv, wo, wu, wg, wd = w(hid, hid), w(hid, kv), w(hid, kv), w(hid, hid), w(hid, ffn), w(hid, ffn), w(ffn, hid)
+    q, k, v, o, up, g, y = (ex.tensor([1, n]) for n in (hid, kv, kv, hid, ffn, ffn, hid))
+    E = ta.Epilogue
+    nm = dict(normed_a=(norm, 1e-5))
+    jobs = [ta.MatmulOp(x, wq, q, **nm), ta.MatmulOp(x, wk, k, **nm), ta.MatmulOp(x, wv, v, **nm),
+            ta.MatmulOp(q, wo, o, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0)),
+            ta.MatmulOp(o, wu, up, **nm),
+            ta.MatmulOp(o, wg, g, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up), **nm),
+            ta.MatmulOp(g, wd, y, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=o, beta=1.0))]
+    nbytes = 2 * (2 * hid * hid + 2 * hid * kv + 2 * hid * ffn + ffn * hid)
+    out = {"weight_bytes": nbytes}
+    saved = os.environ.pop("ML_DEVICE_SCOPE", None)
+    try:
+        for name, env in (("list_order", None), ("persistent", "1")):
+            if env:
+                os.environ["ML_DEVICE_SCOPE"] = env
+            else:
+                os.environ.pop("ML_DEVICE_SCOPE", None)
+            for _ in range(5):
+                ex.run_gemv_chain(jobs)
+            ns = median_ns([ex.run_gemv_chain(jobs) for _ in range(iters)])
+            out[name] = dict(us=ns / 1e3, gbps=nbytes / ns, frac_hbm=nbytes / ns / PEAK_HBM)
+    finally:
+        os.environ.pop("ML_DEVICE_SCOPE", None)
+        if saved is not None:
+            os.environ["ML_DEVICE_SCOPE"] = saved
+    return out
+
+
 def concurrency(ta, ex, iters=20):
     """Independent ops in one ta_run_ops call may run concurrently on
     several streams; the same ops as a dependent op graph run back to back
@@ -540,7 +581,7 @@ def main() -> int:
                          "(declared in the JSON line as clock_settle_ms)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (rocprof counter calibration)")
-    ap.add_argument("--sections", default="decode,gelu,splitk,prefill,concurrency,attention,token_loop,vendor",
+    ap.add_argument("--sections", default="decode,gemv_chain,gelu,splitk,prefill,concurrency,attention,token_loop,vendor",
                     help="comma list of secondary sections to run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -577,6 +618,9 @@ def main() -> int:
     if "decode" in sections:
         log("decode SwiGLU MLP ...")
         secondary["decode_swiglu_mlp_f16w"] = decode_mlp(ta, ex)
+    if "gemv_chain" in sections:
+        log("decode GEMV chain ...")
+        secondary["decode_gemv_chain_tinyllama"] = gemv_chain(ta, ex)
     if "gelu" in sections:
         log("batched GELU GEMM ...")
         secondary["batched_gelu_8x2048^3"] = batched_gelu(ta, ex)

@@ -64,6 +64,9 @@
 namespace {
 
 constexpr int kThreads = 256;
+// Row values of a normed-A GEMV at one row loaded per thread ahead of the
+// weight stream (the rest of a longer row is read after it).
+constexpr int kNormPre = 8;
 constexpr int kWaves = kThreads / 64;
 
 // Standalone launch, decode-MLP producer (gate/up, publishes tagged h),
@@ -364,7 +367,10 @@ struct Gemv {
       }
     } else {
       // X loads go out first, then the first weight group: vmcnt retires
-      // in issue order, so staging X into LDS then waits only for X.
+      // in issue order, so staging X into LDS then waits only for X.  With
+      // normed A at one row, the row's first kNormPre * kThreads values
+      // (its sum of squares) are loaded before the weights too, so the
+      // norm does not wait behind the weight stream.
 #pragma unroll
       for (int j = 0; j < XPT; ++j) {
         bool ok;
@@ -372,10 +378,23 @@ struct Gemv {
         xr[j] = COH ? coherent_load(p.x + xi) : p.x[xi];
         xr[j] = ok ? xr[j] : 0.0f;
       }
+      float pre[kNormPre];
+      const bool norm = MODE == kStandalone && fu && fu->norm_w;
+      if constexpr (MODE == kStandalone && MR == 1) {
+        if (norm) {
+#pragma unroll
+          for (int i = 0; i < kNormPre; ++i) {
+            const uint32_t kk = tid + i * kThreads;
+            const uint32_t at = min(kk, p.k - 1u);
+            const float v = COH ? coherent_load(p.x + at) : p.x[at];
+            pre[i] = kk < p.k ? v : 0.0f;
+          }
+        }
+      }
       issue(0, cur);
       if constexpr (MODE == kStandalone) {
-        if (fu && fu->norm_w)
-          normalize_x(p, *fu, k0, xr, sm);
+        if (norm)
+          normalize_x(p, *fu, k0, xr, sm, pre);
       }
     }
     if constexpr (MF) {
@@ -704,7 +723,8 @@ struct Gemv {
   // + eps).  The whole rows are re-read per unit; they are small and
   // L2-resident.  The X window's LDS (not yet staged) is the scratch.
   static TA_DEVICE void normalize_x(const GemvArgs &p, const GemvFusion &f, uint32_t k0,
-                                    float (&xr)[XROWS * MR / kThreads], Smem &sm) {
+                                    float (&xr)[XROWS * MR / kThreads], Smem &sm,
+                                    const float (&pre)[kNormPre]) {
     constexpr int XPT = XROWS * MR / kThreads;
     static_assert(XS >= kThreads, "reduction scratch");
     const uint32_t tid = threadIdx.x;
@@ -712,7 +732,16 @@ struct Gemv {
     for (uint32_t m = 0; m < p.rows; ++m) {
       const float *row = p.x + (uint64_t)m * p.k;
       float ss = 0.0f;
-      for (uint32_t kk = tid; kk < p.k; kk += kThreads) {
+      uint32_t kk = tid;
+      if constexpr (MR == 1) {
+        // Values loaded before the weights (zero past K: adding 0 to the
+        // non-negative sum leaves it unchanged), in the loop's order.
+#pragma unroll
+        for (int i = 0; i < kNormPre; ++i)
+          ss = fmaf(pre[i], pre[i], ss);
+        kk = tid + kNormPre * kThreads;
+      }
+      for (; kk < p.k; kk += kThreads) {
         const float a = COH ? coherent_load(row + kk) : row[kk];
         ss = fmaf(a, a, ss);
       }

@@ -242,3 +242,83 @@ def test_store_rejects_invalid_forms(ta, ex, oracle):
     for op, msg in cases:
         with pytest.raises(ta.TensorAshError, match=msg):
             ex.run_ops([op])
+
+
+# ------------------------------------------------- grouped decode GEMV launches
+
+@pytest.mark.parametrize("form", ["graph", "prepared", "run_ops"])
+def test_gemv_groups_match_separate_launches(ta, ex, oracle, monkeypatch, form):
+    """A decode layer's one-row GEMVs: q (packed, normed A, RoPE at store),
+    k (packed, normed A, RoPE + scatter into a Kt cache at a device position
+    cell), v (row-major, normed A, scatter into a V cache), then o (residual)
+    beside an independent biased job (ragged N = 1000), the normed SwiGLU
+    pair (one dual launch) and down (residual).  Independent neighbours run
+    as one grouped launch; every output and cache equals, bit for bit, the
+    same ops run one launch per job with no fusion."""
+    k, hd, t_max, kvn, ffn = 2048, 64, 16, 256, 1024
+    x = ex.tensor_from(oracle.fill_det(k, 64000), shape=[1, k])
+    x2 = ex.tensor_from(oracle.fill_det(k, 64001), shape=[1, k])
+    norm = ex.tensor_from(oracle.fill_det(k, 64002) * 0.5 + 1.0, shape=[k])
+    table = ex.tensor_from(oracle.fill_det(t_max * hd, 64003), shape=[t_max, hd // 2, 2])
+    bias = ex.tensor_from(oracle.fill_det(1000, 64004), shape=[1000])
+    cell = pos_cell(ex, 3)
+
+    def w(kk, n, seed, packed=False):
+        wb, _ = f16_weights(oracle, kk, n, seed)
+        return weights_tensor(ta, ex, wb, kk, n, packed)
+
+    wq, wk, wv = w(k, k, 64010, True), w(k, kvn, 64011, True), w(k, kvn, 64012)
+    wo, wb, wu, wg, wd = w(k, k, 64013), w(k, 1000, 64014), w(k, ffn, 64015), w(k, ffn, 64016), w(ffn, k, 64017)
+    h = kvn // hd
+    kt_init = oracle.fill_det(h * hd * t_max, 64020)
+    v_init = oracle.fill_det(h * t_max * hd, 64021)
+
+    def run(group):
+        if group:
+            monkeypatch.delenv("TA_NO_GEMV_GROUP", raising=False)
+            monkeypatch.delenv("TA_NO_FUSE", raising=False)
+        else:
+            monkeypatch.setenv("TA_NO_GEMV_GROUP", "1")
+            monkeypatch.setenv("TA_NO_FUSE", "1")
+        kt = ex.tensor_from(kt_init, shape=[h, hd, t_max])
+        vc = ex.tensor_from(v_init, shape=[h, t_max, hd])
+        q, kk_, v, o, bo, up, g, y = (ex.tensor([1, n]) for n in (k, kvn, kvn, k, 1000, ffn, ffn, k))
+        nm = dict(normed_a=(norm, EPS))
+        E = ta.Epilogue
+        ops = [
+            ta.MatmulOp(x, wq, q, packed_b=True, store=ta.MatmulStore(
+                ta.STORE_ROPE, ta.MatmulStoreDesc(head_dim=hd, pos_base=2, pos_addr=cell.device_address),
+                table=table), **nm),
+            ta.MatmulOp(x, wk, kk_, packed_b=True, store=ta.MatmulStore(
+                ta.STORE_ROPE_SCATTER, ta.MatmulStoreDesc(head_dim=hd, pos_base=2, pos_addr=cell.device_address,
+                                                          pos_scale=1, stride_head=hd * t_max, stride_dim=t_max),
+                table=table, dst=kt), **nm),
+            ta.MatmulOp(x, wv, v, store=ta.MatmulStore(
+                ta.STORE_SCATTER, ta.MatmulStoreDesc(head_dim=hd, pos_base=5, pos_scale=hd,
+                                                     stride_head=t_max * hd, stride_dim=1), dst=vc), **nm),
+            ta.MatmulOp(q, wo, o, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0)),
+            ta.MatmulOp(x2, wb, bo, epilogue=E(bias=bias)),
+            ta.MatmulOp(o, wu, up, **nm),
+            ta.MatmulOp(o, wg, g, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up), **nm),
+            ta.MatmulOp(g, wd, y, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=o, beta=1.0)),
+        ]
+        outs = (q, kt, vc, o, bo, up, g, y)
+        if form == "graph":
+            ex.run_op_graph(ops)
+        elif form == "prepared":
+            p = ex.prepare_op_graph(ops)
+            for _ in range(2):
+                p.run()
+            p.close()
+        else:
+            # independent ops only (the first three, then the two of the o group)
+            ex.run_ops(ops[:3])
+            ex.run_ops(ops[3:5])
+            outs = outs[:5]
+        return [ex.download(t).reshape(-1).copy() for t in outs]
+
+    got, want = run(True), run(False)
+    for i, (a, b) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(a, b, err_msg=f"output {i}")
+    for a in want:
+        assert np.isfinite(a).all() and np.abs(a).max() > 0
