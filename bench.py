@@ -288,7 +288,9 @@ def gemv_chain(ta, ex, iters=30):
     the residual) as a GEMV chain: list-order launches (the default) and
     one persistent launch with grid barriers between dependent groups
     (ML_DEVICE_SCOPE=1).  Bytes = f16 weights plus the f32 activations read
-    and written."""
+    and written.  `packed_op_graph`: the same step with the weights packed
+    in 64-column tiles (the decode layout) as one op graph: q, k and v share
+    a launch, then o, then the normed MLP as one decode-MLP launch."""
     rng = np.random.default_rng(71)
     hid, ffn, kv = 2048, 5632, 256
     w = lambda k, n: ex.tensor_from((rng.standard_normal((k, n), dtype=np.float32) * 0.02), f16=True)
@@ -320,6 +322,24 @@ def gemv_chain(ta, ex, iters=30):
         os.environ.pop("ML_DEVICE_SCOPE", None)
         if saved is not None:
             os.environ["ML_DEVICE_SCOPE"] = saved
+
+    def packed(k, n):
+        wt = (rng.standard_normal(k * n, dtype=np.float32) * 0.02).astype(np.float32)
+        return ex.tensor_from(ta.pack_f16w_row_tiles(wt, k, n, 64), shape=[k, n], f16=True)
+
+    pq, pk, pv, po, pu, pg, pd = (packed(kk, n) for kk, n in ((hid, hid), (hid, kv), (hid, kv), (hid, hid),
+                                                             (hid, ffn), (hid, ffn), (ffn, hid)))
+    pb = dict(packed_b=True)
+    layer = [ta.MatmulOp(x, pq, q, **nm, **pb), ta.MatmulOp(x, pk, k, **nm, **pb),
+             ta.MatmulOp(x, pv, v, **nm, **pb),
+             ta.MatmulOp(q, po, o, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0), **pb),
+             ta.MatmulOp(o, pu, up, **nm, **pb),
+             ta.MatmulOp(o, pg, g, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up), **nm, **pb),
+             ta.MatmulOp(g, pd, y, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=o, beta=1.0), **pb)]
+    for _ in range(5):
+        ex.run_op_graph(layer)
+    ns = median_ns([ex.run_op_graph(layer) for _ in range(iters)])
+    out["packed_op_graph"] = dict(us=ns / 1e3, gbps=nbytes / ns, frac_hbm=nbytes / ns / PEAK_HBM)
     return out
 
 

@@ -378,10 +378,22 @@ struct Gemv {
         xr[j] = COH ? coherent_load(p.x + xi) : p.x[xi];
         xr[j] = ok ? xr[j] : 0.0f;
       }
+      // Normed A: the standalone launch's fusion, or the first layer of a
+      // decode MLP (its x is read from memory, like a standalone launch's).
+      const float *norm_w = nullptr;
+      float norm_eps = 0.0f;
+      if constexpr (MODE == kStandalone) {
+        if (fu && fu->norm_w) {
+          norm_w = fu->norm_w;
+          norm_eps = fu->norm_eps;
+        }
+      } else if constexpr (MODE == kProducer) {
+        norm_w = mlp->norm_w;
+        norm_eps = mlp->norm_eps;
+      }
       float pre[kNormPre];
-      const bool norm = MODE == kStandalone && fu && fu->norm_w;
-      if constexpr (MODE == kStandalone && MR == 1) {
-        if (norm) {
+      if constexpr (MODE != kConsumer && MR == 1) {
+        if (norm_w) {
 #pragma unroll
           for (int i = 0; i < kNormPre; ++i) {
             const uint32_t kk = tid + i * kThreads;
@@ -392,9 +404,9 @@ struct Gemv {
         }
       }
       issue(0, cur);
-      if constexpr (MODE == kStandalone) {
-        if (norm)
-          normalize_x(p, *fu, k0, xr, sm, pre);
+      if constexpr (MODE != kConsumer) {
+        if (norm_w)
+          normalize_x(p, norm_w, norm_eps, k0, xr, sm, pre);
       }
     }
     if constexpr (MF) {
@@ -722,7 +734,8 @@ struct Gemv {
   // staged window values: x' = (x * s_m) * w[k], s_m = 1 / sqrt(sumsq / K
   // + eps).  The whole rows are re-read per unit; they are small and
   // L2-resident.  The X window's LDS (not yet staged) is the scratch.
-  static TA_DEVICE void normalize_x(const GemvArgs &p, const GemvFusion &f, uint32_t k0,
+  static TA_DEVICE void normalize_x(const GemvArgs &p, const float *norm_w, float norm_eps,
+                                    uint32_t k0,
                                     float (&xr)[XROWS * MR / kThreads], Smem &sm,
                                     const float (&pre)[kNormPre]) {
     constexpr int XPT = XROWS * MR / kThreads;
@@ -754,7 +767,7 @@ struct Gemv {
         __syncthreads();
       }
       if (tid == 0)
-        scale[m] = 1.0f / sqrtf(sm.xs[0] / (float)p.k + f.norm_eps);
+        scale[m] = 1.0f / sqrtf(sm.xs[0] / (float)p.k + norm_eps);
       __syncthreads();
     }
 #pragma unroll
@@ -762,7 +775,7 @@ struct Gemv {
       const uint32_t i = tid + j * kThreads;
       const uint32_t kk = i / MR, m = i % MR;
       if (i < p.kchunk * MR && m < p.rows && k0 + kk < p.k)
-        xr[j] = (xr[j] * scale[m]) * f.norm_w[k0 + kk];
+        xr[j] = (xr[j] * scale[m]) * norm_w[k0 + kk];
     }
   }
 

@@ -378,6 +378,11 @@ typedef struct MlpArgs {
   uint32_t tiles_a, tiles_b;
   uint32_t spin_limit; // polls before a wait gives up
   uint32_t layers;
+  // Normed A of the first layer's gate/up (RMSNorm of x folded into their
+  // X staging, as in the standalone GEMV); null when x is used as is.
+  const float *norm_w;
+  float norm_eps;
+  uint32_t pad_norm;
   MlpLayer layer[TA_MLP_MAX_LAYERS];
 } MlpArgs;
 

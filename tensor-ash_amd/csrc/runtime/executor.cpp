@@ -666,7 +666,7 @@ struct ExecutorImpl {
       if (plans[i].role != 0 || plans[i + 1].role != 0)
         continue;
       if (!std::getenv("TA_NO_MLP") && i + 2 < ops.size() && plans[i + 2].role == 0 &&
-          res[i].batch == 1 && res[i].m <= mlp_max_rows() && !ops[i].normed_a &&
+          res[i].batch == 1 && res[i].m <= mlp_max_rows() &&
           fusable_pair(ops[i], plans[i], ops[i + 1], plans[i + 1], res[i]) &&
           mlp_tail_ok(ops[i], ops[i + 1], plans[i + 1], ops[i + 2], plans[i + 2])) {
         plans[i].role = 3;
@@ -725,6 +725,10 @@ struct ExecutorImpl {
       if (res[j + k].m != res[i + k].m || res[j + k].n != res[i + k].n ||
           res[j + k].k != res[i + k].k)
         return false;
+    // A later layer's x is the previous layer's y, handed over inside the
+    // launch: it cannot be normed (its norm needs the whole row first).
+    if (ops[j].normed_a)
+      return false;
     const Tensor *prev_y = ops[j - 1].call.c, *x = ops[j].call.a;
     if (x->buffer_id() != prev_y->buffer_id() || x->shape() != prev_y->shape() ||
         ops[j + 1].call.a->buffer_id() != x->buffer_id())
@@ -862,6 +866,10 @@ struct ExecutorImpl {
     if (layers < 1 || layers > TA_MLP_MAX_LAYERS || i + 3 * layers > ops.size())
       fail("internal: bad decode-MLP chain length");
     MlpArgs m{};
+    if (ops[i].normed_a) {
+      m.norm_w = static_cast<const float *>(ops[i].normed_a->weight->device_ptr());
+      m.norm_eps = ops[i].normed_a->eps;
+    }
     for (uint32_t l = 0; l < layers; ++l) {
       const size_t o = i + 3 * (size_t)l;
       const MatmulOp &up = ops[o], &gate = ops[o + 1], &down = ops[o + 2];

@@ -63,7 +63,8 @@ def test_normed_a_gemv_matches_rms_reference(ta, ex, oracle, m, k, n, kind):
 
 def test_normed_a_composes_with_silu_mul_epilogue_in_graph(ta, ex, oracle):
     """fusion.rs:109-170: up = norm(x) @ Wu, h = silu(norm(x) @ Wg) * up in
-    one dependent op graph (the normed ops are not pair-fused)."""
+    one dependent op graph (the pair with one norm runs as one dual GEMV
+    launch)."""
     k, n = 1024, 768
     x, w_norm = oracle.fill_det(k, 12000), oracle.fill_det(k, 12001)
     wg, wgr = f16_weights(oracle, k, n, 12002)
@@ -322,3 +323,56 @@ def test_gemv_groups_match_separate_launches(ta, ex, oracle, monkeypatch, form):
         np.testing.assert_array_equal(a, b, err_msg=f"output {i}")
     for a in want:
         assert np.isfinite(a).all() and np.abs(a).max() > 0
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+@pytest.mark.parametrize("packed", [True, False])
+def test_normed_swiglu_mlp_matches_separate_launches(ta, ex, oracle, monkeypatch, m, packed):
+    """The decode layer's MLP with its RMSNorm folded in: up = norm(o) @ Wu,
+    h = silu(norm(o) @ Wg) * up, y = h @ Wd + o as one dependent graph (packed
+    weights: one decode-MLP launch whose gate/up units normalise o;
+    row-major: one dual GEMV launch, then down) gives the bits of the three
+    ops run one launch each, and matches the f64 composition on
+    the f16-rounded weights within the GEMV tolerance; two MLPs in a row
+    where the second is normed again stay two launches.  The decode-MLP
+    launch sums the down projection's K in its own 512-row windows, so with
+    packed weights the down outputs (and the second MLP, which reads them)
+    are held to the GEMV tolerance, as in the un-normed MLP's test."""
+    hid, ffn = 2048, 5632
+    o_h = oracle.fill_det(m * hid, 65000 + m)
+    w_norm = oracle.fill_det(hid, 65001) * 0.5 + 1.0
+    (wu, wur), (wg, wgr), (wd, wdr) = (f16_weights(oracle, kk, n, 65010 + i)
+                                       for i, (kk, n) in enumerate(((hid, ffn), (hid, ffn), (ffn, hid))))
+    o, tw = ex.tensor_from(o_h, shape=[m, hid]), ex.tensor_from(w_norm, shape=[hid])
+    tu, tg, td = (weights_tensor(ta, ex, w, kk, n, packed) for w, (kk, n) in
+                  ((wu, (hid, ffn)), (wg, (hid, ffn)), (wd, (ffn, hid))))
+    E = ta.Epilogue
+
+    def mlp(x, up, h, y):
+        nm = dict(normed_a=(tw, EPS), packed_b=packed)
+        return [ta.MatmulOp(x, tu, up, **nm),
+                ta.MatmulOp(x, tg, h, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up), **nm),
+                ta.MatmulOp(h, td, y, packed_b=packed, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0))]
+
+    def run(fused):
+        if fused:
+            monkeypatch.delenv("TA_NO_FUSE", raising=False)
+        else:
+            monkeypatch.setenv("TA_NO_FUSE", "1")
+        t = [ex.tensor([m, n]) for n in (ffn, ffn, hid, ffn, ffn, hid)]
+        ex.run_op_graph(mlp(o, *t[:3]) + mlp(t[2], *t[3:]))
+        return [ex.download(x).reshape(-1).copy() for x in t]
+
+    got, want = run(True), run(False)
+    for i, (a, b) in enumerate(zip(got, want)):
+        if packed and i >= 2:
+            check_f16(a, b, (ffn, hid, hid, ffn)[i - 2], oracle)
+        else:
+            np.testing.assert_array_equal(a, b, err_msg=f"output {i}")
+    xn = oracle.rms_norm_rows(o_h, w_norm, m, hid, EPS)
+    up_ref = oracle.cpu_bmm(xn, wur, None, 1, m, ffn, hid)
+    h_ref = oracle.epilogue(oracle.cpu_bmm(xn, wgr, None, 1, m, ffn, hid), ffn, m * ffn, act=2, binary=2, d=up_ref)
+    y_ref = oracle.epilogue(oracle.cpu_bmm(h_ref, wdr, None, 1, m, hid, ffn), hid, m * hid, binary=1, d=o_h,
+                            beta=1.0)
+    check_f16(got[1], h_ref, hid, oracle)
+    check_f16(got[2], y_ref, ffn, oracle)
