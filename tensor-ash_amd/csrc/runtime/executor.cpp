@@ -367,9 +367,9 @@ struct ExecutorImpl {
       need.partial = g.partial_bytes;
       need.counters = (uint64_t)g.tiles * TA_GEMV_COUNTER_STRIDE;
     } else if (s.kind == KernelKind::GemmF16Mfma && gemm_lds_ok(d)) {
-      need.splitk = a16_bytes(d);
+      need.splitk = 2 * a16_bytes(d); // two f16 copies of A (CvtCache)
     } else if (s.kind == KernelKind::GemmF16Sk) {
-      need.splitk = a16_bytes(d);
+      need.splitk = 2 * a16_bytes(d);
       const uint32_t splits = h16sk_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k, s.tile_m, s.tile_n);
       if (splits > 1) {
         const uint64_t tiles =
@@ -388,16 +388,57 @@ struct ExecutorImpl {
     return (planes * d.m * d.k * 2 + 255) / 256 * 256;
   }
 
-  // The f16 copy of A that the last pre-pass of a submission left in the
-  // split-K region: a later f16w GEMM with the same A (same buffer, same
-  // elements) reuses it unless an op in between wrote that buffer or the
-  // region (record() clears it).
-  struct CvtCache {
+  // f16 copies of A that pre-passes (or a dual launch's f16 output copy)
+  // of a submission left behind: a later f16w GEMM with the same A (same
+  // buffer, same elements) reuses one unless an op in between wrote that
+  // buffer, or wrote the split-K region the copy lives in (record() and
+  // launch_gemm() drop such entries).  Two entries, so a layer that
+  // converts x for QKV and then the attention output for O still finds x
+  // for its up/gate pair.  Pre-pass copies go to the half of the split-K
+  // region the other live copy does not use (scratch_need reserves two
+  // halves, each as large as the op's A).
+  struct CvtEntry {
     const void *buffer = nullptr;
     const void *src = nullptr;
     uint64_t n = 0;
-    void *base = nullptr;              // where the copy lives
-    size_t producer = SIZE_MAX;        // op whose epilogue wrote it, if any
+    void *base = nullptr;       // where the copy lives
+    size_t producer = SIZE_MAX; // op whose epilogue wrote it, if any
+    int half = -1;              // split-K region half, -1 = elsewhere
+    uint64_t age = 0;
+  };
+  struct CvtCache {
+    CvtEntry e[2];
+    uint64_t clock = 0;
+    CvtEntry *find(const void *buffer, const void *src, uint64_t n) {
+      for (auto &x : e)
+        if (x.buffer && x.buffer == buffer && x.src == src && x.n == n)
+          return &x;
+      return nullptr;
+    }
+    // The entry to replace: an empty one, else the older.
+    CvtEntry &victim() {
+      if (!e[0].buffer)
+        return e[0];
+      if (!e[1].buffer)
+        return e[1];
+      return e[0].age <= e[1].age ? e[0] : e[1];
+    }
+    void put(CvtEntry &slot, CvtEntry v) {
+      v.age = ++clock;
+      slot = v;
+    }
+    // An op wrote `buffer`: copies of it are stale (except the one that
+    // op's own epilogue produced).
+    void wrote(const void *buffer, size_t op) {
+      for (auto &x : e)
+        if (x.buffer && x.buffer == buffer && x.producer != op)
+          x = CvtEntry{};
+    }
+    void drop_region() { // the split-K region was overwritten
+      for (auto &x : e)
+        if (x.half >= 0)
+          x = CvtEntry{};
+    }
   };
 
   // Does op i (the gate of a dual SwiGLU launch) feed op i + 1 as A on the
@@ -475,13 +516,22 @@ struct ExecutorImpl {
       if (blocks > 0x7fffffffull)
         fail("f16 conversion grid exceeds the HIP launch limits");
       const void *buf = op.call.a->buffer_id();
-      if (!(cvt.buffer == buf && cvt.src == cv.src && cvt.n == cv.n)) {
+      if (CvtEntry *hit = cvt.find(buf, cv.src, cv.n)) {
+        a.a = hit->base;
+      } else {
+        CvtEntry &v = cvt.victim();
+        const CvtEntry &other = &v == &cvt.e[0] ? cvt.e[1] : cvt.e[0];
+        const int half = other.half == 0 ? 1 : 0;
+        const uint64_t half_bytes = scratch.splitk_bytes / 2 / 256 * 256;
+        if (a16_bytes(d) > half_bytes)
+          fail("internal: f16 copy scratch not reserved");
+        cv.dst = reinterpret_cast<uint16_t *>(static_cast<char *>(splitk_scratch) + half * half_bytes);
         launch("ta_cvt_f32_f16", (uint32_t)blocks, 1, 1, 256, &cv, stream);
-        cvt = CvtCache{buf, cv.src, cv.n, splitk_scratch, SIZE_MAX};
+        cvt.put(v, CvtEntry{buf, cv.src, cv.n, cv.dst, SIZE_MAX, half});
+        a.a = cv.dst;
       }
-      a.a = cvt.base;
     } else if (splits > 1) {
-      cvt = CvtCache{}; // the partial planes overwrite the f16 copy
+      cvt.drop_region(); // the partial planes overwrite the f16 copies
     }
     const uint32_t lds_threads = (uint32_t)ta_h16_lds_threads((int)s.tile_m, (int)s.tile_n);
     if (s.kind == KernelKind::GemmF16Sk) {
@@ -1140,12 +1190,13 @@ struct ExecutorImpl {
     CvtCache cvt;
     for (size_t i = 0; i < ops.size(); ++i) {
       const OpPlan &p = plans[i];
-      // the cached f16 copy of A is stale once an op writes A's buffer
+      // a cached f16 copy of A is stale once an op writes A's buffer
       // (except the op whose epilogue wrote the copy)
-      if (i > 0 && cvt.buffer && cvt.producer != i - 1 &&
-          (ops[i - 1].call.c->buffer_id() == cvt.buffer ||
-           (ops[i - 1].store.dst && ops[i - 1].store.dst->buffer_id() == cvt.buffer)))
-        cvt = CvtCache{};
+      if (i > 0) {
+        cvt.wrote(ops[i - 1].call.c->buffer_id(), i - 1);
+        if (ops[i - 1].store.dst)
+          cvt.wrote(ops[i - 1].store.dst->buffer_id(), i - 1);
+      }
       if (p.role == 1 || p.role == 4 || p.role == 6)
         continue; // produced by the dual launch of op i+1 / the MLP / chain launch
       if (p.role == 5) {
@@ -1172,8 +1223,9 @@ struct ExecutorImpl {
           fail("internal: f16 output copy scratch not reserved");
         uint16_t *c16 = static_cast<uint16_t *>(scratch.shadow);
         launch_gemm(s, res[i], ops[i], 1, scratch, cvt, stream, &ops[i - 1], c16);
-        cvt = CvtCache{ops[i].call.c->buffer_id(), ops[i].call.c->device_ptr(),
-                       (uint64_t)res[i].batch * res[i].m * res[i].n, c16, i};
+        cvt.wrote(ops[i].call.c->buffer_id(), SIZE_MAX);
+        cvt.put(cvt.victim(), CvtEntry{ops[i].call.c->buffer_id(), ops[i].call.c->device_ptr(),
+                                       (uint64_t)res[i].batch * res[i].m * res[i].n, c16, i, -1});
       } else
         launch_gemm(s, res[i], ops[i], p.splitk2.value_or(1), scratch, cvt, stream,
                     p.role == 2 ? &ops[i - 1] : nullptr);

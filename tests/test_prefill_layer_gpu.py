@@ -192,3 +192,45 @@ def test_config5_prefill_layer_one_graph(ta, ex, oracle, io16):
     e = rel_err(got["out"].reshape(T, HID)[rows], out)
     assert e <= 2e-3, f"layer output normwise error {e}"
     assert np.all(np.isfinite(got["out"]))
+
+
+def test_f16_copy_cache_reuse_and_invalidation(ta, ex, oracle):
+    """The f16 copies of A a submission's conversion pre-passes leave
+    behind: x converted for the first GEMM is reused by a later one after
+    another A was converted in between, and an op that overwrites x forces
+    a fresh conversion.  Every result equals the same GEMM run alone, bit
+    for bit (the copy is the same RNE rounding either way)."""
+    m, k, n = 256, 512, 384
+    hx, ha2 = oracle.fill_det(m * k, 6201), oracle.fill_det(m * k, 6202)
+    w1, w2, w3, w4 = (oracle.fill_normal(k * n, s, 0.02) for s in (6203, 6204, 6205, 6206))
+    wx = oracle.fill_normal(k * k, 6207, 0.02)
+    x, a2 = ex.tensor_from(hx, shape=[m, k]), ex.tensor_from(ha2, shape=[m, k])
+    tw = [ex.tensor_from(w, shape=[k, n], f16=True) for w in (w1, w2, w3, w4)]
+    twx = ex.tensor_from(wx, shape=[k, k], f16=True)
+    assert "mfma" in ex.dispatch_info_for(1, m, n, k, True)["kernel"]
+    c = [ex.tensor([m, n]) for _ in range(4)]
+
+    def alone(a_t, w_t):
+        out = ex.tensor([m, n])
+        ex.run_ops([ta.MatmulOp(a_t, w_t, out)])
+        return ex.download(out)
+
+    print("f16 copy cache: x, a2, x (reuse)", flush=True)
+    ex.run_op_graph([ta.MatmulOp(x, tw[0], c[0]), ta.MatmulOp(a2, tw[1], c[1]),
+                     ta.MatmulOp(x, tw[2], c[2])])
+    want_x2 = alone(x, tw[2])
+    np.testing.assert_array_equal(ex.download(c[0]), alone(x, tw[0]))
+    np.testing.assert_array_equal(ex.download(c[1]), alone(a2, tw[1]))
+    np.testing.assert_array_equal(ex.download(c[2]), want_x2)
+
+    # x overwritten in between (x = a2 @ Wx): the last GEMM must see new x.
+    print("f16 copy cache: x, overwrite x, x", flush=True)
+    x_b = ex.tensor_from(hx, shape=[m, k])
+    ex.run_op_graph([ta.MatmulOp(x_b, tw[0], c[0]), ta.MatmulOp(a2, twx, x_b),
+                     ta.MatmulOp(x_b, tw[3], c[3])])
+    new_x = ex.download(x_b)
+    assert not np.array_equal(new_x.reshape(-1), hx)
+    np.testing.assert_array_equal(ex.download(c[3]), alone(x_b, tw[3]))
+    ref = oracle.reference_gemm(oracle.round_via_f16(new_x.reshape(-1)), oracle.round_via_f16(w4), 1, m, n, k)
+    err, idx = oracle.max_abs_err(ex.download(c[3]).reshape(-1), ref)
+    assert err <= 2 * oracle.tolerance(k) + 1e-4, f"abs err {err} at {idx}"
