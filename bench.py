@@ -61,13 +61,19 @@ def time_roofline(flops: float, nbytes: float, seconds: float, peak_tflops: floa
 def load_pmc_traffic() -> dict:
     """HBM bytes per launch of the secondary kernels, from the committed
     rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE per dispatch, each
-    scaled by the same counter on a plain copy): `key traffic_bytes=N`."""
+    scaled by the same counter on a plain copy): `key traffic_bytes=N`,
+    per layer for the multi-layer decode launches (`layers=L`)."""
     out = {}
     try:
         for line in (ROOT / "profiles" / "secondary_pmc.txt").read_text().splitlines():
             parts = line.split()
             if len(parts) >= 2 and parts[1].startswith("traffic_bytes="):
-                out[parts[0]] = int(parts[1].split("=", 1)[1])
+                v = int(parts[1].split("=", 1)[1])
+                # multi-layer decode launches: stored per layer
+                for f in parts[2:]:
+                    if f.startswith("layers="):
+                        v //= int(f.split("=", 1)[1])
+                out[parts[0]] = v
     except OSError:
         pass
     return out
@@ -124,12 +130,15 @@ def headline(ta, ex, steps: int, warmup: int, settle_ms: float):
     )
 
 
-def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=30, layers=10):
+def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=30, layers=16):
     """Config 3: h = silu(x@Wg) * (x@Wu); y = h@Wd + res, packed f16 weights.
 
-    A decode forward runs its layers back to back, so the step is timed the
-    same way: one prepared op graph (hipGraph) chains `layers` MLP layers,
-    layer l reading the previous layer's y as x and as residual, over
+    A decode forward runs its layers back to back (TinyLlama, whose MLP
+    shape this is, has 22), so the step is timed the same way: one prepared
+    op graph (hipGraph) chains `layers` MLP layers - 16, the most one
+    decode-MLP launch holds (22 layers would be 66 ops, over the 64-op
+    submission limit) - layer l reading the previous layer's y as x and as
+    residual, over
     `copies` weight sets rotated so the working set exceeds the 256 MB
     last-level cache (every layer reads its weights from HBM).  step_us is
     the graph's GPU time / layers.  launch_us is one layer prepared alone,
@@ -181,7 +190,7 @@ def decode_mlp(ta, ex, rows_list=(1, 4, 8), iters=30, layers=10):
                             layers_per_graph=layers, launch_us=single_ns / 1e3,
                             wall_us_per_step=wall / iters / layers * 1e6,
                             roofline=roofline("hbm", bytes_step / step_ns, PEAK_HBM, "GB/s",
-                                              traffic // layers if traffic else None))
+                                              traffic))
         chain.close()
         single.close()
     return out
@@ -277,6 +286,17 @@ def prefill_layer(ta, ex, iters=10):
         ex.run_op_graph(layer)
     ns = median_ns([ex.run_op_graph(layer) for _ in range(iters)])
     out["layer_gemms_one_submission"] = dict(
+        us=ns / 1e3, tflops=total_flops / ns / 1e3,
+        roofline=time_roofline(total_flops, total_bytes, ns * 1e-9, PEAK_FP16_MFMA))
+    # The same graph prepared once (prepare_op_graph: captured as a
+    # hipGraph) and replayed, as a prefill that runs its layer repeatedly
+    # would; the events bracket the replay.
+    prepared = ex.prepare_op_graph(layer)
+    for _ in range(3):
+        prepared.run()
+    ns = median_ns([prepared.run() for _ in range(iters)])
+    prepared.close()
+    out["layer_gemms_prepared"] = dict(
         us=ns / 1e3, tflops=total_flops / ns / 1e3,
         roofline=time_roofline(total_flops, total_bytes, ns * 1e-9, PEAK_FP16_MFMA))
     return out
