@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "kernel_args.h"
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -12,25 +14,56 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 #define TA_DEVICE __device__ __forceinline__
 
+// x / y as the hardware reciprocal (v_rcp_f32, about 1 ulp) times x.  The
+// IEEE divide sequence the compiler emits for a '/' or __fdividef (scale,
+// two Newton steps, fixup) was most of a GELU epilogue's time at one wave
+// per SIMD.  y >= 1 wherever it is used here; rcp(inf) = 0.
+TA_DEVICE float ta_fast_div(float x, float y) { return x * __builtin_amdgcn_rcpf(y); }
+
 // Activation of the fused epilogue (shaders/matmul_epilogue_common.glsl:
-// 30-39 semantics).  The transcendental calls go to the HIP device math
-// library; nothing here re-implements them.
-TA_DEVICE float ta_activate(float x, uint32_t act) {
-  if (act == TA_ACT_RELU)
+// 30-39 semantics), one instantiation per activation so an epilogue loop
+// specialised on it has no per-element branches.  exp is HIP's fast
+// __expf (v_exp_f32 on x * log2 e); nothing here re-implements a library
+// routine.
+template <uint32_t ACT>
+TA_DEVICE float ta_act(float x) {
+  if constexpr (ACT == TA_ACT_RELU) {
     return fmaxf(x, 0.0f);
-  // SiLU and GELU use the HIP fast exp / divide intrinsics (a few ulp):
-  // at one wave per SIMD the precise library calls were the longest part
-  // of a large GEMM's epilogue.
-  if (act == TA_ACT_SILU)
-    return __fdividef(x, 1.0f + __expf(-x));
-  if (act == TA_ACT_GELU) {
+  } else if constexpr (ACT == TA_ACT_SILU) {
+    return ta_fast_div(x, 1.0f + __expf(-x));
+  } else if constexpr (ACT == TA_ACT_GELU) {
     // Published tanh form of GELU, 0.5 x (1 + tanh(u)) with u = sqrt(2/pi)
     // (x + 0.044715 x^3), evaluated through the identity 0.5 (1 + tanh(u))
-    // = 1 / (1 + exp(-2u)): one exp and one divide instead of tanh.
+    // = 1 / (1 + exp(-2u)): one exp and one reciprocal instead of tanh.
     const float k2 = 2.0f * 0.7978845608028654f;
-    return __fdividef(x, 1.0f + __expf(-k2 * fmaf(0.044715f * x * x, x, x)));
+    return ta_fast_div(x, 1.0f + __expf(-k2 * fmaf(0.044715f * x * x, x, x)));
+  } else {
+    return x;
   }
+}
+
+TA_DEVICE float ta_activate(float x, uint32_t act) {
+  if (act == TA_ACT_RELU)
+    return ta_act<TA_ACT_RELU>(x);
+  if (act == TA_ACT_SILU)
+    return ta_act<TA_ACT_SILU>(x);
+  if (act == TA_ACT_GELU)
+    return ta_act<TA_ACT_GELU>(x);
   return x;
+}
+
+// Calls f(std::integral_constant<uint32_t, ACT>) for the runtime
+// activation, so the loop inside f is compiled once per activation.
+template <class F>
+TA_DEVICE void ta_with_act(uint32_t act, F &&f) {
+  if (act == TA_ACT_RELU)
+    f(std::integral_constant<uint32_t, TA_ACT_RELU>{});
+  else if (act == TA_ACT_SILU)
+    f(std::integral_constant<uint32_t, TA_ACT_SILU>{});
+  else if (act == TA_ACT_GELU)
+    f(std::integral_constant<uint32_t, TA_ACT_GELU>{});
+  else
+    f(std::integral_constant<uint32_t, TA_ACT_NONE>{});
 }
 
 // Epilogue order (shaders/matmul_epilogue_common.glsl:14-21):
@@ -99,6 +132,8 @@ TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &
     __syncthreads();
     const uint32_t row0 = m0 + wm * WTM + fm * 32;
     const uint32_t col0 = n0 + wn * WTN;
+    ta_with_act(S > 1 ? (uint32_t)TA_ACT_NONE : p.act, [&](auto act_c) __attribute__((always_inline)) {
+    constexpr uint32_t ACT = decltype(act_c)::value;
 #pragma unroll 2
     for (int i = 0; i < (active ? 32 * WTN / 4 / 64 : 0); ++i) {
       const uint32_t e = lane + 64u * i;
@@ -135,7 +170,7 @@ TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &
                 &p.bias[(uint64_t)batch * p.bias_batch_stride + col]);
 #pragma unroll
           for (int c = 0; c < 4; ++c)
-            o[c] = ta_activate(o[c], p.act);
+            o[c] = ta_act<ACT>(o[c]);
           if (p.binary != TA_BIN_NONE) {
             const f32x4 d = *reinterpret_cast<const f32x4 *>(&p.d[base]);
 #pragma unroll
@@ -160,6 +195,7 @@ TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &
         }
       }
     }
+    });
     __syncthreads();
   }
 }
