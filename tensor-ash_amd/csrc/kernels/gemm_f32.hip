@@ -260,16 +260,17 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 // Pipelined FP32 kernel for whole BM x BN tiles of f32 A and B whose
 // K windows hold a multiple of 64 (K % (64 * splits) == 0): the shape of
 // the fastest vendor FP32 kernels on this chip, written out by hand.  The
-// 256x256 instance (2x2 waves of 128x128) serves plain GEMMs; 64x256 (1x4
-// waves of 64x64) and 32x128 (1x2 waves of 32x64) serve split-K stage 1
-// (and plain GEMMs that select those tiles),
+// 256x256 instance (2x2 waves of 128x128) serves plain GEMMs; 64x64 (2x2
+// waves of 32x32) and 32x128 (1x2 waves of 32x64) serve split-K stage 1,
+// 64x256 (1x4 waves of 64x64) plain GEMMs that select that tile,
 // where grid.z = batch * splits and each split writes its partial tile.
 //  * v_mfma_f32_16x16x4_f32; FM x FN blocks of 16x16 accumulators per wave
 //    (256 registers per lane at 128x128, kept in the AGPRs).  MFMA step s
 //    of a 16-deep stage takes k = (lane / 16) * 4 + s from both operands.
 //  * NS stages (ta_mi16_stages: 8 for the 32x128 tile, whose two waves
-//    per CU need the deeper look-ahead to cover the loaded memory latency;
-//    4 elsewhere, where 8 measured slower) of 16-deep A [BM][16] and
+//    per CU need the deeper look-ahead to cover the loaded memory latency,
+//    and for the 64x64 split-K tile with its 8 KiB stages; 4 elsewhere,
+//    where 8 measured slower) of 16-deep A [BM][16] and
 //    B [16][BN] slabs in LDS,
 //    filled by direct global -> LDS loads (global_load_lds_dwordx4) with
 //    16-byte chunks XOR-swizzled per row on the global side:
@@ -333,11 +334,25 @@ template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WGN, wn = wave % WGN;
-    uint32_t tm, tn;
-    ta_tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-    const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t P = p.num_splits;
-    const uint32_t batch = blockIdx.z / P, split = blockIdx.z % P;
+    // Split-K with several tiles per window: consecutive dispatch ids go
+    // to different XCDs, so deal (window, tile) pairs to the XCDs in
+    // contiguous runs - the tiles of one K window then share its A rows in
+    // one XCD's L2.  Which workgroup computes a plane does not change its
+    // value.
+    uint32_t bx = blockIdx.x, bz = blockIdx.z;
+    {
+      const uint32_t tiles = gridDim.x, G = tiles * gridDim.z;
+      if (P > 1 && tiles > 1 && G % (8 * tiles) == 0) {
+        const uint32_t L = bz * tiles + bx, v = (L & 7u) * (G >> 3) + (L >> 3);
+        bz = v / tiles;
+        bx = v % tiles;
+      }
+    }
+    uint32_t tm, tn;
+    ta_tile_coords(bx, p.tiles_m, p.tiles_n, tm, tn);
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t batch = bz / P, split = bz % P;
     // Split-K window (the GemmF32 rule; the host sends only shapes whose
     // windows all hold a multiple of 64 rows of K).
     uint32_t klo = 0, khi = p.k;
@@ -535,14 +550,18 @@ TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4, 16)
 TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2, 16)
 
 // Whole tiles of f32 A and B whose K windows hold multiples of 64 rows
-// (see GemmF32Mi16): the 256x256 data-parallel tile and the two skinny
-// split-K stage-1 tiles.
+// (see GemmF32Mi16): the 256x256 data-parallel tile and the split-K
+// stage-1 tiles (64x64: four column tiles per K window of a 64 x 256
+// output, a quarter of the 64x256 tile's partial bytes).
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m256n256_mi16(GemmArgs p) {
-  GemmF32Mi16<256, 256, 2, 2, ta_mi16_stages(256)>::run(p);
+  GemmF32Mi16<256, 256, 2, 2, ta_mi16_stages(256, 256)>::run(p);
 }
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m64n256_mi16(GemmArgs p) {
-  GemmF32Mi16<64, 256, 1, 4, ta_mi16_stages(64)>::run(p);
+  GemmF32Mi16<64, 256, 1, 4, ta_mi16_stages(64, 256)>::run(p);
 }
 extern "C" __global__ __launch_bounds__(128) void ta_gemm_f32_m32n128_mi16(GemmArgs p) {
-  GemmF32Mi16<32, 128, 1, 2, ta_mi16_stages(32)>::run(p);
+  GemmF32Mi16<32, 128, 1, 2, ta_mi16_stages(32, 128)>::run(p);
+}
+extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m64n64_mi16(GemmArgs p) {
+  GemmF32Mi16<64, 64, 2, 2, ta_mi16_stages(64, 64)>::run(p);
 }

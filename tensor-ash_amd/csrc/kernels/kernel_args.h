@@ -400,13 +400,16 @@ constexpr int ta_flash_qblocks(int /*dh*/) { return 2; }
 constexpr int ta_flash_threads(int dh) { return 64 * ta_flash_qblocks(dh) * ta_flash_parts(dh); }
 constexpr int ta_flash_rows(int dh) { return 32 * ta_flash_qblocks(dh); }
 
-// Pipeline stages of the FP32-MFMA (_mi16) kernels: 8 for the 32 x 128
-// split-K stage-1 tile (two waves per CU), 4 for the others.  Every K
-// window of a launch must hold a multiple of 16 * stages rows.
+// Pipeline stages of the FP32-MFMA (_mi16) kernels: 8 for the split-K
+// stage-1 tiles 32 x 128 (two waves per CU) and 64 x 64 (8 KiB stages), 4
+// for the others.  Every K window of a launch must hold a multiple of
+// 16 * stages rows.
 #ifndef TA_MI16_SKINNY_STAGES
 #define TA_MI16_SKINNY_STAGES 8
 #endif
-constexpr int ta_mi16_stages(int bm) { return bm == 32 ? TA_MI16_SKINNY_STAGES : 4; }
+constexpr int ta_mi16_stages(int bm, int bn) {
+  return bm == 32 || (bm == 64 && bn == 64) ? TA_MI16_SKINNY_STAGES : 4;
+}
 
 // Threads of the pipelined f16-MFMA kernels (ta_gemm_{h16,a16}_<tile>_lds,
 // ta_gemm_h16sk_<tile>): 8 waves (two per SIMD) for tiles of 128 x 64 and

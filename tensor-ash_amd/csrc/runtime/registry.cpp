@@ -128,9 +128,10 @@ uint32_t mi16_threads(uint32_t tile_m) { return tile_m == 32 ? 128u : 256u; }
 // that when K is a multiple of 16 * stages * planes); 32-bit per-lane load
 // offsets span a tile's A rows and 16 rows of B.
 bool f32_mi16_ok(const ResolvedMatmul &d, uint32_t tile_m, uint32_t tile_n, uint32_t planes) {
+  // 64 x 64 only as split-K stage 1 (plain GEMMs keep their measured routes)
   const bool tile = (tile_m == 256 && tile_n == 256) || (tile_m == 64 && tile_n == 256) ||
-                    (tile_m == 32 && tile_n == 128);
-  const uint64_t loop = 16ull * ta_mi16_stages((int)tile_m);
+                    (tile_m == 32 && tile_n == 128) || (tile_m == 64 && tile_n == 64 && planes > 1);
+  const uint64_t loop = 16ull * ta_mi16_stages((int)tile_m, (int)tile_n);
   return tile && planes >= 1 && !d.a_f16 && !d.b_f16 && d.m % tile_m == 0 && d.n % tile_n == 0 &&
          d.k > 0 && d.k % (loop * planes) == 0 && (uint64_t)tile_m * d.k * 4 < (1ull << 32) &&
          16ull * d.n * 4 < (1ull << 32);
@@ -247,13 +248,16 @@ std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims) {
 
 // ---- split-K (src/executor/splitk2.rs:36-271, retuned for 256 CUs) ----
 
-// Skinny split-K shapes take a tile spanning their whole N where possible
-// (A is then read once per window).
+// Skinny split-K shapes: 32-row outputs take a 32 x 128 tile; 64-row
+// outputs take 64 x 64 tiles, whose K windows are then four times as long
+// as those of a tile spanning N = 256 at the same workgroup count, so the
+// partial planes the reduce reads are a quarter (the tiles of one window
+// share its A rows in one XCD's L2).  Measured at 64 x 256 x 65536: stage
+// 1 + reduce 32.8 us against 36.8 us with 64 x 256 tiles.
 const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n) {
   const char *name = m >= 128 && n >= 128 ? "f32_m128n128"
                      : m <= 32            ? "f32_m32n128"
-                     : m <= 64 && n >= 256 ? "f32_m64n256"
-                                           : "f32_m64n64";
+                                          : "f32_m64n64";
   return KERNEL_SPECS[registry_index(name)];
 }
 
@@ -345,7 +349,14 @@ std::optional<uint32_t> heuristic_splits(uint32_t cus, uint32_t batch, uint32_t 
   const uint64_t tiles = (uint64_t)batch * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
   if (tiles * 2 >= cus)
     return std::nullopt;
-  const uint64_t wanted = (2ull * cus + tiles - 1) / tiles;
+  uint64_t wanted = (2ull * cus + tiles - 1) / tiles;
+  // The pipelined stage-1 kernels (whole tiles, K windows of whole
+  // pipeline loops) are fastest at one workgroup per CU: their windows
+  // are then the longest and the partial planes fewest.
+  const uint64_t one = std::max<uint64_t>(1, cus / tiles);
+  if (m % s.tile_m == 0 && n % s.tile_n == 0 &&
+      k % (16ull * ta_mi16_stages((int)s.tile_m, (int)s.tile_n) * one) == 0)
+    wanted = one;
   const uint32_t max_splits = k / 256;
   for (uint32_t splits : {128u, 64u, 32u, 16u, 8u, 4u, 2u})
     if (splits <= wanted && splits <= max_splits)

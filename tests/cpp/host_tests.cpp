@@ -179,7 +179,9 @@ static void test_splitk() {
     }
   const uint32_t cus = 256;
   // Behaviour (targets are this build's own, for 256 CUs):
-  CHECK(heuristic_splits(cus, 1, 64, 256, 65536) == 128u); // 4 tiles -> ~2 WGs per CU
+  // 4 tiles of 64x64, windows of whole pipeline loops: one WG per CU
+  CHECK(heuristic_splits(cus, 1, 64, 256, 65536) == 64u);
+  CHECK(heuristic_splits(cus, 1, 64, 256, 65536 + 64) == 128u); // unaligned: ~2 WGs per CU
   CHECK(heuristic_splits(cus, 1, 32, 128, 131072) == 128u);
   CHECK(heuristic_splits(cus, 1, 64, 64, 1024) == 4u);      // capped by K/256
   CHECK(!heuristic_splits(cus, 1, 64, 64, 512));            // K < 1024

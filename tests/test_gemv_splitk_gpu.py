@@ -353,6 +353,8 @@ def test_config4_splitk_deterministic(ta, ex, oracle, m, n, k, splits):
     # windows of whole 64-deep stages: the pipelined stage-1 kernels
     (64, 512, 8192, 4, 0.5, 2), (32, 256, 16384, 8, 1.0, 1), (64, 256, 4160, 5, 1.0, 1),
     (32, 128, 8192, 2, 2.0, 3),
+    # 64 x 64 stage-1 tiles, several per K window (dealt to the XCDs by window)
+    (64, 256, 16384, 4, 1.0, 2), (64, 1024, 32768, 8, 0.5, 1),
 ])
 def test_splitk_shapes(ta, ex, oracle, m, n, k, splits, alpha, batch):
     """tests/correctness/splitk2.rs:48-122 shapes (odd, batched, alpha)."""
