@@ -301,8 +301,13 @@ struct ExecutorImpl {
     if (splitk_eligible && !b_f16 && selection.is_auto()) {
       std::optional<uint32_t> splits =
           tuned_splits ? *tuned_splits : heuristic_splits(ctx->cu_count(), batch, m, n, k);
-      if (splits && auto_route_fits(batch, m, n, k, *splits))
+      if (splits && auto_route_fits(batch, m, n, k, *splits)) {
         plan.splitk2 = splits;
+        // Stage 1 runs on the split-K tile of run_matmuls_split_k2 (and of
+        // dispatch_info_for), so an op gives the same bits whether it is
+        // submitted alone or together with others.
+        plan.kernel = registry_index(splitk_stage1_spec(m, n).name);
+      }
     }
     return plan;
   }
