@@ -261,8 +261,8 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 // K windows hold a multiple of 64 (K % (64 * splits) == 0): the shape of
 // the fastest vendor FP32 kernels on this chip, written out by hand.  The
 // 256x256 instance (2x2 waves of 128x128) serves plain GEMMs; 64x64 (2x2
-// waves of 32x32) and 32x128 (1x2 waves of 32x64) serve split-K stage 1,
-// 64x256 (1x4 waves of 64x64) plain GEMMs that select that tile,
+// waves of 32x32) and 32x64 (1x2 waves of 32x32) serve split-K stage 1,
+// 64x256 and 32x128 plain GEMMs that select those tiles,
 // where grid.z = batch * splits and each split writes its partial tile.
 //  * v_mfma_f32_16x16x4_f32; FM x FN blocks of 16x16 accumulators per wave
 //    (256 registers per lane at 128x128, kept in the AGPRs).  MFMA step s
@@ -548,11 +548,13 @@ TA_GEMM_F32_FAMILY(m64n64, 64, 64, 2, 2, 16)
 // read once): 64x256 with 1x4 waves, 32x128 with 1x2 waves (128 threads).
 TA_GEMM_F32_FAMILY(m64n256, 64, 256, 1, 4, 16)
 TA_GEMM_F32_FAMILY(m32n128, 32, 128, 1, 2, 16)
+TA_GEMM_F32_FAMILY(m32n64, 32, 64, 1, 2, 16)
 
 // Whole tiles of f32 A and B whose K windows hold multiples of 64 rows
 // (see GemmF32Mi16): the 256x256 data-parallel tile and the split-K
-// stage-1 tiles (64x64: four column tiles per K window of a 64 x 256
-// output, a quarter of the 64x256 tile's partial bytes).
+// stage-1 tiles (64x64 and 32x64: several column tiles per K window, so
+// the windows are longer and the partial planes fewer than with one tile
+// spanning N).
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m256n256_mi16(GemmArgs p) {
   GemmF32Mi16<256, 256, 2, 2, ta_mi16_stages(256, 256)>::run(p);
 }
@@ -564,4 +566,7 @@ extern "C" __global__ __launch_bounds__(128) void ta_gemm_f32_m32n128_mi16(GemmA
 }
 extern "C" __global__ __launch_bounds__(256) void ta_gemm_f32_m64n64_mi16(GemmArgs p) {
   GemmF32Mi16<64, 64, 2, 2, ta_mi16_stages(64, 64)>::run(p);
+}
+extern "C" __global__ __launch_bounds__(128) void ta_gemm_f32_m32n64_mi16(GemmArgs p) {
+  GemmF32Mi16<32, 64, 1, 2, ta_mi16_stages(32, 64)>::run(p);
 }

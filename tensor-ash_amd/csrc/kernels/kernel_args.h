@@ -400,8 +400,8 @@ constexpr int ta_flash_qblocks(int /*dh*/) { return 2; }
 constexpr int ta_flash_threads(int dh) { return 64 * ta_flash_qblocks(dh) * ta_flash_parts(dh); }
 constexpr int ta_flash_rows(int dh) { return 32 * ta_flash_qblocks(dh); }
 
-// Pipeline stages of the FP32-MFMA (_mi16) kernels: 8 for the split-K
-// stage-1 tiles 32 x 128 (two waves per CU) and 64 x 64 (8 KiB stages), 4
+// Pipeline stages of the FP32-MFMA (_mi16) kernels: 8 for the 32-row
+// tiles (two waves per CU) and the 64 x 64 split-K tile (8 KiB stages), 4
 // for the others.  Every K window of a launch must hold a multiple of
 // 16 * stages rows.
 #ifndef TA_MI16_SKINNY_STAGES

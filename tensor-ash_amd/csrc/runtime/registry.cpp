@@ -22,6 +22,7 @@ const KernelSpec KERNEL_SPECS[] = {
     {"f32_m64n64", 64, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m64n64", "small"},
     {"f32_m64n256", 64, 256, 16, KernelKind::GemmF32, "ta_gemm_f32_m64n256", ""},
     {"f32_m32n128", 32, 128, 16, KernelKind::GemmF32, "ta_gemm_f32_m32n128", ""},
+    {"f32_m32n64", 32, 64, 16, KernelKind::GemmF32, "ta_gemm_f32_m32n64", ""},
     {"f16w_m256n256", 256, 256, 32, KernelKind::GemmF16w, "ta_gemm_f16w_m256n256", ""},
     {"f16w_m256n128", 256, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m256n128", ""},
     {"f16w_m128n128", 128, 128, 16, KernelKind::GemmF16w, "ta_gemm_f16w_m128n128", ""},
@@ -130,7 +131,8 @@ uint32_t mi16_threads(uint32_t tile_m) { return tile_m == 32 ? 128u : 256u; }
 bool f32_mi16_ok(const ResolvedMatmul &d, uint32_t tile_m, uint32_t tile_n, uint32_t planes) {
   // 64 x 64 only as split-K stage 1 (plain GEMMs keep their measured routes)
   const bool tile = (tile_m == 256 && tile_n == 256) || (tile_m == 64 && tile_n == 256) ||
-                    (tile_m == 32 && tile_n == 128) || (tile_m == 64 && tile_n == 64 && planes > 1);
+                    (tile_m == 32 && tile_n == 128) ||
+                    (((tile_m == 64 && tile_n == 64) || (tile_m == 32 && tile_n == 64)) && planes > 1);
   const uint64_t loop = 16ull * ta_mi16_stages((int)tile_m, (int)tile_n);
   return tile && planes >= 1 && !d.a_f16 && !d.b_f16 && d.m % tile_m == 0 && d.n % tile_n == 0 &&
          d.k > 0 && d.k % (loop * planes) == 0 && (uint64_t)tile_m * d.k * 4 < (1ull << 32) &&
@@ -248,15 +250,16 @@ std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims) {
 
 // ---- split-K (src/executor/splitk2.rs:36-271, retuned for 256 CUs) ----
 
-// Skinny split-K shapes: 32-row outputs take a 32 x 128 tile; 64-row
-// outputs take 64 x 64 tiles, whose K windows are then four times as long
-// as those of a tile spanning N = 256 at the same workgroup count, so the
-// partial planes the reduce reads are a quarter (the tiles of one window
-// share its A rows in one XCD's L2).  Measured at 64 x 256 x 65536: stage
-// 1 + reduce 32.8 us against 36.8 us with 64 x 256 tiles.
+// Skinny split-K shapes take 64-column tiles (64 x 64, or 32 x 64 for
+// outputs of at most 32 rows): at the same workgroup count their K windows
+// are longer than those of a tile spanning N, so the partial planes the
+// reduce reads are fewer (the tiles of one window share its A rows in one
+// XCD's L2).  Measured, stage 1 + reduce: 64 x 256 x 65536 32.8 us against
+// 36.8 us with 64 x 256 tiles; 32 x 128 x 131072 30.4 against 31.8 us
+// with 32 x 128 tiles.
 const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n) {
   const char *name = m >= 128 && n >= 128 ? "f32_m128n128"
-                     : m <= 32            ? "f32_m32n128"
+                     : m <= 32            ? "f32_m32n64"
                                           : "f32_m64n64";
   return KERNEL_SPECS[registry_index(name)];
 }
