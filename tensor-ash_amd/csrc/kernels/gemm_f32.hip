@@ -280,10 +280,10 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 //      B rows (BN * 4 bytes): chunk ^ 4 * ((row >> 2) & 3), so the four rows a
 //        wave reads at once (k = group * 4 + s) use four 16-bank quarters.
 //  * One barrier per stage.  The LDS operands of stage k+1 are read into a
-//    second register set while stage k's MFMAs run, and the side
-//    operations of a stage (direct loads, ds_read_b128 of A,
-//    ds_read2st64_b32 of B) are spread evenly between them, so the MFMA pipe
-//    never waits on LDS latency or instruction issue.  The MFMAs and side
+//    second register set while stage k's MFMAs run: the side operations of
+//    a stage (direct loads, ds_read_b128 of A, ds_read2st64_b32 of B) go
+//    one after each of its first MFMAs, so their latency is covered by the
+//    rest of the stage and the MFMA pipe never waits on LDS.  The MFMAs and side
 //    operations are volatile inline asm so this order is the one executed;
 //    the explicit s_waitcnt at the end of a stage covers the register set
 //    read during it.
@@ -321,13 +321,13 @@ template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
     return (((row >> 1) ^ (row >> 3)) & 1u) | (((row >> 2) & 1u) << 1);
   }
   static TA_DEVICE uint32_t swz_b(uint32_t row) { return 4u * ((row >> 2) & 3u); }
-  // The side operation issued after MFMA i of a stage, or -1.
-  static constexpr int side_after(int i) {
-    for (int j = 0; j < SIDE; ++j)
-      if ((j + 1) * MFMAS / SIDE - 1 == i)
-        return j;
-    return -1;
-  }
+  // The side operation issued after MFMA i of a stage, or -1: one after
+  // each of the first SIDE MFMAs, so the next stage's LDS reads land under
+  // this stage's remaining MFMAs.  (Spread evenly over the stage, the last
+  // read followed the last MFMA and its latency was exposed at the stage's
+  // closing lgkmcnt wait: 5% of a 64x64 split-K tile's stage-1 time, ~1%
+  // of the 256x256 tile's.)
+  static constexpr int side_after(int i) { return i < SIDE ? i : -1; }
 
   static TA_DEVICE void run(const GemmArgs &p) {
     __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
@@ -475,8 +475,8 @@ template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
     auto body = [&](auto stg_c, uint32_t kt) __attribute__((always_inline)) {
       constexpr int stg = decltype(stg_c)::value, cur = stg % 2; // stg = kt % NS
       asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * LD) : "memory");
-      // Side operation j follows MFMA (j + 1) * MFMAS / SIDE - 1: loads at
-      // the even slots below 2 * LD, LDS reads in the others.
+      // Side operation j follows MFMA j: loads at the even slots below
+      // 2 * LD, LDS reads in the others.
       ta_static_for<MFMAS>([&](auto ic) __attribute__((always_inline)) {
         constexpr int i = decltype(ic)::value;
         mfma(std::integral_constant<int, cur>{}, ic);
