@@ -989,15 +989,16 @@ template <int MR> constexpr int standalone_unroll() { return MR >= 4 ? 8 : 16; }
 // tail.  No launch-wide counter is touched at
 // unit start (one hot atomic would serialise the starts).
 // K windows: gate/up units take 256 rows (one group of 16 loads per
-// matrix); down units take 512 rows (one group of 32 loads) so they are
-// fewer and a down unit's whole weight window is in flight before it
-// starts waiting.
-constexpr int kMlpRowsA = 256;
-constexpr int kMlpRowsB = 512;
+// matrix), down units 256 rows too (one group of 16 loads; 512-row down
+// windows, half as many units, measured the same at one row and 1-2%
+// slower at four and eight).
+constexpr int kMlpRowsA = TA_MLP_ROWS_A;
+constexpr int kMlpRowsB = TA_MLP_ROWS_B;
+static_assert(kMlpRowsA % 256 == 0 && kMlpRowsB % 256 == 0, "whole groups of 16 loads");
 
 template <int MR> struct DecodeMlp {
-  typedef Gemv<MR, true, 64, false, kProducer, kMlpRowsA, 16> A;
-  typedef Gemv<MR, false, 64, false, kConsumer, kMlpRowsB, 32> B;
+  typedef Gemv<MR, true, 64, false, kProducer, kMlpRowsA, kMlpRowsA / 16> A;
+  typedef Gemv<MR, false, 64, false, kConsumer, kMlpRowsB, kMlpRowsB / 16> B;
   union Smem {
     typename A::Smem a;
     typename B::Smem b;

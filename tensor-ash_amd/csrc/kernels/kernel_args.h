@@ -360,6 +360,15 @@ typedef struct AttnCombineArgs {
 // no hand-off word ever needs clearing.  The a/b partial and counters
 // fields are unused: the tagged buffers replace them.
 #define TA_MLP_MAX_LAYERS 16
+// K windows of the decode MLP's two phases: gate/up units take
+// TA_MLP_ROWS_A rows of x, down units TA_MLP_ROWS_B rows of h (multiples of
+// 256; a unit issues rows / 16 weight loads per lane and matrix).
+#ifndef TA_MLP_ROWS_A
+#define TA_MLP_ROWS_A 256
+#endif
+#ifndef TA_MLP_ROWS_B
+#define TA_MLP_ROWS_B 256
+#endif
 
 typedef struct MlpLayer {
   GemvArgs a;

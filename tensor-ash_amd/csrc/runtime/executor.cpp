@@ -860,8 +860,8 @@ struct ExecutorImpl {
     uint32_t mr, tiles_a, kch_a, tiles_b, kch_b;
     uint64_t gen, done, tag_a, tag_h, tag_b, tag_y, bytes;
   };
-  // K windows of the two phases (kernel constants kMlpRowsA / kMlpRowsB).
-  static constexpr uint32_t kMlpRowsA = 256, kMlpRowsB = 512;
+  // K windows of the two phases (shared with the kernel).
+  static constexpr uint32_t kMlpRowsA = TA_MLP_ROWS_A, kMlpRowsB = TA_MLP_ROWS_B;
 
   static MlpGeom mlp_geom(const ResolvedMatmul &up, const ResolvedMatmul &down) {
     MlpGeom g{};

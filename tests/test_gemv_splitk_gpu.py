@@ -126,7 +126,7 @@ def test_swiglu_mlp_graph(ta, ex, oracle, m, monkeypatch):
     one dependent op graph (tools/llama-ash forward/mod.rs:186-210).  The
     three ops run as one persistent decode-MLP launch.  The gate/up outputs
     are bit-identical to the unfused launches (same K windows); the
-    down-proj sums K in 512-row windows inside the MLP launch and in the
+    down-proj sums K in 256-row windows inside the MLP launch and in the
     planner's windows standalone, so both are checked against the oracle,
     and repeated MLP launches must repeat their bits."""
     monkeypatch.setenv("TA_MLP_MAX_ROWS", "8")  # the MLP launch at every M (the default)
