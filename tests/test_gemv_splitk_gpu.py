@@ -239,6 +239,51 @@ def test_decode_mlp_chain(ta, ex, oracle, m, monkeypatch):
     prep.close()
 
 
+@pytest.mark.parametrize("m", [1, 4])
+def test_decode_mlp_chain_256_row_windows(ta, ex, oracle, m, monkeypatch):
+    """Hidden 768 and FFN 1280: K windows of 256 rows in both phases, and
+    an FFN width that is not a multiple of 512 (5 down windows).  Two
+    chained layers, each checked against the oracle on the GPU's own layer
+    input; the chain gives the bits of per-layer MLP launches."""
+    monkeypatch.setenv("TA_MLP_MAX_ROWS", "8")
+    hdim, ffn, layers = 768, 1280, 2
+    pk = lambda w, k, n: ex.tensor_from(ta.pack_f16w_row_tiles(w, k, n, ta.f16w_row_tile_n(k, n)),
+                                        shape=[k, n], f16=True)
+    wts, refs = [], []
+    for l in range(layers):
+        wg, wgr = f16_weights(oracle, hdim, ffn, 501 + 3 * l)
+        wu, wur = f16_weights(oracle, hdim, ffn, 502 + 3 * l)
+        wd, wdr = f16_weights(oracle, ffn, hdim, 503 + 3 * l)
+        wts.append((pk(wg, hdim, ffn), pk(wu, hdim, ffn), pk(wd, ffn, hdim)))
+        refs.append((wgr, wur, wdr))
+    xs = [ex.tensor_from(oracle.fill_det(m * hdim, 53), shape=[m, hdim])]
+    xs += [ex.tensor([m, hdim]) for _ in range(layers)]
+    ups = [ex.tensor([m, ffn]) for _ in range(layers)]
+    hs = [ex.tensor([m, ffn]) for _ in range(layers)]
+    ops = []
+    for l in range(layers):
+        ops += _mlp_layer_ops(ta, xs[l], wts[l], ups[l], hs[l], xs[l + 1], xs[l])
+    ex.run_op_graph(ops)
+    got = [ex.download(t).copy() for t in xs + ups + hs]
+    for l in range(layers):
+        wgr, wur, wdr = refs[l]
+        xin = got[l]
+        ref_up = oracle.cpu_bmm(xin, wur, None, 1, m, ffn, hdim)
+        ref_h = oracle.reference_gemm(xin, wgr, 1, m, ffn, hdim, act=2, binary=2, d=ref_up)
+        check_f16(got[layers + 1 + l], ref_up, hdim, oracle)
+        check_f16(got[2 * layers + 1 + l], ref_h, hdim, oracle)
+        ref_y = oracle.reference_gemm(got[2 * layers + 1 + l], wdr, 1, m, hdim, ffn, binary=1, d=xin,
+                                      beta=1.0)
+        check_f16(got[l + 1], ref_y, ffn, oracle)
+    for t in xs[1:] + ups + hs:
+        ex.upload(t, np.zeros(int(np.prod(t.shape)), np.float32))
+    monkeypatch.setenv("TA_NO_MLP_CHAIN", "1")
+    ex.run_op_graph(ops)
+    monkeypatch.delenv("TA_NO_MLP_CHAIN")
+    for a, b in zip([ex.download(t) for t in xs + ups + hs], got):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_decode_mlp_chain_long(ta, ex, oracle, monkeypatch):
     """18 layers over two ping-pong activation buffers and shared up/h
     buffers (the decode-forward form): the executor splits the chain into
