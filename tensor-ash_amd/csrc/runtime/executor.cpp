@@ -428,7 +428,12 @@ struct ExecutorImpl {
         return e[1];
       return e[0].age <= e[1].age ? e[0] : e[1];
     }
+    // A copy written at `v.base` replaces whatever entry that memory held
+    // (every dual launch writes its f16 output copy to the same scratch).
     void put(CvtEntry &slot, CvtEntry v) {
+      for (auto &x : e)
+        if (&x != &slot && x.buffer && x.base == v.base)
+          x = CvtEntry{};
       v.age = ++clock;
       slot = v;
     }

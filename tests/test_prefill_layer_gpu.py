@@ -234,3 +234,39 @@ def test_f16_copy_cache_reuse_and_invalidation(ta, ex, oracle):
     ref = oracle.reference_gemm(oracle.round_via_f16(new_x.reshape(-1)), oracle.round_via_f16(w4), 1, m, n, k)
     err, idx = oracle.max_abs_err(ex.download(c[3]).reshape(-1), ref)
     assert err <= 2 * oracle.tolerance(k) + 1e-4, f"abs err {err} at {idx}"
+
+
+def test_f16_copy_cache_two_swiglu_outputs(ta, ex, oracle):
+    """Two SwiGLU triples in one submission, each dual launch leaving the
+    f16 copy of its output h for its down projection in the same scratch.
+    A later GEMM that reads the first h as A must not be served the second
+    h's copy: it equals the same GEMM run alone, bit for bit."""
+    m, hid, ffn = 256, 512, 768
+    hx = oracle.fill_det(m * hid, 6301)
+    x = ex.tensor_from(hx, shape=[m, hid])
+    wt = lambda k, n, s: ex.tensor_from(oracle.fill_normal(k * n, s, 0.02), shape=[k, n], f16=True)
+    wu1, wg1, wu2, wg2 = (wt(hid, ffn, s) for s in (6302, 6303, 6304, 6305))
+    wd1, wd2, wd3 = (wt(ffn, hid, s) for s in (6306, 6307, 6308))
+    u1, h1, u2, h2 = (ex.tensor([m, ffn]) for _ in range(4))
+    y1, y2, z = (ex.tensor([m, hid]) for _ in range(3))
+    E = ta.Epilogue
+    ops = [ta.MatmulOp(x, wu1, u1),
+           ta.MatmulOp(x, wg1, h1, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=u1)),
+           ta.MatmulOp(h1, wd1, y1),
+           ta.MatmulOp(x, wu2, u2),
+           ta.MatmulOp(x, wg2, h2, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=u2)),
+           ta.MatmulOp(h2, wd2, y2),
+           ta.MatmulOp(h1, wd3, z)]
+    print("f16 copy cache: two SwiGLU outputs, first h re-read", flush=True)
+    ex.run_op_graph(ops)
+    got = {name: ex.download(t).copy() for name, t in (("h1", h1), ("h2", h2), ("y1", y1), ("y2", y2), ("z", z))}
+    assert not np.array_equal(got["h1"], got["h2"])
+
+    def alone(a_t, w_t):
+        out = ex.tensor([m, hid])
+        ex.run_ops([ta.MatmulOp(a_t, w_t, out)])
+        return ex.download(out)
+
+    np.testing.assert_array_equal(got["y1"], alone(h1, wd1))
+    np.testing.assert_array_equal(got["y2"], alone(h2, wd2))
+    np.testing.assert_array_equal(got["z"], alone(h1, wd3))
