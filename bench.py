@@ -311,23 +311,41 @@ def gemv_chain(ta, ex, iters=30):
     and written.  `packed_op_graph`: the same step with the weights packed
     in 64-column tiles (the decode layout) as one op graph: q, k and v share
     a launch, then o, then the normed MLP as one decode-MLP launch;
-    `packed_prepared`: that graph captured once and replayed."""
+    `packed_prepared`: that graph captured once per weight set and
+    replayed.  Consecutive timed steps read different weight sets
+    (`copies` of them, together larger than the 256 MB last-level cache),
+    as a decode over all of a model's layers does."""
     rng = np.random.default_rng(71)
     hid, ffn, kv = 2048, 5632, 256
-    w = lambda k, n: ex.tensor_from((rng.standard_normal((k, n), dtype=np.float32) * 0.02), f16=True)
+    shapes = ((hid, hid), (hid, kv), (hid, kv), (hid, hid), (hid, ffn), (hid, ffn), (ffn, hid))
+    nbytes = 2 * (2 * hid * hid + 2 * hid * kv + 2 * hid * ffn + ffn * hid)
+    copies = max(3, math.ceil(LLC_BYTES / nbytes) + 1)
     x = ex.tensor_from(rng.uniform(-1, 1, (1, hid)).astype(np.float32))
     norm = ex.tensor_from(rng.uniform(0.5, 1.5, hid).astype(np.float32))
-    wq, wk, wv, wo, wu, wg, wd = w(hid, hid), w(hid, kv), w(hid, kv), w(hid, hid), w(hid, ffn), w(hid, ffn), w(ffn, hid)
     q, k, v, o, up, g, y = (ex.tensor([1, n]) for n in (hid, kv, kv, hid, ffn, ffn, hid))
     E = ta.Epilogue
     nm = dict(normed_a=(norm, 1e-5))
-    jobs = [ta.MatmulOp(x, wq, q, **nm), ta.MatmulOp(x, wk, k, **nm), ta.MatmulOp(x, wv, v, **nm),
-            ta.MatmulOp(q, wo, o, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0)),
-            ta.MatmulOp(o, wu, up, **nm),
-            ta.MatmulOp(o, wg, g, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up), **nm),
-            ta.MatmulOp(g, wd, y, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=o, beta=1.0))]
-    nbytes = 2 * (2 * hid * hid + 2 * hid * kv + 2 * hid * ffn + ffn * hid)
-    out = {"weight_bytes": nbytes}
+
+    def step_ops(ws, **pb):
+        wq, wk, wv, wo, wu, wg, wd = ws
+        return [ta.MatmulOp(x, wq, q, **nm, **pb), ta.MatmulOp(x, wk, k, **nm, **pb),
+                ta.MatmulOp(x, wv, v, **nm, **pb),
+                ta.MatmulOp(q, wo, o, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0), **pb),
+                ta.MatmulOp(o, wu, up, **nm, **pb),
+                ta.MatmulOp(o, wg, g, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up),
+                            **nm, **pb),
+                ta.MatmulOp(g, wd, y, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=o, beta=1.0), **pb)]
+
+    def rotated(run, n_sets):
+        for i in range(2 * n_sets):
+            run(i % n_sets)
+        return median_ns([run(i % n_sets) for i in range(iters)])
+
+    weights = lambda k_, n_: (rng.standard_normal(k_ * n_, dtype=np.float32) * 0.02).astype(np.float32)
+    row_sets = [[ex.tensor_from(weights(kk, nn), shape=[kk, nn], f16=True) for kk, nn in shapes]
+                for _ in range(copies)]
+    chains = [step_ops(ws) for ws in row_sets]
+    out = {"weight_bytes": nbytes, "weight_copies": copies}
     saved = os.environ.pop("ML_DEVICE_SCOPE", None)
     try:
         for name, env in (("list_order", None), ("persistent", "1")):
@@ -335,39 +353,25 @@ def gemv_chain(ta, ex, iters=30):
                 os.environ["ML_DEVICE_SCOPE"] = env
             else:
                 os.environ.pop("ML_DEVICE_SCOPE", None)
-            for _ in range(5):
-                ex.run_gemv_chain(jobs)
-            ns = median_ns([ex.run_gemv_chain(jobs) for _ in range(iters)])
+            ns = rotated(lambda i: ex.run_gemv_chain(chains[i]), copies)
             out[name] = dict(us=ns / 1e3, gbps=nbytes / ns, frac_hbm=nbytes / ns / PEAK_HBM)
     finally:
         os.environ.pop("ML_DEVICE_SCOPE", None)
         if saved is not None:
             os.environ["ML_DEVICE_SCOPE"] = saved
+    del chains, row_sets
 
-    def packed(k, n):
-        wt = (rng.standard_normal(k * n, dtype=np.float32) * 0.02).astype(np.float32)
-        return ex.tensor_from(ta.pack_f16w_row_tiles(wt, k, n, 64), shape=[k, n], f16=True)
-
-    pq, pk, pv, po, pu, pg, pd = (packed(kk, n) for kk, n in ((hid, hid), (hid, kv), (hid, kv), (hid, hid),
-                                                             (hid, ffn), (hid, ffn), (ffn, hid)))
-    pb = dict(packed_b=True)
-    layer = [ta.MatmulOp(x, pq, q, **nm, **pb), ta.MatmulOp(x, pk, k, **nm, **pb),
-             ta.MatmulOp(x, pv, v, **nm, **pb),
-             ta.MatmulOp(q, po, o, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0), **pb),
-             ta.MatmulOp(o, pu, up, **nm, **pb),
-             ta.MatmulOp(o, pg, g, epilogue=E(activation=ta.ACTIVATION_SILU, binary=ta.BINARY_MUL, d=up), **nm, **pb),
-             ta.MatmulOp(g, pd, y, epilogue=E(binary=ta.BINARY_ADD_SCALED, d=o, beta=1.0), **pb)]
-    for _ in range(5):
-        ex.run_op_graph(layer)
-    ns = median_ns([ex.run_op_graph(layer) for _ in range(iters)])
+    packed_sets = [[ex.tensor_from(ta.pack_f16w_row_tiles(weights(kk, nn), kk, nn, 64), shape=[kk, nn], f16=True)
+                    for kk, nn in shapes] for _ in range(copies)]
+    layers = [step_ops(ws, packed_b=True) for ws in packed_sets]
+    ns = rotated(lambda i: ex.run_op_graph(layers[i]), copies)
     out["packed_op_graph"] = dict(us=ns / 1e3, gbps=nbytes / ns, frac_hbm=nbytes / ns / PEAK_HBM)
-    prep = ex.prepare_op_graph(layer)
+    preps = [ex.prepare_op_graph(layer) for layer in layers]
     try:
-        for _ in range(5):
-            prep.run()
-        ns = median_ns([prep.run() for _ in range(iters)])
+        ns = rotated(lambda i: preps[i].run(), copies)
     finally:
-        prep.close()
+        for prep in preps:
+            prep.close()
     out["packed_prepared"] = dict(us=ns / 1e3, gbps=nbytes / ns, frac_hbm=nbytes / ns / PEAK_HBM)
     return out
 
