@@ -240,29 +240,63 @@ def splitk(ta, ex, iters=10):
 
 
 def prefill_layer(ta, ex, iters=10):
-    """Config 5 GEMMs (TinyLlama-1.1B-shaped, seq 512, f16 weights, f32 acts)."""
+    """Config 5 GEMMs (TinyLlama-1.1B-shaped, seq 512, f16 weights, f32 acts).
+    Consecutive timed runs read different weight sets (`weight_copies` of
+    them, together larger than the 256 MB last-level cache), as a prefill
+    over all of a model's layers does."""
     s, hid, ffn, qkv = 512, 2048, 5632, 2560
     rng = np.random.default_rng(61)
-    wt = lambda k, n: ex.tensor_from((rng.standard_normal((k, n), dtype=np.float32) * 0.02), f16=True)
+    host_w = {}
+
+    def wt(k, n, key):
+        # Copies of one weight share their host values: only their number
+        # (and so the bytes a rotation streams) matters to the caches.
+        if key not in host_w:
+            host_w[key] = (rng.standard_normal((k, n), dtype=np.float32) * 0.02).astype(np.float32)
+        return ex.tensor_from(host_w[key], f16=True)
+
+    cold = lambda nbytes: max(3, math.ceil(LLC_BYTES / nbytes) + 1)  # sets whose sum exceeds the LLC
     x = ex.tensor_from(rng.uniform(-1, 1, (s, hid)).astype(np.float32))
     attn = ex.tensor_from(rng.uniform(-1, 1, (s, hid)).astype(np.float32))
-    wq, wo, wg, wu, wd = wt(hid, qkv), wt(hid, hid), wt(hid, ffn), wt(hid, ffn), wt(ffn, hid)
+    w_bytes = 2 * (hid * qkv + hid * hid + 2 * hid * ffn + ffn * hid)
+    copies = cold(w_bytes)
+    sets = [(wt(hid, qkv, "q"), wt(hid, hid, "o"), wt(hid, ffn, "g"), wt(hid, ffn, "u"), wt(ffn, hid, "d"))
+            for _ in range(copies)]
     q, o, up, h, y = ex.tensor([s, qkv]), ex.tensor([s, hid]), ex.tensor([s, ffn]), ex.tensor([s, ffn]), ex.tensor([s, hid])
-    cases = {
-        "qkv_512x2560x2048": [ta.MatmulOp(x, wq, q)],
-        "o_512x2048x2048": [ta.MatmulOp(attn, wo, o, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0))],
-        "up_512x5632x2048": [ta.MatmulOp(x, wu, up)],
-        "gate_silu_mul_512x5632x2048": [ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=2, binary=2, d=up))],
-        "down_512x2048x5632": [ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=1, d=x, beta=1.0))],
-    }
-    out = {}
+
+    def cases(ws):
+        wq, wo, wg, wu, wd = ws
+        return {
+            "qkv_512x2560x2048": [ta.MatmulOp(x, wq, q)],
+            "o_512x2048x2048": [ta.MatmulOp(attn, wo, o, epilogue=ta.Epilogue(binary=ta.BINARY_ADD_SCALED, d=x, beta=1.0))],
+            "up_512x5632x2048": [ta.MatmulOp(x, wu, up)],
+            "gate_silu_mul_512x5632x2048": [ta.MatmulOp(x, wg, h, epilogue=ta.Epilogue(activation=2, binary=2, d=up))],
+            "down_512x2048x5632": [ta.MatmulOp(h, wd, y, epilogue=ta.Epilogue(binary=1, d=x, beta=1.0))],
+        }
+
+    per_set = [cases(ws) for ws in sets]
+
+    def rotated(run, n_sets):
+        for i in range(n_sets):
+            run(i)
+        return median_ns([run(i % n_sets) for i in range(max(iters, n_sets))])
+
+    out = {"weight_copies": copies}
     total_ns = 0.0
     total_flops = 0.0
     total_bytes = 0.0
-    for name, ops in cases.items():
-        for _ in range(3):
-            ex.run_ops(ops)
-        ns = median_ns([ex.run_ops(ops) for _ in range(iters)])
+    case_w = {"qkv": ("q", hid, qkv, 0), "o": ("o", hid, hid, 1), "up": ("u", hid, ffn, 3),
+              "gate": ("g", hid, ffn, 2), "down": ("d", ffn, hid, 4)}
+    for name, ops in per_set[0].items():
+        # A single GEMM alone: enough copies of its one weight to exceed the
+        # LLC (the layer's sets alone would still fit).
+        key, kk_w, nn_w, pos = case_w[name.split("_")[0]]
+        n_case = cold(2 * kk_w * nn_w)
+        extra = [wt(kk_w, nn_w, key) for _ in range(max(0, n_case - copies))]
+        ws_case = [sets[i][pos] for i in range(copies)] + extra
+        case_ops = [[ta.MatmulOp(op.a, w_i, op.c, epilogue=op.epilogue) for op in ops] for w_i in ws_case]
+        ns = rotated(lambda i: ex.run_ops(case_ops[i]), len(case_ops))
+        del case_ops, extra
         mm, nn, kk = [int(v) for v in name.split("_")[-1].split("x")]
         flops = 2.0 * mm * nn * kk
         # A f32, W f16, C f32 (+ D f32 for the binary epilogues)
@@ -281,21 +315,20 @@ def prefill_layer(ta, ex, iters=10):
     # graph (one event pair).  up and gate run as one dual launch, which
     # also leaves the f16 copy of h that down reads; x is converted for QKV
     # and again for up/gate (O's conversion of attn sits between them).
-    layer = [op for ops in cases.values() for op in ops]
-    for _ in range(3):
-        ex.run_op_graph(layer)
-    ns = median_ns([ex.run_op_graph(layer) for _ in range(iters)])
+    layers = [[op for ops in c.values() for op in ops] for c in per_set]
+    ns = rotated(lambda i: ex.run_op_graph(layers[i]), copies)
     out["layer_gemms_one_submission"] = dict(
         us=ns / 1e3, tflops=total_flops / ns / 1e3,
         roofline=time_roofline(total_flops, total_bytes, ns * 1e-9, PEAK_FP16_MFMA))
-    # The same graph prepared once (prepare_op_graph: captured as a
-    # hipGraph) and replayed, as a prefill that runs its layer repeatedly
-    # would; the events bracket the replay.
-    prepared = ex.prepare_op_graph(layer)
-    for _ in range(3):
-        prepared.run()
-    ns = median_ns([prepared.run() for _ in range(iters)])
-    prepared.close()
+    # The same graph prepared once per weight set (prepare_op_graph:
+    # captured as a hipGraph) and replayed, as a prefill that runs its
+    # layers repeatedly would; the events bracket the replay.
+    preps = [ex.prepare_op_graph(layer) for layer in layers]
+    try:
+        ns = rotated(lambda i: preps[i].run(), copies)
+    finally:
+        for prep in preps:
+            prep.close()
     out["layer_gemms_prepared"] = dict(
         us=ns / 1e3, tflops=total_flops / ns / 1e3,
         roofline=time_roofline(total_flops, total_bytes, ns * 1e-9, PEAK_FP16_MFMA))
