@@ -205,13 +205,19 @@ static size_t pick_f16_mfma(bool a16, uint32_t cus, uint32_t batch, uint32_t m, 
   auto tiles = [&](uint32_t bm, uint32_t bn) {
     return (uint64_t)batch * div_ceil(m, bm) * div_ceil(n, bn);
   };
+  // Chosen with the weights streamed from HBM (a model's layers together
+  // exceed the last-level cache): with more columns than rows, 64 x 128
+  // tiles beat 128 x 64 at the same tile count (512x2560x2048: 17.9 against
+  // 19.3 us), and deep-K shapes split 128 x 128 tiles rather than 128 x 64
+  // (512x2048x5632: 26.4 us with 4 splits against 29.5 with 2).
   const uint64_t most = cus * 6ull / 10;
+  const bool wide = n > m && tiles(64, 128) == tiles(128, 64);
   const char *tile = tiles(256, 256) >= cus   ? "m256n256"
                      : tiles(128, 128) >= most ? "m128n128"
-                     : tiles(128, 64) >= most  ? "m128n64"
+                     : tiles(128, 64) >= most  ? (wide ? "m64n128" : "m128n64")
                                                : "m64n64";
   if (!a16 && std::string(tile) == "m64n64" && k / 64 >= 64 && 2 * tiles(128, 64) <= cus)
-    return registry_index("f16w_sk_m128n64");
+    return registry_index(2 * tiles(128, 128) <= cus ? "f16w_sk_m128n128" : "f16w_sk_m128n64");
   return registry_index((pre + tile).c_str());
 }
 

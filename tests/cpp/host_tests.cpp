@@ -132,11 +132,13 @@ static void test_routing() {
   CHECK(name(8, 2048, 2048, 2048, false, false) == "f32_m256n256");
   CHECK(name(1, 512, 512, 512, false, false) == "f32_m64n64");
   // config-5 prefill shapes (M = 512): QKV, O, gate/up, down
-  CHECK(name(1, 512, 2560, 2048, true, false) == "f16w_mfma_m128n64");
+  CHECK(name(1, 512, 2560, 2048, true, false) == "f16w_mfma_m64n128");
+  CHECK(name(1, 2560, 512, 2048, true, false) == "f16w_mfma_m128n64");
   CHECK(name(1, 512, 2048, 2048, true, false) == "f16w_mfma_m64n64");
   CHECK(name(1, 512, 5632, 2048, true, false) == "f16w_mfma_m128n128");
-  CHECK(name(1, 512, 2048, 5632, true, false) == "f16w_sk_m128n64");
+  CHECK(name(1, 512, 2048, 5632, true, false) == "f16w_sk_m128n128");
   CHECK(h16sk_splits(cus, 1, 512, 2048, 5632, 128, 64) == 2);
+  CHECK(h16sk_splits(cus, 1, 512, 2048, 5632, 128, 128) == 4);
   CHECK(h16sk_splits(cus, 1, 4096, 4096, 4096, 64, 128) == 1);
   CHECK(name(1, 4096, 4096, 4096, true, false) == "f16w_mfma_m256n256");
   CHECK(name(1, 2048, 4096, 4096, true, false) == "f16w_mfma_m128n128");

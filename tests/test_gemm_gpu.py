@@ -434,7 +434,7 @@ def test_f16_split_k_kernels(ta, ctx, oracle, monkeypatch, name, splits):
 def test_f16_split_k_prefill_shapes(ta, ctx, oracle, shape):
     """The split-K f16w kernels at config-5 shapes with their default split
     counts, against the oracle (the down projection 512x2048x5632 routes to
-    f16w_sk_m128n64 by default)."""
+    f16w_sk_m128n128 by default)."""
     m, n, k = shape
     ha, hb = oracle.fill_det(m * k, 7210), oracle.fill_normal(k * n, 7211, 0.02)
     refs = f16_mfma_refs(ha, hb, 1, m, n, k, oracle)
