@@ -216,12 +216,27 @@ int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a,
                        const ta_tensor *b, const ta_tensor *c, float alpha,
                        uint32_t splits, ta_run_stats *stats);
 
+/* Executor::run_op_split_k2: ta_matmul_split_k2 for a whole op.  Stage 1
+ * writes alpha-scaled partial planes, the reduce sums them in a fixed
+ * order and then applies the op's epilogue once (accumulate, bias,
+ * activation, binary with D, in the order of ref tensor_ash.h:47-59), so
+ * the result is bit-identical from run to run.  No reference symbol: the
+ * reference splits plain calls only (src/executor/mod.rs:179-210,
+ * shaders/matmul_f32_splitk2_reduce.comp:44-75); ta_run_ops takes this
+ * route by itself for deep-K f32 ops whose tiles leave most CUs idle.
+ * splits == 0 picks the default; splits == 1 is the data-parallel route. */
+int ta_run_op_split_k2(const ta_executor *exec, const ta_matmul_op *op,
+                       uint32_t splits, ta_run_stats *stats);
+
 /* No counterpart in the reference.  For callers that cannot allocate
- * device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc): ta_matmul_split_k2 with the same
- * kernels and bit-identical results, but its partial planes live in a
- * fixed per-device array of TA_NOALLOC_SCRATCH_BYTES that the library
- * holds until the process ends, so the call allocates nothing.  Fails
+ * device memory (tight serving loops, harnesses that forbid hipMalloc):
+ * ta_matmul_split_k2 with the same kernels and bit-identical results at
+ * every split count (splits == 1 included: the same data-parallel route),
+ * but its partial planes live in a fixed per-device array of
+ * TA_NOALLOC_SCRATCH_BYTES that the library holds until the process
+ * ends, so the call allocates nothing (ta_allocation_count is unchanged
+ * across it).  It runs on the executor's own stream and waits for it, so
+ * it is not a call to make inside a caller's stream capture.  Fails
  * (-1, ta_last_error) when the planes would exceed that size: batch * M *
  * N * splits * sub-windows * 4 bytes, where the library adds sub-windows
  * to fill the device (64x256 and 32x128 outputs use 16 MiB and 4 MiB at
@@ -233,6 +248,12 @@ int ta_matmul_split_k2_noalloc(const ta_executor *exec, const ta_tensor *a,
                                const ta_tensor *b, const ta_tensor *c,
                                float alpha, uint32_t splits,
                                ta_run_stats *stats);
+
+/* No counterpart in the reference (a diagnostic): the number of device
+ * and pinned-host allocations the library has made in this process
+ * (tensors, cells, executor scratch).  Unchanged across a call that
+ * allocates nothing. */
+uint64_t ta_allocation_count(void);
 
 /* MatmulOp::with_packed_b (src/matmul/api.rs:260-265): B holds the packed
  * decode layout produced by ta_pack_f16w_row_tiles with

@@ -23,7 +23,9 @@ enum {
 // Bytes of the fixed device scratch that the allocation-free split-K
 // entry point keeps its partial planes in (one array per device, held
 // until the process ends).  Config 4's largest plane set is 16 MiB.
-#define TA_NOALLOC_SCRATCH_BYTES (32u << 20)
+// The public header states the same figure as TA_NOALLOC_SCRATCH_BYTES;
+// capi.cpp, which sees both, asserts that they agree.
+#define TA_FIXED_SCRATCH_BYTES (32u << 20)
 
 // Most chunks a split-K decode-attention launch uses per kv head: stage 2
 // (ta_attn_decode_combine) keeps one register slot per chunk and one LDS
@@ -87,6 +89,9 @@ typedef struct GemmArgs {
 
 // Fixed-order reduction of split-K partial planes:
 // C[b][e] = sum_{s=0}^{S-1} scratch[(b * S + s) * mn + e].
+// The sum then takes the op's fused epilogue without alpha, which stage 1
+// already applied to every partial: v = sum (+C_old) -> +bias -> act ->
+// (+beta*D | *D); flags / act / binary / beta take GemmArgs' meaning.
 typedef struct SplitReduceArgs {
   const float *scratch;
   float *c;
@@ -94,6 +99,14 @@ typedef struct SplitReduceArgs {
   uint64_t mn;
   uint32_t num_splits;
   uint32_t groups; // plane groups per element: power of two <= min(num_splits, 256)
+  const float *bias;
+  const float *d;
+  uint32_t n; // columns of C (epilogue column = (e % mn) % n)
+  uint32_t flags;
+  uint32_t act;
+  uint32_t binary;
+  uint32_t bias_batch_stride;
+  float beta;
 } SplitReduceArgs;
 
 // Element-wise f32 -> f16 (RNE) conversion: dst[i] = src[i], i < n.

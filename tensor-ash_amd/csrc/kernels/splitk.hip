@@ -1,5 +1,7 @@
 // Stage 2 of the deterministic two-stage split-K (stage 1 is the GEMM
-// kernel with num_splits > 1, see gemm_f32.hip).
+// kernel with num_splits > 1, see gemm_f32.hip), which also applies the
+// op's fused epilogue once, to the finished sum
+// (shaders/matmul_epilogue_common.glsl:30-82 on the reduced value).
 //
 // Contract (the reference's reduce, shaders/matmul_f32_splitk2_reduce.comp:
 // 44-75, sums the S planes of batch b in order; here there are P planes,
@@ -38,10 +40,30 @@ TA_DEVICE f32x4 load_quad(const SplitReduceArgs &p, bool vec, uint64_t base, uin
   }
   return v;
 }
+// The fused epilogue on the plane sum v of element i (batch-major index
+// into C): the order of ta_epilogue with alpha already in v
+// (shaders/matmul_epilogue_common.glsl:14-21).  A C read for accumulate
+// happens before this thread's store of the same element.
+TA_DEVICE float reduce_epilogue(const SplitReduceArgs &p, float v, uint64_t i) {
+  if (p.flags & TA_FLAG_ACCUMULATE)
+    v += p.c[i];
+  if (p.flags & TA_FLAG_BIAS) {
+    const uint32_t b = (uint32_t)(i / p.mn);
+    const uint32_t col = (uint32_t)(i % p.mn % p.n);
+    v += p.bias[(uint64_t)b * p.bias_batch_stride + col];
+  }
+  v = ta_activate(v, p.act);
+  if (p.binary == TA_BIN_ADD_SCALED)
+    v = fmaf(p.beta, p.d[i], v);
+  else if (p.binary == TA_BIN_MUL)
+    v *= p.d[i];
+  return v;
+}
 } // namespace
 
 extern "C" __global__ __launch_bounds__(kThreads) void ta_splitk_reduce(SplitReduceArgs p) {
   __shared__ f32x4 part[kThreads];
+  const bool epi = p.flags != 0u || p.act != TA_ACT_NONE || p.binary != TA_BIN_NONE;
   const uint64_t quads = (p.total + 3) / 4;
   const bool vec = (p.mn & 3u) == 0u;
   const uint32_t P = p.num_splits;
@@ -80,8 +102,12 @@ extern "C" __global__ __launch_bounds__(kThreads) void ta_splitk_reduce(SplitRed
     }
     __syncthreads();
     if (g == 0 && q < quads) {
-      const f32x4 r = part[ql];
+      f32x4 r = part[ql];
       const uint64_t base = q * 4;
+      if (epi)
+        for (uint32_t c = 0; c < 4; ++c)
+          if (base + c < p.total)
+            r[c] = reduce_epilogue(p, r[c], base + c);
       if (vec) {
         *reinterpret_cast<f32x4 *>(p.c + base) = r;
       } else {

@@ -9,6 +9,9 @@
 #include "../../../include/tensor_ash.h"
 #include "internal.hpp"
 
+static_assert(TA_NOALLOC_SCRATCH_BYTES == TA_FIXED_SCRATCH_BYTES,
+              "include/tensor_ash.h and kernel_args.h disagree on the fixed scratch size");
+
 using namespace tensor_ash;
 
 struct ta_context {
@@ -427,6 +430,19 @@ int ta_matmul_split_k2(const ta_executor *exec, const ta_tensor *a, const ta_ten
     ta_matmul_call raw{a, b, c, alpha, 0};
     write_stats(stats,
                 e.exec->run_matmuls_split_k2(checked_call(e, raw, "ta_matmul_split_k2"), splits));
+  });
+}
+
+uint64_t ta_allocation_count(void) { return allocation_count(); }
+
+int ta_run_op_split_k2(const ta_executor *exec, const ta_matmul_op *op, uint32_t splits,
+                       ta_run_stats *stats) {
+  return ffi_status([&] {
+    const ta_executor &e = checked_ref(exec, "ta_run_op_split_k2: exec is null");
+    if (!op)
+      fail("ta_run_op_split_k2: op is null");
+    write_stats(stats,
+                e.exec->run_op_split_k2(checked_op(e, *op, "ta_run_op_split_k2"), splits));
   });
 }
 

@@ -1,5 +1,6 @@
 // HIP device context, code-object loading and tensor storage.
 // Replaces src/context/ and src/buffer.rs / src/tensor.rs allocation.
+#include <atomic>
 #include <dirent.h>
 #include <dlfcn.h>
 
@@ -21,6 +22,22 @@ void hip_check(hipError_t err, const char *what) {
   if (err != hipSuccess)
     fail(std::string(what) + " failed: " + hipGetErrorString(err));
 }
+
+namespace {
+std::atomic<uint64_t> g_allocations{0};
+} // namespace
+
+hipError_t device_malloc(void **ptr, size_t bytes) {
+  g_allocations.fetch_add(1, std::memory_order_relaxed);
+  return hipMalloc(ptr, bytes);
+}
+
+hipError_t host_malloc(void **ptr, size_t bytes, unsigned int flags) {
+  g_allocations.fetch_add(1, std::memory_order_relaxed);
+  return hipHostMalloc(ptr, bytes, flags);
+}
+
+uint64_t allocation_count() { return g_allocations.load(std::memory_order_relaxed); }
 
 namespace {
 
@@ -201,7 +218,7 @@ Tensor Tensor::uninit_device(const std::shared_ptr<Context> &ctx,
   buf->ctx = ctx;
   buf->bytes = (n * 4 + 15) / 16 * 16;
   ctx->make_current();
-  hip_check(hipMalloc(&buf->ptr, buf->bytes), "hipMalloc");
+  hip_check(device_malloc(&buf->ptr, buf->bytes), "hipMalloc");
   return Tensor(shape, DType::F32, buf);
 }
 
@@ -214,7 +231,7 @@ Tensor Tensor::uninit_device_f16(const std::shared_ptr<Context> &ctx,
   buf->ctx = ctx;
   buf->bytes = (n * 2 + 15) / 16 * 16;
   ctx->make_current();
-  hip_check(hipMalloc(&buf->ptr, buf->bytes), "hipMalloc");
+  hip_check(device_malloc(&buf->ptr, buf->bytes), "hipMalloc");
   return Tensor(shape, DType::F16, buf);
 }
 
@@ -252,7 +269,7 @@ std::unique_ptr<U32Cell> U32Cell::create(const std::shared_ptr<Context> &ctx, ui
   ctx->make_current();
   std::unique_ptr<U32Cell> c(new U32Cell());
   void *host = nullptr;
-  hip_check(hipHostMalloc(&host, (size_t)cap * 4, hipHostMallocMapped), "hipHostMalloc (u32 cell)");
+  hip_check(host_malloc(&host, (size_t)cap * 4, hipHostMallocMapped), "hipHostMalloc (u32 cell)");
   void *dev = nullptr;
   const hipError_t e = hipHostGetDevicePointer(&dev, host, 0);
   if (e != hipSuccess) {

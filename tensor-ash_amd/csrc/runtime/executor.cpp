@@ -73,7 +73,7 @@ struct Scratch {
   void ensure_barrier(bool want) {
     if (!want || barrier)
       return;
-    hip_check(hipMalloc(reinterpret_cast<void **>(&barrier), 2 * TA_GEMV_COUNTER_STRIDE * 4),
+    hip_check(device_malloc(reinterpret_cast<void **>(&barrier), 2 * TA_GEMV_COUNTER_STRIDE * 4),
               "hipMalloc (GEMV chain barrier)");
     hip_check(hipMemset(barrier, 0, 2 * TA_GEMV_COUNTER_STRIDE * 4), "hipMemset (GEMV chain barrier)");
   }
@@ -83,7 +83,7 @@ struct Scratch {
     if (shadow)
       hip_check(hipFree(shadow), "hipFree");
     shadow = nullptr;
-    hip_check(hipMalloc(&shadow, bytes), "hipMalloc (f16 output copy)");
+    hip_check(device_malloc(&shadow, bytes), "hipMalloc (f16 output copy)");
     shadow_bytes = bytes;
   }
   void ensure_mlp(uint64_t bytes) {
@@ -92,7 +92,7 @@ struct Scratch {
     if (mlp)
       hip_check(hipFree(mlp), "hipFree");
     mlp = nullptr;
-    hip_check(hipMalloc(&mlp, bytes), "hipMalloc (decode-MLP scratch)");
+    hip_check(device_malloc(&mlp, bytes), "hipMalloc (decode-MLP scratch)");
     mlp_bytes = bytes;
     reset_mlp();
   }
@@ -109,21 +109,21 @@ struct Scratch {
       if (splitk)
         hip_check(hipFree(splitk), "hipFree");
       splitk = nullptr;
-      hip_check(hipMalloc(&splitk, sk_bytes), "hipMalloc (split-K scratch)");
+      hip_check(device_malloc(&splitk, sk_bytes), "hipMalloc (split-K scratch)");
       splitk_bytes = sk_bytes;
     }
     if (part_bytes > partial_bytes) {
       if (partial)
         hip_check(hipFree(partial), "hipFree");
       partial = nullptr;
-      hip_check(hipMalloc(&partial, part_bytes), "hipMalloc (GEMV partials)");
+      hip_check(device_malloc(&partial, part_bytes), "hipMalloc (GEMV partials)");
       partial_bytes = part_bytes;
     }
     if (n_counters > counters_len) {
       if (counters)
         hip_check(hipFree(counters), "hipFree");
       counters = nullptr;
-      hip_check(hipMalloc(reinterpret_cast<void **>(&counters), n_counters * 4),
+      hip_check(device_malloc(reinterpret_cast<void **>(&counters), n_counters * 4),
                 "hipMalloc (GEMV counters)");
       hip_check(hipMemset(counters, 0, n_counters * 4), "hipMemset (GEMV counters)");
       counters_len = n_counters;
@@ -155,7 +155,7 @@ struct Slot {
 // Mapped pinned word the decode-MLP kernel reports its wait status into.
 uint32_t *alloc_host_status() {
   void *p = nullptr;
-  hip_check(hipHostMalloc(&p, 64, hipHostMallocMapped), "hipHostMalloc");
+  hip_check(host_malloc(&p, 64, hipHostMallocMapped), "hipHostMalloc");
   *static_cast<volatile uint32_t *>(p) = 0;
   return static_cast<uint32_t *>(p);
 }
@@ -306,7 +306,7 @@ struct ExecutorImpl {
         // Stage 1 runs on the split-K tile of run_matmuls_split_k2 (and of
         // dispatch_info_for), so an op gives the same bits whether it is
         // submitted alone or together with others.
-        plan.kernel = registry_index(splitk_stage1_spec(m, n).name);
+        plan.kernel = registry_index(splitk_stage1_spec(m, n, k).name);
       }
     }
     return plan;
@@ -587,6 +587,19 @@ struct ExecutorImpl {
       r.num_splits = a.num_splits;
       const uint64_t quads = (r.total + 3) / 4;
       r.groups = splitk_reduce_groups(ctx->cu_count(), quads, r.num_splits);
+      // The op's epilogue runs once, on the finished plane sum.
+      r.n = d.n;
+      r.flags = op.call.accumulate ? TA_FLAG_ACCUMULATE : 0;
+      if (op.epilogue.bias) {
+        r.flags |= TA_FLAG_BIAS;
+        r.bias = static_cast<const float *>(op.epilogue.bias->device_ptr());
+        r.bias_batch_stride = op.epilogue.bias->shape().size() == 2 ? d.n : 0;
+      }
+      r.act = (uint32_t)op.epilogue.activation;
+      r.binary = (uint32_t)op.epilogue.binary.kind;
+      if (const Tensor *dt = op.epilogue.d_tensor())
+        r.d = static_cast<const float *>(dt->device_ptr());
+      r.beta = op.epilogue.binary.beta;
       const uint64_t per_wg = kReduceThreads / r.groups;
       const uint64_t wgs = std::min<uint64_t>((quads + per_wg - 1) / per_wg, 8ull * ctx->cu_count());
       launch("ta_splitk_reduce", (uint32_t)std::max<uint64_t>(wgs, 1), 1, 1, kReduceThreads, &r,
@@ -1578,7 +1591,7 @@ struct ExecutorImpl {
     // Reduction pass: probe split-K against the DP winner on deep-K,
     // few-tile shapes (executor/tuning.rs:203-250).
     std::optional<uint32_t> best_splits;
-    const KernelSpec &s1 = splitk_stage1_spec(d.m, d.n);
+    const KernelSpec &s1 = splitk_stage1_spec(d.m, d.n, d.k);
     const uint64_t tiles = (uint64_t)d.batch * div_ceil(d.m, s1.tile_m) * div_ceil(d.n, s1.tile_n);
     if (!d.b_f16 && !d.packed_b && d.k >= 1024 && tiles < ctx->cu_count()) {
       std::optional<uint64_t> best;
@@ -1637,20 +1650,21 @@ struct ExecutorImpl {
       }
     }
 
-    // Split-K eligibility: plain ops (src/executor/mod.rs:125-139).  The
-    // reference also excludes multi-op run_ops submissions, whose ops share
-    // one scratch with no barriers between them; here each stream lane has
-    // its own scratch and runs in stream order, so every plain op may take
-    // the split-K route.
+    // Split-K eligibility.  The reference offers it to plain ops only
+    // (src/executor/mod.rs:125-139) and also excludes multi-op run_ops
+    // submissions, whose ops share one scratch with no barriers between
+    // them.  Here each stream lane has its own scratch and runs in stream
+    // order, and the reduce applies the fused epilogue (accumulate, bias,
+    // activation, binary with D) once to the finished plane sum, so every
+    // f32 op may take the split-K route: a deep-K skinny GEMM with an
+    // epilogue would otherwise run a handful of workgroups on 256 CUs.
     std::vector<OpPlan> plans;
-    for (size_t i = 0; i < ops.size(); ++i) {
-      const bool eligible = !ops[i].call.accumulate && ops[i].epilogue.is_none();
-      plans.push_back(plan_op(ops[i], res[i], eligible));
-    }
+    for (size_t i = 0; i < ops.size(); ++i)
+      plans.push_back(plan_op(ops[i], res[i], true));
     if (graph)
       mark_fusions(ops, res, plans);
     if (!graph && plans.size() == 1 && plans[0].splitk2)
-      return run_split_k2(ops[0].call, *plans[0].splitk2);
+      return run_split_k2(ops[0], *plans[0].splitk2, "run_ops", true);
     const uint32_t lanes = graph ? 1u : run_ops_lanes(res, plans);
     if (lanes == 1)
       mark_groups(ops, res, plans);
@@ -1703,21 +1717,25 @@ struct ExecutorImpl {
   }
 
   // ---- split-K (src/executor/reduction.rs:21-70) ----
-  // Validates the call and resolves the split count (0 = default).
-  uint32_t split_k2_splits(const MatmulCall &call, uint32_t num_k_splits,
-                           ResolvedMatmul &d) const {
-    validate_call(call);
-    if (call.accumulate)
-      fail("run_matmuls_split_k2: accumulate=true is not supported");
-    d = ResolvedMatmul::from_call(call);
+  // Validates the op and resolves the split count (0 = default).  `fn`
+  // names the entry point in error texts; the call form keeps the
+  // reference's refusal of accumulate, the op form applies it in the
+  // reduce with the rest of the epilogue.
+  uint32_t split_k2_splits(const MatmulOp &op, uint32_t num_k_splits, ResolvedMatmul &d,
+                           const std::string &fn, bool allow_accumulate) const {
+    validate_op(op);
+    if (op.call.accumulate && !allow_accumulate)
+      fail(fn + ": accumulate=true is not supported");
+    if (op.has_decode_fusion())
+      fail(fn + ": decode fusions (normed A, RoPE/scatter store) need a decode GEMV route");
+    d = ResolvedMatmul::from_op(op);
     if (num_k_splits > 0xFFFF)
-      fail("run_matmuls_split_k2: num_k_splits=" + std::to_string(num_k_splits) +
-           " out of range [1, 65535]");
+      fail(fn + ": num_k_splits=" + std::to_string(num_k_splits) + " out of range [1, 65535]");
     if (num_k_splits > d.k)
-      fail("run_matmuls_split_k2: num_k_splits=" + std::to_string(num_k_splits) +
-           " exceeds K=" + std::to_string(d.k));
+      fail(fn + ": num_k_splits=" + std::to_string(num_k_splits) + " exceeds K=" +
+           std::to_string(d.k));
     if (d.a_f16 || d.b_f16)
-      fail("run_matmuls_split_k2: split-K stage 1 reads f32 A and B only");
+      fail(fn + ": split-K stage 1 reads f32 A and B only");
     const uint32_t splits =
         num_k_splits == 0 ? default_num_k_splits(ctx->cu_count(), d.batch, d.m, d.n, d.k)
                           : num_k_splits;
@@ -1730,50 +1748,60 @@ struct ExecutorImpl {
     return splits;
   }
 
-  RunStats run_split_k2(const MatmulCall &call, uint32_t num_k_splits) {
+  // The route of an explicit split count: the split-K stage-1 tile plus
+  // the reduce for splits > 1, else the data-parallel route (the same
+  // plan run_ops gives an op that may not split), which needs no scratch
+  // for f32 operands.  The allocating and the allocation-free entry
+  // points share it, so they launch the same kernels.
+  OpPlan split_k2_plan(const MatmulOp &op, const ResolvedMatmul &d, uint32_t splits) const {
+    if (splits <= 1)
+      return plan_op(op, d, false);
+    OpPlan p;
+    p.kernel = registry_index(splitk_stage1_spec(d.m, d.n, d.k).name);
+    p.splitk2 = splits;
+    return p;
+  }
+
+  RunStats run_split_k2(const MatmulOp &op, uint32_t num_k_splits, const std::string &fn,
+                        bool allow_accumulate) {
     ctx->make_current();
     ResolvedMatmul d;
-    const uint32_t splits = split_k2_splits(call, num_k_splits, d);
-    if (splits <= 1)
-      return run_ops_impl({MatmulOp(call)}, false);
-    OpPlan p;
-    p.kernel = registry_index(splitk_stage1_spec(d.m, d.n).name);
-    p.splitk2 = splits;
+    const uint32_t splits = split_k2_splits(op, num_k_splits, d, fn, allow_accumulate);
+    const OpPlan p = split_k2_plan(op, d, splits);
     Lease lease(this);
-    const uint64_t ns = submit_and_wait(lease.s, {MatmulOp(call)}, {d}, {p});
+    const uint64_t ns = submit_and_wait(lease.s, {op}, {d}, {p});
     return RunStats{ns, 1, d.total_flops};
   }
 
-  // The same two launches with the partial planes in the device's fixed
+  // The same launches with the partial planes in the device's fixed
   // scratch array instead of slot memory: nothing is allocated, on the
-  // device or pinned.  A single split runs the stage-1 kernel straight
-  // into C (no scratch).  Calls on one device are serialised here, from
-  // the first launch until the stream has drained, because they share
-  // the array; the planes need no clearing (every element is stored
-  // before the reduce reads it).
+  // device or pinned.  Calls on one device are serialised here, from the
+  // first launch until the stream has drained, because they share the
+  // array; the planes need no clearing (every element is stored before
+  // the reduce reads it).
   RunStats run_split_k2_noalloc(const MatmulCall &call, uint32_t num_k_splits) {
     ctx->make_current();
+    const std::string fn = "run_matmuls_split_k2_noalloc";
+    const MatmulOp op(call);
     ResolvedMatmul d;
-    const uint32_t splits = split_k2_splits(call, num_k_splits, d);
-    OpPlan p;
-    p.kernel = registry_index(splitk_stage1_spec(d.m, d.n).name);
-    if (splits > 1)
-      p.splitk2 = splits;
-    const uint64_t need = scratch_need(d, p).splitk;
-    if (need > TA_NOALLOC_SCRATCH_BYTES)
-      fail("run_matmuls_split_k2_noalloc: partial planes need " + std::to_string(need) +
-           " bytes (B=" + std::to_string(d.batch) + " " + std::to_string(d.m) + "x" +
-           std::to_string(d.n) + ", " + std::to_string(splits) +
-           " splits) > the fixed scratch of " + std::to_string(TA_NOALLOC_SCRATCH_BYTES) +
-           " bytes");
+    const uint32_t splits = split_k2_splits(op, num_k_splits, d, fn, false);
+    const OpPlan p = split_k2_plan(op, d, splits);
+    const ScratchNeed need = scratch_need(d, p);
+    if (need.partial || need.counters)
+      fail("internal: " + fn + " route needs slot scratch");
+    if (need.splitk > TA_FIXED_SCRATCH_BYTES)
+      fail(fn + ": partial planes need " + std::to_string(need.splitk) + " bytes (B=" +
+           std::to_string(d.batch) + " " + std::to_string(d.m) + "x" + std::to_string(d.n) +
+           ", " + std::to_string(splits) + " splits) > the fixed scratch of " +
+           std::to_string(TA_FIXED_SCRATCH_BYTES) + " bytes");
     void *base = nullptr;
     hip_check(fixed_scratch_address(ctx->device(), &base), "hipGetSymbolAddress (fixed scratch)");
     Scratch fixed;
     fixed.splitk = base;
-    fixed.splitk_bytes = TA_NOALLOC_SCRATCH_BYTES;
+    fixed.splitk_bytes = TA_FIXED_SCRATCH_BYTES;
     std::lock_guard<std::mutex> serial(fixed_scratch_mutex(ctx->device()));
     Lease lease(this);
-    const uint64_t ns = submit_on(lease.s, {MatmulOp(call)}, {d}, {p}, fixed);
+    const uint64_t ns = submit_on(lease.s, {op}, {d}, {p}, fixed);
     return RunStats{ns, 1, d.total_flops};
   }
 
@@ -1958,7 +1986,11 @@ RunStats Executor::run_gemv_chain(const std::vector<MatmulOp> &jobs) const {
 }
 
 RunStats Executor::run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const {
-  return impl_->run_split_k2(call, num_k_splits);
+  return impl_->run_split_k2(MatmulOp(call), num_k_splits, "run_matmuls_split_k2", false);
+}
+
+RunStats Executor::run_op_split_k2(const MatmulOp &op, uint32_t num_k_splits) const {
+  return impl_->run_split_k2(op, num_k_splits, "run_op_split_k2", true);
 }
 
 RunStats Executor::run_matmuls_split_k2_noalloc(const MatmulCall &call,
@@ -2757,7 +2789,7 @@ DispatchInfo Executor::dispatch_info(uint32_t batch, uint32_t m, uint32_t n, uin
 DispatchInfo Executor::dispatch_info_for(uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
                                          bool b_f16) const {
   OpPlan p = impl_->plan_shape(batch, m, n, k, b_f16, true);
-  const KernelSpec &s = p.splitk2 ? splitk_stage1_spec(m, n) : KERNEL_SPECS[p.kernel];
+  const KernelSpec &s = p.splitk2 ? splitk_stage1_spec(m, n, k) : KERNEL_SPECS[p.kernel];
   DispatchInfo info;
   info.kernel = s.name;
   info.tile = {s.tile_m, s.tile_n, s.tile_k};

@@ -15,7 +15,8 @@
 
 #include "../kernels/kernel_args.h"
 
-static __device__ __align__(256) unsigned char scratch[TA_NOALLOC_SCRATCH_BYTES];
+static __device__ __align__(256) unsigned char scratch[TA_FIXED_SCRATCH_BYTES];
+static_assert(sizeof(scratch) == TA_FIXED_SCRATCH_BYTES, "fixed scratch size");
 
 namespace tensor_ash {
 

@@ -18,6 +18,13 @@ namespace tensor_ash {
 std::string fmt_shape(const std::vector<uint32_t> &shape); // "[a, b, c]"
 void hip_check(hipError_t err, const char *what);
 
+// Every device and pinned-host allocation the library makes goes through
+// these two, which count the calls (allocation_count) so a caller can
+// check that an entry point allocated nothing.
+hipError_t device_malloc(void **ptr, size_t bytes);
+hipError_t host_malloc(void **ptr, size_t bytes, unsigned int flags);
+uint64_t allocation_count();
+
 struct DeviceBuffer {
   std::shared_ptr<Context> ctx;
   void *ptr = nullptr;
@@ -71,7 +78,7 @@ size_t registry_index(const char *name);
 // ---- split-K (src/executor/splitk2.rs) ----
 constexpr uint32_t kReduceThreads = 256;
 constexpr uint64_t kAutoScratchCapBytes = 256ull << 20;
-const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n);
+const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n, uint32_t k);
 uint32_t gemm_threads(const KernelSpec &s);
 uint32_t h16sk_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k,
                       uint32_t tile_m, uint32_t tile_n);

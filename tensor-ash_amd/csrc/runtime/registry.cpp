@@ -263,10 +263,17 @@ std::vector<size_t> tune_candidate_indices(const ResolvedMatmul &dims) {
 // XCD's L2).  Measured, stage 1 + reduce: 64 x 256 x 65536 32.8 us against
 // 36.8 us with 64 x 256 tiles; 32 x 128 x 131072 30.4 against 31.8 us
 // with 32 x 128 tiles.
-const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n) {
-  const char *name = m >= 128 && n >= 128 ? "f32_m128n128"
-                     : m <= 32            ? "f32_m32n64"
-                                          : "f32_m64n64";
+// Outputs of at least 128 x 128 whose sides are whole 64-column tiles and
+// whose K splits into windows of whole eight-stage loops at up to 16
+// planes (K % 2048 == 0) take the pipelined 64 x 64 tile as well: a
+// 256 x 256 x 16384 op then runs 16 tiles x 16 windows of 1024 on the
+// FP32-MFMA pipeline (38.7-39.8 us on the 128 x 128 register-staged tile
+// at 64 planes).
+const KernelSpec &splitk_stage1_spec(uint32_t m, uint32_t n, uint32_t k) {
+  const bool pipelined64 = m % 64 == 0 && n % 64 == 0 && k % 2048 == 0;
+  const char *name = m >= 128 && n >= 128 && !pipelined64 ? "f32_m128n128"
+                     : m <= 32                            ? "f32_m32n64"
+                                                          : "f32_m64n64";
   return KERNEL_SPECS[registry_index(name)];
 }
 
@@ -314,7 +321,7 @@ uint32_t gemm_threads(const KernelSpec &s) {
 uint32_t splitk_sub_splits(uint32_t cus, const ResolvedMatmul &d, uint32_t splits) {
   if (splits < 2 || d.batch == 0)
     return 1;
-  const KernelSpec &s = splitk_stage1_spec(d.m, d.n);
+  const KernelSpec &s = splitk_stage1_spec(d.m, d.n, d.k);
   const uint64_t tiles = (uint64_t)d.batch * div_ceil(d.m, s.tile_m) * div_ceil(d.n, s.tile_n);
   const uint64_t plane = (uint64_t)d.batch * d.m * d.n;
   auto capped = [&](uint64_t t) {
@@ -354,7 +361,7 @@ std::optional<uint32_t> heuristic_splits(uint32_t cus, uint32_t batch, uint32_t 
                                          uint32_t k) {
   if (batch == 0 || m <= 1 || n <= 1 || k < 1024)
     return std::nullopt;
-  const KernelSpec &s = splitk_stage1_spec(m, n);
+  const KernelSpec &s = splitk_stage1_spec(m, n, k);
   const uint64_t tiles = (uint64_t)batch * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
   if (tiles * 2 >= cus)
     return std::nullopt;
@@ -379,7 +386,7 @@ std::optional<uint32_t> heuristic_splits(uint32_t cus, uint32_t batch, uint32_t 
 uint32_t default_num_k_splits(uint32_t cus, uint32_t batch, uint32_t m, uint32_t n, uint32_t k) {
   if (auto h = heuristic_splits(cus, batch, m, n, k))
     return *h;
-  const KernelSpec &s = splitk_stage1_spec(m, n);
+  const KernelSpec &s = splitk_stage1_spec(m, n, k);
   const uint64_t tiles =
       (uint64_t)std::max(batch, 1u) * div_ceil(m, s.tile_m) * div_ceil(n, s.tile_n);
   if (tiles == 0)

@@ -587,6 +587,11 @@ public:
   // earlier jobs' writes) on the decode GEMV launches.
   RunStats run_gemv_chain(const std::vector<MatmulOp> &jobs) const;
   RunStats run_matmuls_split_k2(const MatmulCall &call, uint32_t num_k_splits) const;
+  // run_matmuls_split_k2 for a whole op: the reduce applies the op's
+  // fused epilogue (accumulate, bias, activation, binary with D) once to
+  // the fixed-order plane sum.  No reference counterpart: the reference
+  // splits plain calls only (src/executor/mod.rs:179-210).
+  RunStats run_op_split_k2(const MatmulOp &op, uint32_t num_k_splits) const;
   // run_matmuls_split_k2 without allocating: partial planes live in a
   // fixed per-device array of TA_NOALLOC_SCRATCH_BYTES (no reference
   // counterpart; for callers that cannot allocate device memory).

@@ -150,6 +150,8 @@ _sig("ta_run_op_graph", C.c_int, P, C.POINTER(_Op), sz, C.POINTER(RunStats))
 _sig("ta_run_ops_v2", C.c_int, P, C.POINTER(_OpV2), sz, C.POINTER(RunStats))
 _sig("ta_run_op_graph_v2", C.c_int, P, C.POINTER(_OpV2), sz, C.POINTER(RunStats))
 _sig("ta_matmul_split_k2", C.c_int, P, P, P, P, f32, u32, C.POINTER(RunStats))
+_sig("ta_allocation_count", C.c_uint64)
+_sig("ta_run_op_split_k2", C.c_int, P, P, u32, C.POINTER(RunStats))
 _sig("ta_matmul_split_k2_noalloc", C.c_int, P, P, P, P, f32, u32, C.POINTER(RunStats))
 _sig("ta_prepared_create", P, P, C.POINTER(_Op), sz, u32)
 _sig("ta_prepared_create_v2", P, P, C.POINTER(_OpV2), sz, u32)
@@ -218,6 +220,12 @@ def kernel_names() -> list[str]:
 
 def f16w_row_tile_n(k: int, n: int) -> int:
     return int(_lib.ta_f16w_row_tile_n(k, n))
+
+
+def allocation_count() -> int:
+    """Device and pinned-host allocations the library has made in this
+    process (include/tensor_ash.h ta_allocation_count)."""
+    return int(_lib.ta_allocation_count())
 
 
 def pack_f16w_row_tiles(src: np.ndarray, k: int, n: int, tile_n: int) -> np.ndarray:
@@ -757,6 +765,17 @@ class Executor:
     def run_matmuls_split_k2(self, a: Tensor, b: Tensor, c: Tensor, splits: int, alpha: float = 1.0) -> RunStats:
         st = RunStats()
         _check(_lib.ta_matmul_split_k2(self._h, a.handle, b.handle, c.handle, alpha, splits, C.byref(st)))
+        return st
+
+    def run_op_split_k2(self, op: MatmulOp, splits: int = 0) -> RunStats:
+        """run_matmuls_split_k2 for a whole op: the reduce applies the op's
+        fused epilogue once to the fixed-order plane sum (include/tensor_ash.h
+        ta_run_op_split_k2)."""
+        if op.packed_b or op.normed_a is not None or op.store is not None:
+            raise TensorAshError("run_op_split_k2: packed B and decode fusions need a decode GEMV route")
+        st = RunStats()
+        raw = op._raw()
+        _check(_lib.ta_run_op_split_k2(self._h, C.byref(raw), splits, C.byref(st)))
         return st
 
     def run_matmuls_split_k2_noalloc(self, a: Tensor, b: Tensor, c: Tensor, splits: int,

@@ -185,6 +185,9 @@ static void test_splitk() {
   CHECK(heuristic_splits(cus, 1, 64, 256, 65536) == 64u);
   CHECK(heuristic_splits(cus, 1, 64, 256, 65536 + 64) == 128u); // unaligned: ~2 WGs per CU
   CHECK(heuristic_splits(cus, 1, 32, 128, 131072) == 128u);
+  CHECK(heuristic_splits(cus, 1, 256, 256, 16384) == 16u);  // 64x64 pipelined stage 1: 16 tiles
+  CHECK(std::string(splitk_stage1_spec(256, 256, 16384).name) == "f32_m64n64");
+  CHECK(std::string(splitk_stage1_spec(256, 256, 16000).name) == "f32_m128n128");
   CHECK(heuristic_splits(cus, 1, 64, 64, 1024) == 4u);      // capped by K/256
   CHECK(!heuristic_splits(cus, 1, 64, 64, 512));            // K < 1024
   CHECK(!heuristic_splits(cus, 1, 4096, 4096, 4096));       // grid already full

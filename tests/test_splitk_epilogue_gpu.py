@@ -1,0 +1,150 @@
+"""GPU parity of the deterministic split-K route for ops with a fused
+epilogue (bias, activation, binary with D, accumulate).
+
+Stage 1 writes alpha-scaled partial planes; the reduce sums them in a fixed
+order and then applies the epilogue once, in the order of
+shaders/matmul_epilogue_common.glsl:14-21.  The reference splits plain
+calls only (src/executor/mod.rs:179-210); the reduce's plane order follows
+shaders/matmul_f32_splitk2_reduce.comp:44-75.
+
+Bar: the f32 tolerances of test_gemm_gpu against the oracle's cpu_bmm plus
+the f64 epilogue on the same inputs, and bit-identical output over 10 runs
+at S = 8 / 16 / 32.
+"""
+
+import functools
+
+import numpy as np
+import pytest
+
+from test_gemm_gpu import check_f32
+
+pytestmark = pytest.mark.gpu
+
+# (name, bias kind, activation, binary, beta, accumulate)
+EPILOGUES = {
+    "bias_gelu": ("n", 3, 0, 0.0, False),
+    "silu_mul_d": (None, 2, 2, 0.0, False),
+    "bias_bn_add_scaled_d": ("bn", 0, 1, 0.75, False),
+    "bias_relu_accumulate": ("n", 1, 0, 0.0, True),
+}
+
+
+@functools.lru_cache(maxsize=None)
+def _inputs(oracle, batch, m, n, k, seed):
+    ha = oracle.fill_det(batch * m * k, seed)
+    hb = oracle.fill_det(k * n, seed + 1)
+    return ha, hb
+
+
+@functools.lru_cache(maxsize=None)
+def _raw_product(oracle, batch, m, n, k, seed, alpha):
+    ha, hb = _inputs(oracle, batch, m, n, k, seed)
+    return oracle.cpu_bmm(ha, hb, None, batch, m, n, k, alpha)
+
+
+def _case(ta, ex, oracle, batch, m, n, k, name, alpha=1.0, seed=81):
+    bias_kind, act, binary, beta, acc = EPILOGUES[name]
+    ha, hb = _inputs(oracle, batch, m, n, k, seed)
+    sa = [batch, m, k] if batch > 1 else [m, k]
+    sc = [batch, m, n] if batch > 1 else [m, n]
+    a, b, c = ex.tensor_from(ha, shape=sa), ex.tensor_from(hb, shape=[k, n]), ex.tensor(sc)
+    hbias = bias = hd = d = hc0 = None
+    stride = 0
+    if bias_kind == "n":
+        hbias = oracle.fill_det(n, seed + 2)
+        bias = ex.tensor_from(hbias, shape=[n])
+    elif bias_kind == "bn":
+        hbias = oracle.fill_det(batch * n, seed + 2)
+        bias = ex.tensor_from(hbias, shape=[batch, n])
+        stride = n
+    if binary:
+        hd = oracle.fill_det(batch * m * n, seed + 3)
+        d = ex.tensor_from(hd, shape=sc)
+    if acc:
+        hc0 = oracle.fill_det(batch * m * n, seed + 4)
+    op = ta.MatmulOp(a, b, c, alpha=alpha, accumulate=acc,
+                     epilogue=ta.Epilogue(bias=bias, activation=act, binary=binary, d=d, beta=beta))
+    # cpu_bmm, then (+C_old) and the f64 epilogue: accumulate adds C_old
+    # after alpha, before the bias (matmul_epilogue_common.glsl:14-21).
+    raw = _raw_product(oracle, batch, m, n, k, seed, alpha)
+    if acc:
+        raw = (raw.astype(np.float64) + hc0.astype(np.float64)).astype(np.float32)
+    ref = oracle.epilogue(raw, n, m * n, hbias, stride, act, binary, hd, beta)
+
+    def reset():
+        if acc:
+            ex.upload(c, hc0)
+
+    return op, c, ref, reset
+
+
+@pytest.mark.parametrize("name", list(EPILOGUES))
+@pytest.mark.parametrize("splits", [8, 16, 32])
+def test_splitk_epilogue_deterministic(ta, ex, oracle, name, splits):
+    """256x256x16384 (the deep-K skinny shape of the bench's run_ops
+    section) through explicit split counts: within tolerance of the oracle
+    and bit-identical over 10 runs."""
+    m = n = 256
+    k = 16384
+    op, c, ref, reset = _case(ta, ex, oracle, 1, m, n, k, name)
+    reset()
+    st = ex.run_op_split_k2(op, splits)
+    assert st.total_flops == 2 * m * n * k
+    first = ex.download(c).copy()
+    check_f32(first, ref, k, oracle)
+    for _ in range(9):
+        reset()
+        ex.run_op_split_k2(op, splits)
+        np.testing.assert_array_equal(ex.download(c), first)
+
+
+@pytest.mark.parametrize("name", list(EPILOGUES))
+def test_run_ops_routes_fused_deep_k_through_splitk(ta, ex, oracle, name):
+    """run_ops takes the split-K route by itself for a fused deep-K op whose
+    tiles leave most CUs idle, and gives the bits of run_op_split_k2 at the
+    planner's split count."""
+    m = n = 256
+    k = 16384
+    info = ex.dispatch_info_for(1, m, n, k)
+    assert info["split_k2"] is not None and info["split_k2"] >= 2, info
+    op, c, ref, reset = _case(ta, ex, oracle, 1, m, n, k, name)
+    reset()
+    ex.run_ops([op])
+    got = ex.download(c).copy()
+    check_f32(got, ref, k, oracle)
+    reset()
+    ex.run_op_split_k2(op, info["split_k2"])
+    np.testing.assert_array_equal(ex.download(c), got)
+
+
+@pytest.mark.parametrize("batch,m,n,k,splits,name,alpha", [
+    (3, 33, 65, 4000, 5, "bias_bn_add_scaled_d", 0.25),   # ragged: the generic stage-1 kernel
+    (2, 64, 256, 16384, 4, "bias_gelu", 0.5),             # 64x64 stage-1 tiles, batched
+    (1, 101, 103, 999, 7, "silu_mul_d", 1.0),             # odd N: quads cross rows in the reduce
+    (1, 64, 256, 65536, 16, "bias_relu_accumulate", 1.0),  # config 4a shape with an epilogue
+])
+def test_splitk_epilogue_shapes(ta, ex, oracle, batch, m, n, k, splits, name, alpha):
+    op, c, ref, reset = _case(ta, ex, oracle, batch, m, n, k, name, alpha)
+    reset()
+    ex.run_op_split_k2(op, splits)
+    check_f32(ex.download(c), ref, k, oracle)
+
+
+def test_splitk_epilogue_single_split_is_data_parallel(ta, ex, oracle):
+    """splits == 1 runs the data-parallel route with the epilogue in the
+    GEMM kernel itself."""
+    m, n, k = 128, 256, 4096
+    op, c, ref, reset = _case(ta, ex, oracle, 1, m, n, k, "bias_gelu")
+    ex.run_op_split_k2(op, 1)
+    check_f32(ex.download(c), ref, k, oracle)
+
+
+def test_run_op_split_k2_rejects_f16_and_fusions(ta, ex):
+    a, c = ex.tensor([4, 64]), ex.tensor([4, 8])
+    b16 = ex.tensor([64, 8], f16=True)
+    with pytest.raises(ta.TensorAshError, match="f32 A and B only"):
+        ex.run_op_split_k2(ta.MatmulOp(a, b16, c), 2)
+    b = ex.tensor([64, 8])
+    with pytest.raises(ta.TensorAshError, match="exceeds K=64"):
+        ex.run_op_split_k2(ta.MatmulOp(a, b, c), 65)

@@ -45,13 +45,32 @@ def test_noalloc_batched_and_default_splits(ta, ex, oracle):
     _run_pair(ta, ex, oracle, 40, 72, 2048, 4, 83, batch=2)
 
 
-def test_noalloc_single_split_within_tolerance(ta, ex, oracle):
+def test_noalloc_single_split_matches_split_k2(ta, ex, oracle):
+    """splits == 1 takes the data-parallel route in both entry points, so
+    the bits agree; also against the oracle."""
     m, n, k = 96, 160, 1024
-    ha, hb = oracle.fill_det(m * k, 91), oracle.fill_det(k * n, 92)
-    a, b, c = ex.tensor_from(ha, shape=[m, k]), ex.tensor_from(hb, shape=[k, n]), ex.tensor([m, n])
-    ex.run_matmuls_split_k2_noalloc(a, b, c, 1)
-    err, _ = oracle.max_abs_err(ex.download(c).reshape(-1), oracle.cpu_bmm(ha, hb, None, 1, m, n, k))
+    got, ha, hb = _run_pair(ta, ex, oracle, m, n, k, 1, 91)
+    err, _ = oracle.max_abs_err(got.reshape(-1), oracle.cpu_bmm(ha, hb, None, 1, m, n, k))
     assert err <= oracle.tolerance(k) * 2 + 1e-4
+
+
+def test_noalloc_first_call_allocates_nothing(ta, ctx, oracle):
+    """On a fresh executor whose slots hold no scratch yet, the call makes
+    no device or pinned allocation (the library counts every one), then
+    agrees bit for bit with the allocating entry point."""
+    fresh = ta.Executor(ctx, n_slots=1, max_calls_per_submit=8, tune=False)
+    m, n, k, s = 64, 256, 65536, 32     # config 4a: the largest plane set that fits
+    ha, hb = oracle.fill_det(m * k, 95), oracle.fill_det(k * n, 96)
+    a, b = fresh.tensor_from(ha, shape=[m, k]), fresh.tensor_from(hb, shape=[k, n])
+    c_fix, c_ref = fresh.tensor([m, n]), fresh.tensor([m, n])
+    print(f"noalloc fresh executor {m}x{n}x{k} splits={s}", flush=True)
+    before = ta.allocation_count()
+    fresh.run_matmuls_split_k2_noalloc(a, b, c_fix, s)
+    fresh.run_matmuls_split_k2_noalloc(a, b, c_fix, s)
+    assert ta.allocation_count() == before
+    fresh.run_matmuls_split_k2(a, b, c_ref, s)
+    assert ta.allocation_count() > before    # the allocating form grows the slot scratch
+    np.testing.assert_array_equal(fresh.download(c_fix), fresh.download(c_ref))
 
 
 def test_noalloc_rejects_planes_beyond_capacity(ta, ex, oracle):
