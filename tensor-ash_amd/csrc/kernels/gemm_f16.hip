@@ -497,20 +497,27 @@ struct GemmH16Pipe {
           __hip_atomic_store(mine + (uint64_t)(f * 8 + r2) * T + tid, w, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         }
-      // Publication: every thread's partial stores are complete before the
-      // barrier, and the counter increment is an agent-scope release (the
-      // barrier makes the workgroup's stores precede it); the last arriver
-      // takes an agent-scope acquire before it reads the other partials.
+      // Publication.  Partials, counter and the last arriver's reads are
+      // all agent-scope atomics (sc1: performed at the device-coherent
+      // level, never from a stale L2 line).  Every thread's partial stores
+      // have completed (vmcnt(0)) before the barrier, the counter increment
+      // is issued after it, and the reads are issued only once the
+      // increment's returned value, broadcast through the second barrier,
+      // has named this workgroup the last; the barriers' workgroup fences
+      // keep the compiler from moving the atomics across them.  An
+      // agent-scope release on the increment plus an acquire fence in the
+      // last arriver (an L2 write-back and invalidate) measured 35.3 ->
+      // 39.8 us on the 512x2048x5632 down projection, so the ordering rests
+      // on the completed stores instead.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       uint32_t *counter = p.counters + tile_id * TA_GEMV_COUNTER_STRIDE;
       if (tid == 0)
         last_flag =
-            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
       __syncthreads();
       if (!last_flag)
         return;
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       // Fixed split order: acc = ((p0 + p1) + p2) + ...
       f32x16 tot[FM][FN];
       for (uint32_t j = 0; j < S; ++j) {
