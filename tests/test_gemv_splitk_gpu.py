@@ -156,6 +156,9 @@ def test_swiglu_mlp_graph(ta, ex, oracle, m, monkeypatch):
     # down-proj checked against the oracle on the GPU's own h (isolates this GEMV)
     ref_y = oracle.reference_gemm(got_h, wdr, 1, m, hdim, ffn, binary=1, d=res, beta=1.0)
     check_f16(ex.download(y), ref_y, ffn, oracle)
+    # end to end: the oracle's own h through the oracle's down projection
+    ref_y_e2e = oracle.reference_gemm(ref_h, wdr, 1, m, hdim, ffn, binary=1, d=res, beta=1.0)
+    check_f16(ex.download(y), ref_y_e2e, ffn, oracle)
     # same graph unfused (run_ops on independent pieces) gives identical bits
     up2, h2 = ex.tensor([m, ffn]), ex.tensor([m, ffn])
     ex.run_ops([ta.MatmulOp(tx, tu, up2, packed_b=True)])
