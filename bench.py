@@ -485,6 +485,76 @@ def splitk_fused(ta, ex, iters=20):
     return out
 
 
+TUNER_SHAPES = (  # (config, B, M, N, K, f16 weights); one shape per BASELINE config
+    ("c1_512x512x512_f32", 1, 512, 512, 512, False),
+    ("c2_4096x4096x4096_f32", 1, 4096, 4096, 4096, False),
+    ("c3_gemv_1x5632x2048_f16w", 1, 1, 5632, 2048, True),
+    ("c4_64x256x65536_f32", 1, 64, 256, 65536, False),
+    ("c5_qkv_512x2560x2048_f16w", 1, 512, 2560, 2048, True),
+)
+
+
+def tuner(ta, ctx, iters=10):
+    """The ML_TUNE measured auto-tuner (src/executor/tuning.rs:76-250) on
+    one shape per BASELINE config, from an empty store: its pick (kernel and
+    split count) and, beside it, every registry kernel that supports the
+    shape forced through the executor's kernel selection (median of `iters`
+    run_ops GPU times), plus the split counts of the split-K probe.  Run
+    under rocprofv3 --pmc, the same dispatches give each candidate's
+    counters (MFMA busy cycles, HBM bytes), which is what justifies a pick."""
+    import tempfile
+    saved = os.environ.get("XDG_CACHE_HOME")
+    os.environ["XDG_CACHE_HOME"] = tempfile.mkdtemp(prefix="ta_tune_")
+    try:
+        tune_ex = ta.Executor(ctx, tune=True)
+    finally:
+        if saved is None:
+            os.environ.pop("XDG_CACHE_HOME", None)
+        else:
+            os.environ["XDG_CACHE_HOME"] = saved
+    forced = {}
+    rng = np.random.default_rng(81)
+    out = {}
+    for name, bt, m, n, k, f16 in TUNER_SHAPES:
+        a = tune_ex.tensor_from(rng.uniform(-1, 1, (m, k)).astype(np.float32))
+        b = tune_ex.tensor_from(rng.uniform(-1, 1, (k, n)).astype(np.float32), f16=f16)
+        c = tune_ex.tensor([m, n])
+        op = ta.MatmulOp(a, b, c)
+        log(f"  tuner {name} ...")
+        tune_ex.run_ops([op])  # tunes on first sight, then runs the pick
+        pick = tune_ex.dispatch_info_for(bt, m, n, k, f16)
+        picked_ns = median_ns([tune_ex.run_ops([op]) for _ in range(iters)])
+        cands = {}
+        for kname in ta.kernel_names():
+            if kname not in forced:
+                forced[kname] = ta.Executor(ctx, kernel_selection=kname, tune=False)
+            fx = forced[kname]
+            try:
+                for _ in range(2):
+                    fx.run_ops([op])
+            except ta.TensorAshError:
+                continue
+            cands[kname] = median_ns([fx.run_ops([op]) for _ in range(iters)]) / 1e3
+        entry = dict(pick=pick, pick_us=picked_ns / 1e3, candidates_us=cands)
+        if not f16:
+            splits = {}
+            for sk in (4, 8, 16, 32, 64, 128):
+                if k // sk < 128:
+                    continue
+                try:
+                    tune_ex.run_matmuls_split_k2(a, b, c, sk)
+                except ta.TensorAshError:
+                    continue
+                splits[sk] = median_ns([tune_ex.run_matmuls_split_k2(a, b, c, sk)
+                                        for _ in range(iters)]) / 1e3
+            entry["split_k2_us"] = splits
+        out[name] = entry
+    for fx in forced.values():
+        fx.close()
+    tune_ex.close()
+    return out
+
+
 def concurrency(ta, ex, iters=20):
     """Independent ops in one ta_run_ops call may run concurrently on
     several streams; the same ops as a dependent op graph run back to back
@@ -789,6 +859,9 @@ def main() -> int:
     if "splitk_fused" in sections:
         log("split-K with fused epilogues ...")
         secondary["splitk_fused_epilogue_f32"] = splitk_fused(ta, ex)
+    if "tuner" in sections:
+        log("ML_TUNE candidates ...")
+        secondary["tuner"] = tuner(ta, ctx)
     if "gelu" in sections:
         log("batched GELU GEMM ...")
         secondary["batched_gelu_8x2048^3"] = batched_gelu(ta, ex)

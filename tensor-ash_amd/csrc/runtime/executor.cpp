@@ -1571,8 +1571,14 @@ struct ExecutorImpl {
     std::optional<uint64_t> heur_ns;
     size_t win = cands[0];
     std::optional<uint64_t> win_ns;
+    const bool log = std::getenv("TA_LOG") != nullptr;
     for (size_t i = 0; i < cands.size(); ++i) {
       auto md = median(samples[i]);
+      if (log)
+        std::fprintf(stderr, "tensor-ash: tune B=%u %ux%ux%u candidate %s: median %.2f us (%zu samples)%s\n",
+                     d.batch, d.m, d.n, d.k, KERNEL_SPECS[cands[i]].name,
+                     md ? (double)*md / 1e3 : -1.0, samples[i].size(),
+                     cands[i] == heur ? " [heuristic]" : "");
       if (!md)
         continue;
       if (cands[i] == heur)
@@ -1605,6 +1611,9 @@ struct ExecutorImpl {
             ss.push_back(*ns);
         }
         auto md = median(ss);
+        if (log)
+          std::fprintf(stderr, "tensor-ash: tune B=%u %ux%ux%u split-K %s x %u: median %.2f us\n",
+                       d.batch, d.m, d.n, d.k, s1.name, splits, md ? (double)*md / 1e3 : -1.0);
         if (md && (!best || *md < *best)) {
           best = md;
           best_splits = splits;
