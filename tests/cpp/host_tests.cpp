@@ -233,6 +233,12 @@ static void test_gemv_plan() {
                                  : p.partial_bytes == (uint64_t)p.kchunks * p.tiles *
                                                           (dual ? 2 : 1) * p.mr * tw * 4);
           }
+  // One row, at least one tile per CU: whole-K units (lm_head); fewer tiles
+  // keep ~3 workgroups per CU.
+  const uint32_t u1 = gemv_unit(64, false, false, 1);
+  CHECK(plan_gemv(256, 1, 32000, 2048, 64, false, u1).kchunks == 1u);
+  CHECK(plan_gemv(256, 1, 5632, 2048, 64, false, u1).kchunks == 8u);
+  CHECK(plan_gemv(256, 4, 32000, 2048, 64, false, gemv_unit(64, false, false, 4)).kchunks > 1u);
 }
 
 static void test_tuner_helpers() {

@@ -34,7 +34,7 @@ def check_f16(got, ref, k, oracle):
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
-@pytest.mark.parametrize("k,n", [(2048, 5632), (5632, 2048), (300, 96), (64, 64)])
+@pytest.mark.parametrize("k,n", [(2048, 5632), (5632, 2048), (300, 96), (64, 64), (2048, 32000)])
 def test_packed_gemv(ta, ex, oracle, m, k, n):
     w, wr = f16_weights(oracle, k, n, 40 + m)
     x = oracle.fill_det(m * k, 41)
