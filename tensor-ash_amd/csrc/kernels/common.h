@@ -132,6 +132,18 @@ TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &
     __syncthreads();
     const uint32_t row0 = m0 + wm * WTM + fm * 32;
     const uint32_t col0 = n0 + wn * WTN;
+    // A lane's column quad is the same on every row it stores (64 lanes
+    // step through rows of WTN / 4 quads), so its bias quad is loaded once
+    // per block, not once per row: inside the loop each load's latency
+    // stood between the LDS read and the store.
+    static_assert(64 % (WTN / 4) == 0, "a lane keeps its columns across rows");
+    f32x4 bias_q = {0.f, 0.f, 0.f, 0.f};
+    if (!C_F16 && S == 1 && active && (p.flags & TA_FLAG_BIAS) && vec_out) {
+      const uint32_t col = col0 + (lane % (WTN / 4)) * 4;
+      if (col + 4 <= p.n)
+        bias_q = *reinterpret_cast<const f32x4 *>(
+            &p.bias[(uint64_t)batch * p.bias_batch_stride + col]);
+    }
     ta_with_act(S > 1 ? (uint32_t)TA_ACT_NONE : p.act, [&](auto act_c) __attribute__((always_inline)) {
     constexpr uint32_t ACT = decltype(act_c)::value;
 #pragma unroll 2
@@ -166,8 +178,7 @@ TA_DEVICE void ta_store_tile_staged(float *smem, Stage &&stage, const GemmArgs &
           if (p.flags & TA_FLAG_ACCUMULATE)
             o += *reinterpret_cast<const f32x4 *>(&p.c[base]);
           if (p.flags & TA_FLAG_BIAS)
-            o += *reinterpret_cast<const f32x4 *>(
-                &p.bias[(uint64_t)batch * p.bias_batch_stride + col]);
+            o += bias_q;
 #pragma unroll
           for (int c = 0; c < 4; ++c)
             o[c] = ta_act<ACT>(o[c]);
