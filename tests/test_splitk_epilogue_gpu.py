@@ -13,6 +13,7 @@ at S = 8 / 16 / 32.
 """
 
 import functools
+import os
 
 import numpy as np
 import pytest
@@ -148,3 +149,36 @@ def test_run_op_split_k2_rejects_f16_and_fusions(ta, ex):
     b = ex.tensor([64, 8])
     with pytest.raises(ta.TensorAshError, match="exceeds K=64"):
         ex.run_op_split_k2(ta.MatmulOp(a, b, c), 65)
+
+
+def test_splitk_fused_ops_in_graph_and_lanes(ta, ex, oracle):
+    """Fused deep-K ops on the split-K route inside one submission: two
+    independent ops in run_ops (one stream lane each or in order) give the
+    bits of the ops run alone, and in run_op_graph a later op reads the
+    first op's finished (reduced, epilogued) output as its A."""
+    m, n, k = 256, 256, 16384
+    op1, c1, ref1, _ = _case(ta, ex, oracle, 1, m, n, k, "bias_gelu", seed=91)
+    op2, c2, ref2, _ = _case(ta, ex, oracle, 1, m, n, k, "silu_mul_d", seed=93)
+    ex.run_ops([op1])
+    alone1 = ex.download(c1).copy()
+    ex.run_ops([op2])
+    alone2 = ex.download(c2).copy()
+    check_f32(alone1, ref1, k, oracle)
+    check_f32(alone2, ref2, k, oracle)
+    for lanes in ("1", "2"):
+        os.environ["TA_RUN_OPS_LANES"] = lanes
+        try:
+            ex.run_ops([op1, op2])
+        finally:
+            del os.environ["TA_RUN_OPS_LANES"]
+        np.testing.assert_array_equal(ex.download(c1), alone1)
+        np.testing.assert_array_equal(ex.download(c2), alone2)
+    # dependent graph: C3 = C1 @ B3 (256 x 64 x 256), reading op1's output
+    hb3 = oracle.fill_det(n * 64, 95)
+    b3, c3 = ex.tensor_from(hb3, shape=[n, 64]), ex.tensor([m, 64])
+    ex.run_op_graph([op1, ta.MatmulOp(c1, b3, c3)])
+    np.testing.assert_array_equal(ex.download(c1), alone1)
+    # A = C1 is not unit-scaled (|C1| up to ~70), so the bound scales with max|A|
+    got3, ref3 = ex.download(c3).reshape(-1), oracle.cpu_bmm(alone1, hb3, None, 1, m, 64, n)
+    err, idx = oracle.max_abs_err(got3, ref3)
+    assert err <= oracle.tolerance(n) * float(np.max(np.abs(alone1))), f"abs err {err} at {idx}"
