@@ -160,6 +160,21 @@ uint32_t *alloc_host_status() {
   return static_cast<uint32_t *>(p);
 }
 
+// Device address of a status word, looked up once per word: the runtime
+// call sits between a submission's start event and its first launch.
+uint32_t *device_status(uint32_t *host) {
+  static std::mutex mu;
+  static std::map<uint32_t *, uint32_t *> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(host);
+  if (it != cache.end())
+    return it->second;
+  void *dp = nullptr;
+  hip_check(hipHostGetDevicePointer(&dp, host, 0), "hipHostGetDevicePointer");
+  cache[host] = static_cast<uint32_t *>(dp);
+  return static_cast<uint32_t *>(dp);
+}
+
 void check_host_status(uint32_t *word, void *mlp, uint64_t mlp_bytes) {
   volatile uint32_t *w = word;
   if (*w != 0) {
@@ -993,8 +1008,7 @@ struct ExecutorImpl {
     m.tag_b = reinterpret_cast<uint64_t *>(base + g.tag_b);
     m.tag_y = reinterpret_cast<uint64_t *>(base + g.tag_y);
     m.spin_limit = 1u << 20; // ~1 s of polling (a round is about a memory round trip)
-    void *dev_status = nullptr;
-    hip_check(hipHostGetDevicePointer(&dev_status, host_status, 0), "hipHostGetDevicePointer");
+    void *dev_status = device_status(host_status);
     m.status = static_cast<uint32_t *>(dev_status);
     m.units_a = g.tiles_a * g.kch_a;
     m.units_b = g.tiles_b * g.kch_b;
@@ -1171,8 +1185,7 @@ struct ExecutorImpl {
     c.n_jobs = n;
     c.spin_limit = 1u << 22; // ~seconds of polling: a safety net, see the kernel
     c.barrier = scratch.barrier;
-    void *dev_status = nullptr;
-    hip_check(hipHostGetDevicePointer(&dev_status, host_status, 0), "hipHostGetDevicePointer");
+    void *dev_status = device_status(host_status);
     c.status = static_cast<uint32_t *>(dev_status);
     const uint64_t grid = std::max<uint64_t>(1, std::min<uint64_t>(widest, 2ull * ctx->cu_count()));
     launch("ta_gemv_chain_f16_m1", (uint32_t)grid, 1, 1, 256, &c, stream);
