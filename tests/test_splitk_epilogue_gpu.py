@@ -182,3 +182,63 @@ def test_splitk_fused_ops_in_graph_and_lanes(ta, ex, oracle):
     got3, ref3 = ex.download(c3).reshape(-1), oracle.cpu_bmm(alone1, hb3, None, 1, m, 64, n)
     err, idx = oracle.max_abs_err(got3, ref3)
     assert err <= oracle.tolerance(n) * float(np.max(np.abs(alone1))), f"abs err {err} at {idx}"
+
+
+def _rand_cases():
+    """Seeded mixed shapes: ragged and aligned tiles, batched A or B, every
+    epilogue, explicit split counts (the generic and the pipelined stage-1
+    kernels both appear)."""
+    rng = np.random.default_rng(123)
+    names = list(EPILOGUES)
+    out = []
+    for i in range(12):
+        m = int(rng.choice([17, 32, 64, 96, 128, 192]))
+        n = int(rng.choice([8, 33, 64, 128, 256]))
+        k = int(rng.choice([512, 1000, 2048, 4096, 6144]))
+        splits = int(rng.choice([2, 3, 4, 8, 16]))
+        batch = int(rng.choice([1, 1, 2]))
+        b_batched = batch > 1 and bool(rng.integers(0, 2))
+        out.append((i, batch, b_batched, m, n, k, splits, names[i % len(names)]))
+    return out
+
+
+@pytest.mark.parametrize("i,batch,b_batched,m,n,k,splits,name", _rand_cases())
+def test_splitk_epilogue_mixed_shapes(ta, ex, oracle, i, batch, b_batched, m, n, k, splits, name):
+    bias_kind, act, binary, beta, acc = EPILOGUES[name]
+    seed = 200 + 7 * i
+    ha = oracle.fill_det(batch * m * k, seed)
+    nb = batch if b_batched else 1
+    hb = oracle.fill_det(nb * k * n, seed + 1)
+    sa = [batch, m, k] if batch > 1 else [m, k]
+    sb = [nb, k, n] if nb > 1 else [k, n]
+    sc = [batch, m, n] if batch > 1 else [m, n]
+    a, b, c = ex.tensor_from(ha, shape=sa), ex.tensor_from(hb, shape=sb), ex.tensor(sc)
+    hbias = bias = hd = d = None
+    stride = 0
+    if bias_kind == "n":
+        hbias = oracle.fill_det(n, seed + 2)
+        bias = ex.tensor_from(hbias, shape=[n])
+    elif bias_kind == "bn":
+        hbias = oracle.fill_det(batch * n, seed + 2)
+        bias = ex.tensor_from(hbias, shape=[batch, n] if batch > 1 else [n])
+        stride = n if batch > 1 else 0
+    if binary:
+        hd = oracle.fill_det(batch * m * n, seed + 3)
+        d = ex.tensor_from(hd, shape=sc)
+    hc0 = oracle.fill_det(batch * m * n, seed + 4) if acc else None
+    if acc:
+        ex.upload(c, hc0)
+    op = ta.MatmulOp(a, b, c, accumulate=acc,
+                     epilogue=ta.Epilogue(bias=bias, activation=act, binary=binary, d=d, beta=beta))
+    print(f"fused split-K case {i}: B={batch} (B batched {b_batched}) {m}x{n}x{k} S={splits} {name}",
+          flush=True)
+    ex.run_op_split_k2(op, min(splits, k))
+    if b_batched:
+        raw = np.concatenate([oracle.cpu_bmm(ha[j * m * k:(j + 1) * m * k], hb[j * k * n:(j + 1) * k * n],
+                                             None, 1, m, n, k) for j in range(batch)])
+    else:
+        raw = oracle.cpu_bmm(ha, hb, None, batch, m, n, k)
+    if acc:
+        raw = (raw.astype(np.float64) + hc0.astype(np.float64)).astype(np.float32)
+    ref = oracle.epilogue(raw, n, m * n, hbias, stride, act, binary, hd, beta)
+    check_f32(ex.download(c), ref, k, oracle)
