@@ -502,16 +502,25 @@ def tuner(ta, ctx, iters=10):
     run_ops GPU times), plus the split counts of the split-K probe.  Run
     under rocprofv3 --pmc, the same dispatches give each candidate's
     counters (MFMA busy cycles, HBM bytes), which is what justifies a pick."""
+    import shutil
     import tempfile
+    # A private, empty tune store for the whole section (the store is read
+    # when the executor is created and rewritten after every tuned shape).
     saved = os.environ.get("XDG_CACHE_HOME")
-    os.environ["XDG_CACHE_HOME"] = tempfile.mkdtemp(prefix="ta_tune_")
+    store = tempfile.mkdtemp(prefix="ta_tune_")
+    os.environ["XDG_CACHE_HOME"] = store
     try:
-        tune_ex = ta.Executor(ctx, tune=True)
+        return _tuner_runs(ta, ctx, iters)
     finally:
         if saved is None:
             os.environ.pop("XDG_CACHE_HOME", None)
         else:
             os.environ["XDG_CACHE_HOME"] = saved
+        shutil.rmtree(store, ignore_errors=True)
+
+
+def _tuner_runs(ta, ctx, iters):
+    tune_ex = ta.Executor(ctx, tune=True)
     forced = {}
     rng = np.random.default_rng(81)
     out = {}
