@@ -632,10 +632,11 @@ TA_GEMM_DUAL(m64n64, 64, 64, 64, 2, 2, 4)
 #else
 TA_PIPE_TILES
 #endif
-// f32 -> f16 (RNE) of n elements, 8 per thread: the A pre-pass of the
-// pipelined f16w kernels.
-extern "C" __global__ __launch_bounds__(256) void ta_cvt_f32_f16(CvtArgs p) {
-  const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+// f32 -> f16 (RNE) of n elements, 8 per thread (block b of a launch):
+// the A pre-pass of the pipelined f16w kernels.
+namespace {
+TA_DEVICE void cvt_block(const CvtArgs &p, uint64_t b) {
+  const uint64_t i = (b * 256 + threadIdx.x) * 8;
   if (i + 8 <= p.n) {
     const f32x4 lo = *reinterpret_cast<const f32x4 *>(p.src + i);
     const f32x4 hi = *reinterpret_cast<const f32x4 *>(p.src + i + 4);
@@ -650,4 +651,16 @@ extern "C" __global__ __launch_bounds__(256) void ta_cvt_f32_f16(CvtArgs p) {
     for (uint64_t j = i; j < p.n; ++j)
       reinterpret_cast<_Float16 *>(p.dst)[j] = (_Float16)p.src[j];
   }
+}
+} // namespace
+
+extern "C" __global__ __launch_bounds__(256) void ta_cvt_f32_f16(CvtArgs p) {
+  cvt_block(p, blockIdx.x);
+}
+
+extern "C" __global__ __launch_bounds__(256) void ta_cvt_f32_f16_pair(CvtPairArgs p) {
+  if (blockIdx.x < p.blocks0)
+    cvt_block(p.job[0], blockIdx.x);
+  else
+    cvt_block(p.job[1], blockIdx.x - p.blocks0);
 }

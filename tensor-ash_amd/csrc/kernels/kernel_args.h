@@ -116,6 +116,13 @@ typedef struct CvtArgs {
   uint64_t n;
 } CvtArgs;
 
+// Two conversions in one launch: blocks [0, blocks0) convert job[0], the
+// rest job[1] (the inputs a submission's f16w GEMMs convert, up front).
+typedef struct CvtPairArgs {
+  CvtArgs job[2];
+  uint64_t blocks0;
+} CvtPairArgs;
+
 // Decode GEMV over packed f16 weights W[N/TW][K][TW] (or row-major):
 // Y[m, :] = epilogue(alpha * X[m, :] @ W) for m < rows (rows <= 8).
 // With `w2` set (dual mode) the same launch also computes

@@ -466,6 +466,76 @@ struct ExecutorImpl {
     }
   };
 
+  // Does op i take the f32 -> f16 pre-pass of its A (the pipelined f16w
+  // route; not a16, whose A is f16 already)?
+  bool converts_a(const ResolvedMatmul &d, const OpPlan &p) const {
+    if (p.role == 1 || p.role == 3 || p.role == 4 || p.role == 5 || p.role == 6 || p.splitk2)
+      return false;
+    const KernelSpec &s = KERNEL_SPECS[p.kernel];
+    return (s.kind == KernelKind::GemmF16Mfma || s.kind == KernelKind::GemmF16Sk) &&
+           gemm_lds_ok(d);
+  }
+
+  // The first two distinct A's of a submission that take the pre-pass and
+  // that no earlier op writes (inputs, so converting them first changes no
+  // value) are converted by one launch into the two halves of the copy
+  // region and entered in the cache, where the ops then find them: one
+  // launch instead of two on the submission's critical path (the prefill
+  // layer converts x for QKV and up/gate and the attention output for O).
+  // Not with split-K ops in the submission: their planes share the region.
+  void convert_inputs_up_front(const std::vector<MatmulOp> &ops,
+                               const std::vector<ResolvedMatmul> &res,
+                               const std::vector<OpPlan> &plans, Scratch &scratch, CvtCache &cvt,
+                               hipStream_t stream) const {
+    if (std::getenv("TA_NO_CVT_PAIR"))
+      return;
+    for (const auto &p : plans)
+      if (p.splitk2)
+        return;
+    std::vector<const void *> written;
+    CvtArgs job[2];
+    const void *bufs[2] = {nullptr, nullptr};
+    int found = 0;
+    for (size_t i = 0; i < ops.size() && found < 2; ++i) {
+      const MatmulOp &op = ops[i];
+      if (converts_a(res[i], plans[i])) {
+        const void *buf = op.call.a->buffer_id();
+        const float *src = static_cast<const float *>(op.call.a->device_ptr());
+        const uint64_t n =
+            (res[i].batch_stride_a ? (uint64_t)res[i].batch : 1) * res[i].m * res[i].k;
+        const bool input = std::find(written.begin(), written.end(), buf) == written.end();
+        const bool seen = found > 0 && job[0].src == src && job[0].n == n && bufs[0] == buf;
+        if (input && !seen) {
+          job[found] = CvtArgs{src, nullptr, n};
+          bufs[found] = buf;
+          ++found;
+        }
+      }
+      written.push_back(op.call.c->buffer_id());
+      if (op.store.dst)
+        written.push_back(op.store.dst->buffer_id());
+    }
+    if (found < 2)
+      return;
+    const uint64_t half_bytes = scratch.splitk_bytes / 2 / 256 * 256;
+    for (int j = 0; j < 2; ++j)
+      if ((job[j].n * 2 + 255) / 256 * 256 > half_bytes)
+        return;
+    CvtPairArgs pa{};
+    for (int j = 0; j < 2; ++j) {
+      pa.job[j] = job[j];
+      pa.job[j].dst = reinterpret_cast<uint16_t *>(static_cast<char *>(scratch.splitk) +
+                                                   j * half_bytes);
+    }
+    pa.blocks0 = (job[0].n + 8 * 256 - 1) / (8 * 256);
+    const uint64_t blocks = pa.blocks0 + (job[1].n + 8 * 256 - 1) / (8 * 256);
+    if (blocks > 0x7fffffffull)
+      return;
+    launch("ta_cvt_f32_f16_pair", (uint32_t)blocks, 1, 1, 256, &pa, stream);
+    for (int j = 0; j < 2; ++j)
+      cvt.put(cvt.e[j], CvtEntry{bufs[j], pa.job[j].src, job[j].n, pa.job[j].dst, SIZE_MAX, j});
+  }
+
   // Does op i (the gate of a dual SwiGLU launch) feed op i + 1 as A on the
   // f16w pipelined route?  Then the dual launch also writes an f16 copy of
   // its output (the conversion pre-pass's values: the same RNE rounding of
@@ -1224,6 +1294,7 @@ struct ExecutorImpl {
               const std::vector<OpPlan> &plans, Scratch &scratch, uint32_t *host_status,
               hipStream_t stream) const {
     CvtCache cvt;
+    convert_inputs_up_front(ops, res, plans, scratch, cvt, stream);
     for (size_t i = 0; i < ops.size(); ++i) {
       const OpPlan &p = plans[i];
       // a cached f16 copy of A is stale once an op writes A's buffer

@@ -271,3 +271,33 @@ def test_f16_copy_cache_two_swiglu_outputs(ta, ex, oracle):
     np.testing.assert_array_equal(got["y1"], alone(h1, wd1))
     np.testing.assert_array_equal(got["y2"], alone(h2, wd2))
     np.testing.assert_array_equal(got["z"], alone(h1, wd3))
+
+
+def test_f16_paired_conversion_skips_produced_inputs(ta, ex, oracle):
+    """The two input A's a submission converts up front in one launch are
+    the first two that no earlier op writes.  Here the second distinct A
+    (y) is produced by the first op, so the pair is x and a2, and y is
+    converted when its op runs.  Every result equals the same GEMM run
+    alone, bit for bit."""
+    m, k, n = 256, 512, 512
+    hx, ha2 = oracle.fill_det(m * k, 6401), oracle.fill_det(m * k, 6402)
+    w = [ex.tensor_from(oracle.fill_normal(k * n, s, 0.02), shape=[k, n], f16=True)
+         for s in (6403, 6404, 6405, 6406)]
+    x, a2 = ex.tensor_from(hx, shape=[m, k]), ex.tensor_from(ha2, shape=[m, k])
+    y = ex.tensor([m, n])
+    c = [ex.tensor([m, n]) for _ in range(3)]
+    assert "mfma" in ex.dispatch_info_for(1, m, n, k, True)["kernel"]
+    print("paired conversion: x -> y, y, a2, x", flush=True)
+    ex.run_op_graph([ta.MatmulOp(x, w[0], y), ta.MatmulOp(y, w[1], c[0]),
+                     ta.MatmulOp(a2, w[2], c[1]), ta.MatmulOp(x, w[3], c[2])])
+
+    def alone(a_t, w_t):
+        out = ex.tensor([m, n])
+        ex.run_ops([ta.MatmulOp(a_t, w_t, out)])
+        return ex.download(out)
+
+    want_y = alone(x, w[0])
+    np.testing.assert_array_equal(ex.download(y), want_y)
+    np.testing.assert_array_equal(ex.download(c[0]), alone(y, w[1]))
+    np.testing.assert_array_equal(ex.download(c[1]), alone(a2, w[2]))
+    np.testing.assert_array_equal(ex.download(c[2]), alone(x, w[3]))
