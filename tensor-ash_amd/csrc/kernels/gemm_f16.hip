@@ -276,10 +276,15 @@ struct GemmH16Pipe {
   // is XORed with a pattern that separates the rows in chunk bits (b1,b2)
   // and in (b2,b3) - for 8-chunk rows, bit b2 together with the row parity.
   // BK = 32 (4-chunk A rows, 4 rows per 256-byte bank line): the slot is
-  // c ^ (((row >> 1) ^ (row >> 3)) & 3), distinct in (row & 3, slot) over
-  // 16 consecutive rows and in (row & 1, slot) over 8.
+  // c ^ (((row >> 1) ^ (row >> 2)) & 3).  Chosen by measurement: the
+  // pattern c ^ (((row >> 1) ^ (row >> 3)) & 3), which separates 8 and 16
+  // consecutive rows just as well on paper, stalled the dual 128 x 128
+  // tile's LDS on bank conflicts for a third of its active cycles
+  // (SQ_LDS_BANK_CONFLICT 1.5 M against 0.09 M cycles), as did
+  // (row >> 1) & 3; (row ^ (row >> 2)) & 3 and (row >> 2) & 3 measured
+  // conflict-free too.
   static TA_DEVICE uint32_t swz_a(uint32_t row) {
-    return CPA == 8 ? (row & 7u) ^ ((row >> 3) & 1u) : ((row >> 1) ^ (row >> 3)) & 3u;
+    return CPA == 8 ? (row & 7u) ^ ((row >> 3) & 1u) : ((row >> 1) ^ (row >> 2)) & 3u;
   }
   static TA_DEVICE uint32_t swz_b(uint32_t row) {
     return CPR >= 16 ? (0xACA60u >> (4u * (row & 3u))) & 15u : 2u * (row & 3u);
