@@ -274,9 +274,11 @@ template <int N, class F> TA_DEVICE void ta_static_for(F &&f) {
 //    B [16][BN] slabs in LDS,
 //    filled by direct global -> LDS loads (global_load_lds_dwordx4) with
 //    16-byte chunks XOR-swizzled per row on the global side:
-//      A rows (64 bytes): chunk ^ ((b1 ^ b3) | b2 << 1) of the row index, so
-//        8 consecutive rows of a ds_read_b128 hit distinct chunk slots in
-//        a 128-byte bank window and 16 rows distinct slots in 256 bytes;
+//      A rows (64 bytes): chunk ^ ((b1 ^ b2) | (b2 ^ b3) << 1) of the row
+//        index.  Chosen by measurement (SQ_LDS_BANK_CONFLICT): the pattern
+//        chunk ^ ((b1 ^ b3) | b2 << 1), which separates 8 and 16
+//        consecutive rows on paper, spent a quarter of the LDS's active
+//        cycles on bank conflicts in every tile; this one none;
 //      B rows (BN * 4 bytes): chunk ^ 4 * ((row >> 2) & 3), so the four rows a
 //        wave reads at once (k = group * 4 + s) use four 16-bank quarters.
 //  * One barrier per stage.  The LDS operands of stage k+1 are read into a
@@ -318,7 +320,7 @@ template <int BM, int BN, int WGM, int WGN, int NS> struct GemmF32Mi16 {
   typedef float f32x2 __attribute__((ext_vector_type(2)));
 
   static TA_DEVICE uint32_t swz_a(uint32_t row) {
-    return (((row >> 1) ^ (row >> 3)) & 1u) | (((row >> 2) & 1u) << 1);
+    return ((row >> 1) ^ (row >> 2)) & 3u;
   }
   static TA_DEVICE uint32_t swz_b(uint32_t row) { return 4u * ((row >> 2) & 3u); }
   // The side operation issued after MFMA i of a stage, or -1: one after
