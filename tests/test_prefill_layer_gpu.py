@@ -301,3 +301,33 @@ def test_f16_paired_conversion_skips_produced_inputs(ta, ex, oracle):
     np.testing.assert_array_equal(ex.download(c[0]), alone(y, w[1]))
     np.testing.assert_array_equal(ex.download(c[1]), alone(a2, w[2]))
     np.testing.assert_array_equal(ex.download(c[2]), alone(x, w[3]))
+
+
+def test_f16_paired_conversion_batched_inputs(ta, ex, oracle):
+    """Paired up-front conversion with batched A (each copy holds
+    batch * m * k values): two batched inputs, the first read again by a
+    third op, each result equal to the same GEMM run alone, bit for bit."""
+    batch, m, k, n = 3, 128, 256, 256
+    ha, hb = oracle.fill_det(batch * m * k, 6501), oracle.fill_det(batch * m * k, 6502)
+    w = [ex.tensor_from(oracle.fill_normal(k * n, s, 0.02), shape=[k, n], f16=True)
+         for s in (6503, 6504, 6505)]
+    a, b = ex.tensor_from(ha, shape=[batch, m, k]), ex.tensor_from(hb, shape=[batch, m, k])
+    c = [ex.tensor([batch, m, n]) for _ in range(3)]
+    assert "mfma" in ex.dispatch_info_for(batch, m, n, k, True)["kernel"]
+    print("paired conversion: batched a, b, a", flush=True)
+    ex.run_op_graph([ta.MatmulOp(a, w[0], c[0]), ta.MatmulOp(b, w[1], c[1]), ta.MatmulOp(a, w[2], c[2])])
+
+    def alone(a_t, w_t):
+        out = ex.tensor([batch, m, n])
+        ex.run_ops([ta.MatmulOp(a_t, w_t, out)])
+        return ex.download(out)
+
+    np.testing.assert_array_equal(ex.download(c[0]), alone(a, w[0]))
+    np.testing.assert_array_equal(ex.download(c[1]), alone(b, w[1]))
+    np.testing.assert_array_equal(ex.download(c[2]), alone(a, w[2]))
+    # and the copy is the right one: against the oracle on f16-rounded inputs
+    wb = oracle.round_via_f16(oracle.fill_normal(k * n, 6504, 0.02))
+    ref = np.concatenate([oracle.cpu_bmm(oracle.round_via_f16(hb[i * m * k:(i + 1) * m * k]), wb, None, 1, m, n, k)
+                          for i in range(batch)])
+    err, idx = oracle.max_abs_err(ex.download(c[1]).reshape(-1), ref)
+    assert err <= 2 * oracle.tolerance(k) + 1e-4, f"abs err {err} at {idx}"
