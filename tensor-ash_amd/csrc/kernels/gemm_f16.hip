@@ -600,7 +600,7 @@ TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
 // workgroups per tile).
 #define TA_GEMM_PIPE(NAME, BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF, DUAL)                \
   extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(GemmArgs p) {             \
-    static_assert(64 * WGM * WGN == ta_h16_lds_threads(BM, BN), "host launch width");         \
+    static_assert(64 * WGM * WGN == ta_h16_lds_threads(BM, BN, DUAL), "host launch width");   \
     GemmH16Pipe<BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF, DUAL>::run(p);                  \
   }
 #define TA_GEMM_LDS(TAG, BM, BN, BK, WGM, WGN, NS, DBUF)                                      \
@@ -623,13 +623,13 @@ TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
 // 64-deep slabs through 3 stages.
 #ifndef TA_PIPE_TILES
 TA_GEMM_LDS(m256n256, 256, 256, 64, 2, 4, 2, false)
-TA_GEMM_LDS(m128n128, 128, 128, 64, 2, 4, 4, true)
+TA_GEMM_LDS(m128n128, 128, 128, 64, 4, 4, 4, true)
 TA_GEMM_LDS(m128n64, 128, 64, 64, 4, 2, 4, true)
 TA_GEMM_LDS(m64n128, 64, 128, 64, 2, 4, 4, true)
 TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4, true)
 TA_GEMM_SK(m64n128, 64, 128, 64, 2, 4, 4)
 TA_GEMM_SK(m128n64, 128, 64, 64, 4, 2, 4)
-TA_GEMM_SK(m128n128, 128, 128, 64, 2, 4, 4)
+TA_GEMM_SK(m128n128, 128, 128, 64, 4, 4, 4)
 TA_GEMM_DUAL(m128n128, 128, 128, 32, 2, 4, 5)
 TA_GEMM_DUAL(m128n64, 128, 64, 64, 4, 2, 4)
 TA_GEMM_DUAL(m64n128, 64, 128, 64, 2, 4, 3)
