@@ -437,7 +437,8 @@ struct GemmH16Pipe {
 
     if constexpr (!DBUF) {
       // One register set: wait for stage kt, barrier, refill, read, MFMAs
-      // (the 256 x 256 tile: two 64 KiB stages leave no room for a third).
+      // (the 256 x 256 tile: two 64 KiB stages leave no room for a third;
+      // the dual 128 x 128 tile at 16 waves, whose second set would spill).
       for (uint32_t kt = 0; kt < kts; ++kt) {
         if (kt + NS - 2 < kts)
           asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * LD) : "memory");
@@ -600,7 +601,7 @@ TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
 // workgroups per tile).
 #define TA_GEMM_PIPE(NAME, BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF, DUAL)                \
   extern "C" __global__ __launch_bounds__(64 * WGM * WGN) void NAME(GemmArgs p) {             \
-    static_assert(64 * WGM * WGN == ta_h16_lds_threads(BM, BN, DUAL), "host launch width");   \
+    static_assert(64 * WGM * WGN == ta_h16_lds_threads(BM, BN), "host launch width");         \
     GemmH16Pipe<BM, BN, BK, WGM, WGN, NS, C_F16, SPLIT, DBUF, DUAL>::run(p);                  \
   }
 #define TA_GEMM_LDS(TAG, BM, BN, BK, WGM, WGN, NS, DBUF)                                      \
@@ -610,17 +611,18 @@ TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
   TA_GEMM_PIPE(ta_gemm_h16sk_##TAG, BM, BN, BK, WGM, WGN, NS, false, true, true, false)
 // SwiGLU pair in one pass: C = act(alpha * A @ B + bias) * U with
 // U = alpha * A @ B2 stored to c2 (A read once for both weight matrices).
-#define TA_GEMM_DUAL(TAG, BM, BN, BK, WGM, WGN, NS)                                           \
-  TA_GEMM_PIPE(ta_gemm_h16dual_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, false, false, true, true)
+#define TA_GEMM_DUAL(TAG, BM, BN, BK, WGM, WGN, NS, DBUF)                                     \
+  TA_GEMM_PIPE(ta_gemm_h16dual_##TAG##_lds, BM, BN, BK, WGM, WGN, NS, false, false, DBUF, true)
 
 // Stage counts and loop forms as measured fastest on the config-5 shapes
 // and 4096^3 (64 x 64: 11.9 us for 512x2048x2048; 128 x 64: 14.4 us for
 // 512x2560x2048; 128 x 128: 21.7 us for 512x5632x2048; split 128 x 64,
 // S = 2: 22.1 us for 512x2048x5632; 256 x 256: 110 us for 4096^3).  The
-// dual 128 x 128 tile streams 32-deep slabs through 5 stages (four in
-// flight behind the awaited one): with its weights coming from HBM rather
-// than the last-level cache, 47 us for 512x5632x2048 against 51 us with
-// 64-deep slabs through 3 stages.
+// 128 x 128 tiles run 16 waves.  The dual one keeps a single fragment
+// register set (double-buffered, its two accumulator sets spill at 16
+// waves); the other three waves of each SIMD cover the reads, and the
+// config-5 layer took 114.6 us against 120.4-121.4 us with 8 waves,
+// 32-deep slabs through 5 stages and two fragment sets.
 #ifndef TA_PIPE_TILES
 TA_GEMM_LDS(m256n256, 256, 256, 64, 2, 4, 2, false)
 TA_GEMM_LDS(m128n128, 128, 128, 64, 4, 4, 4, true)
@@ -630,10 +632,10 @@ TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4, true)
 TA_GEMM_SK(m64n128, 64, 128, 64, 2, 4, 4)
 TA_GEMM_SK(m128n64, 128, 64, 64, 4, 2, 4)
 TA_GEMM_SK(m128n128, 128, 128, 64, 4, 4, 4)
-TA_GEMM_DUAL(m128n128, 128, 128, 32, 2, 4, 5)
-TA_GEMM_DUAL(m128n64, 128, 64, 64, 4, 2, 4)
-TA_GEMM_DUAL(m64n128, 64, 128, 64, 2, 4, 3)
-TA_GEMM_DUAL(m64n64, 64, 64, 64, 2, 2, 4)
+TA_GEMM_DUAL(m128n128, 128, 128, 64, 4, 4, 3, false)
+TA_GEMM_DUAL(m128n64, 128, 64, 64, 4, 2, 4, true)
+TA_GEMM_DUAL(m64n128, 64, 128, 64, 2, 4, 3, true)
+TA_GEMM_DUAL(m64n64, 64, 64, 64, 2, 2, 4, true)
 #else
 TA_PIPE_TILES
 #endif

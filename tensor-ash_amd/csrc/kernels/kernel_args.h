@@ -442,11 +442,9 @@ constexpr int ta_mi16_stages(int bm, int bn) {
 
 // Threads of the pipelined f16-MFMA kernels (ta_gemm_{h16,a16}_<tile>_lds,
 // ta_gemm_h16sk_<tile>, ta_gemm_h16dual_<tile>_lds): 16 waves (four per
-// SIMD, one 32 x 32 block each) for the single-matrix 128 x 128 tile, 8
-// waves (two per SIMD) for the dual 128 x 128 tile (at 16 waves its two
-// accumulator sets spill) and the other tiles of 128 x 64 and larger, 4
-// waves for 64 x 64.
-constexpr int ta_h16_lds_threads(int bm, int bn, bool dual = false) {
-  return bm == 128 && bn == 128 && !dual ? 1024 : bm * bn >= 128 * 64 ? 512 : 256;
+// SIMD, one 32 x 32 block each) for 128 x 128 tiles, 8 waves (two per SIMD)
+// for the other tiles of 128 x 64 and larger, 4 waves for 64 x 64.
+constexpr int ta_h16_lds_threads(int bm, int bn) {
+  return bm == 128 && bn == 128 ? 1024 : bm * bn >= 128 * 64 ? 512 : 256;
 }
 #endif

@@ -652,8 +652,7 @@ struct ExecutorImpl {
       a.c16 = c16;
       std::string sym = s.symbol;
       sym.replace(0, std::strlen("ta_gemm_h16_"), "ta_gemm_h16dual_");
-      launch(sym + "_lds", (uint32_t)gx, 1, (uint32_t)gz,
-             (uint32_t)ta_h16_lds_threads((int)s.tile_m, (int)s.tile_n, true), &a, stream);
+      launch(sym + "_lds", (uint32_t)gx, 1, (uint32_t)gz, lds_threads, &a, stream);
       return;
     }
     const bool vec = d.k % 4 == 0 && d.n % 4 == 0;
