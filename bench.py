@@ -313,8 +313,9 @@ def prefill_layer(ta, ex, iters=10):
                               roofline=time_roofline(total_flops, total_bytes, total_ns * 1e-9, PEAK_FP16_MFMA))
     # The layer as a prefill runs it: the five GEMMs in one dependent op
     # graph (one event pair).  up and gate run as one dual launch, which
-    # also leaves the f16 copy of h that down reads; x is converted for QKV
-    # and again for up/gate (O's conversion of attn sits between them).
+    # also leaves the f16 copy of h that down reads; x and attn are
+    # converted to f16 by one paired launch at the start, and x's copy
+    # serves QKV and up/gate.
     layers = [[op for ops in c.values() for op in ops] for c in per_set]
     ns = rotated(lambda i: ex.run_op_graph(layers[i]), copies)
     out["layer_gemms_one_submission"] = dict(
