@@ -492,31 +492,26 @@ struct ExecutorImpl {
     for (const auto &p : plans)
       if (p.splitk2)
         return;
-    std::vector<const void *> written;
-    CvtArgs job[2];
-    const void *bufs[2] = {nullptr, nullptr};
-    int found = 0;
-    for (size_t i = 0; i < ops.size() && found < 2; ++i) {
+    std::vector<CvtCandidate> cand(ops.size());
+    for (size_t i = 0; i < ops.size(); ++i) {
       const MatmulOp &op = ops[i];
-      if (converts_a(res[i], plans[i])) {
-        const void *buf = op.call.a->buffer_id();
-        const float *src = static_cast<const float *>(op.call.a->device_ptr());
-        const uint64_t n =
-            (res[i].batch_stride_a ? (uint64_t)res[i].batch : 1) * res[i].m * res[i].k;
-        const bool input = std::find(written.begin(), written.end(), buf) == written.end();
-        const bool seen = found > 0 && job[0].src == src && job[0].n == n && bufs[0] == buf;
-        if (input && !seen) {
-          job[found] = CvtArgs{src, nullptr, n};
-          bufs[found] = buf;
-          ++found;
-        }
-      }
-      written.push_back(op.call.c->buffer_id());
-      if (op.store.dst)
-        written.push_back(op.store.dst->buffer_id());
+      cand[i].a_buffer = op.call.a->buffer_id();
+      cand[i].a_ptr = op.call.a->device_ptr();
+      cand[i].n = (res[i].batch_stride_a ? (uint64_t)res[i].batch : 1) * res[i].m * res[i].k;
+      cand[i].converts = converts_a(res[i], plans[i]);
+      cand[i].writes[0] = op.call.c->buffer_id();
+      cand[i].writes[1] = op.store.dst ? op.store.dst->buffer_id() : nullptr;
     }
-    if (found < 2)
+    const std::vector<size_t> picks = paired_conversion_picks(cand);
+    if (picks.size() != 2)
       return;
+    CvtArgs job[2];
+    const void *bufs[2];
+    for (int j = 0; j < 2; ++j) {
+      const CvtCandidate &c = cand[picks[j]];
+      job[j] = CvtArgs{static_cast<const float *>(c.a_ptr), nullptr, c.n};
+      bufs[j] = c.a_buffer;
+    }
     const uint64_t half_bytes = scratch.splitk_bytes / 2 / 256 * 256;
     for (int j = 0; j < 2; ++j)
       if ((job[j].n * 2 + 255) / 256 * 256 > half_bytes)

@@ -101,6 +101,22 @@ uint32_t gemv_unit(uint32_t tw, bool f32_weights, bool dual, uint32_t rows);
 GemvPlan plan_gemv(uint32_t cus, uint32_t rows, uint32_t n, uint32_t k, uint32_t tw, bool dual,
                    uint32_t unit);
 
+// ---- f16w A conversions converted up front ----
+// One op of a submission as the paired up-front conversion sees it: its A
+// (buffer, device pointer, values converted), whether its route converts A
+// to f16, and the buffers it writes.
+struct CvtCandidate {
+  const void *a_buffer = nullptr;
+  const void *a_ptr = nullptr;
+  uint64_t n = 0;
+  bool converts = false;
+  const void *writes[2] = {nullptr, nullptr};
+};
+// Indices of the ops whose A is converted at submission start: the first
+// two distinct A's that take the conversion and that no earlier op writes
+// (fewer than two: nothing is paired).
+std::vector<size_t> paired_conversion_picks(const std::vector<CvtCandidate> &ops);
+
 // ---- tuner (src/executor/tuning.rs:300-313, pipeline/tuning.rs) ----
 std::optional<uint64_t> median(std::vector<uint64_t> samples);
 size_t candidate_at(size_t len, uint32_t round, size_t offset);

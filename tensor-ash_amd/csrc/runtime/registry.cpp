@@ -472,6 +472,26 @@ GemvPlan plan_gemv(uint32_t cus, uint32_t rows, uint32_t n, uint32_t k, uint32_t
   return p;
 }
 
+std::vector<size_t> paired_conversion_picks(const std::vector<CvtCandidate> &ops) {
+  std::vector<const void *> written;
+  std::vector<size_t> picks;
+  for (size_t i = 0; i < ops.size() && picks.size() < 2; ++i) {
+    const CvtCandidate &c = ops[i];
+    if (c.converts && std::find(written.begin(), written.end(), c.a_buffer) == written.end()) {
+      const bool seen = !picks.empty() && ops[picks[0]].a_buffer == c.a_buffer &&
+                        ops[picks[0]].a_ptr == c.a_ptr && ops[picks[0]].n == c.n;
+      if (!seen)
+        picks.push_back(i);
+    }
+    for (const void *w : c.writes)
+      if (w)
+        written.push_back(w);
+  }
+  if (picks.size() < 2)
+    picks.clear();
+  return picks;
+}
+
 // ---- tuner helpers (src/executor/tuning.rs:283-313) ----
 
 std::optional<uint64_t> median(std::vector<uint64_t> s) {

@@ -7,6 +7,7 @@
 #include <functional>
 #include <set>
 #include <string>
+#include <vector>
 
 #include "../../tensor-ash_amd/csrc/runtime/internal.hpp"
 
@@ -308,6 +309,49 @@ static void test_dtype() {
   CHECK(has(error_of([&] { pack_f16w_row_tiles(src, 4, 4, 3); }), "not a multiple of tile_n=3"));
 }
 
+static void test_paired_conversion_picks() {
+  // The f16w route's up-front conversion pairs the first two distinct A's
+  // that are converted and that no earlier op of the submission writes.
+  int x, y, z, a2, c0, c1, c2, c3;
+  auto op = [](const void *a, bool conv, const void *c, uint64_t n = 100) {
+    CvtCandidate k;
+    k.a_buffer = a;
+    k.a_ptr = a;
+    k.n = n;
+    k.converts = conv;
+    k.writes[0] = c;
+    return k;
+  };
+  using V = std::vector<size_t>;
+  // the prefill layer: QKV(x), O(attn), up(x), gate(x), down(h from gate)
+  CHECK(paired_conversion_picks({op(&x, true, &c0), op(&a2, true, &c1), op(&x, true, &c2),
+                                 op(&x, true, &y), op(&y, true, &c3)}) == V{0, 1});
+  // a repeated A is not paired with itself
+  CHECK(paired_conversion_picks({op(&x, true, &c0), op(&x, true, &c1), op(&a2, true, &c2)}) ==
+        V{0, 2});
+  // an A an earlier op writes is skipped (converted when its op runs)
+  CHECK(paired_conversion_picks({op(&x, true, &y), op(&y, true, &c0), op(&a2, true, &c1),
+                                 op(&x, true, &c2)}) == V{0, 2});
+  CHECK(paired_conversion_picks({op(&a2, true, &x), op(&x, true, &c0), op(&z, true, &c1)}) ==
+        V{0, 2});
+  // a store destination counts as written too
+  {
+    auto w = op(&c0, false, &c1);
+    w.writes[1] = &x;
+    CHECK(paired_conversion_picks({w, op(&x, true, &c2), op(&a2, true, &c3), op(&z, true, &y)}) ==
+          V{2, 3});
+  }
+  // ops whose route does not convert A are ignored
+  CHECK(paired_conversion_picks({op(&x, false, &c0), op(&a2, true, &c1), op(&z, true, &c2)}) ==
+        V{1, 2});
+  // the same buffer viewed with a different element count is a distinct copy
+  CHECK(paired_conversion_picks({op(&x, true, &c0, 100), op(&x, true, &c1, 200)}) == V{0, 1});
+  // fewer than two candidates: nothing paired
+  CHECK(paired_conversion_picks({op(&x, true, &c0), op(&x, true, &c1)}).empty());
+  CHECK(paired_conversion_picks({op(&x, true, &c0), op(&a2, false, &c1)}).empty());
+  CHECK(paired_conversion_picks({}).empty());
+}
+
 int main() {
   test_resolution();
   test_registry();
@@ -316,6 +360,7 @@ int main() {
   test_gemv_plan();
   test_tuner_helpers();
   test_dtype();
+  test_paired_conversion_picks();
   std::printf("%d checks, %d failed\n", g_pass + g_fail, g_fail);
   if (g_fail == 0)
     std::printf("all passed\n");
