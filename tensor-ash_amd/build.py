@@ -107,10 +107,21 @@ def build_vendor_bench() -> Path:
     return out
 
 
+def build_handoff_probe() -> Path:
+    """lib/handoff_probe: the cross-workgroup hand-off latency probe
+    (measurement tool, not part of the library)."""
+    src = PKG / "vendor_bench" / "handoff_probe.cpp"
+    out = LIB / "handoff_probe"
+    LIB.mkdir(exist_ok=True)
+    _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+          "-packed-fp32-ops", str(src), "-o", str(out)])
+    return out
+
+
 def build_all() -> None:
     with cf.ThreadPoolExecutor(max_workers=4) as pool:
         futs = [pool.submit(build_kernels), pool.submit(build_host), pool.submit(build_oracle),
-                pool.submit(build_vendor_bench)]
+                pool.submit(build_vendor_bench), pool.submit(build_handoff_probe)]
         for f in futs:
             f.result()
 
