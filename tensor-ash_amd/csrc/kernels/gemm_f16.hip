@@ -618,17 +618,19 @@ TA_GEMM_H16_FAMILY(m64n64, 64, 64, 2, 2)
 // and 4096^3 (64 x 64: 11.9 us for 512x2048x2048; 128 x 64: 14.4 us for
 // 512x2560x2048; 128 x 128: 21.7 us for 512x5632x2048; split 128 x 64,
 // S = 2: 22.1 us for 512x2048x5632; 256 x 256: 110 us for 4096^3).  The
-// 128 x 128 tiles run 16 waves.  The dual one keeps a single fragment
-// register set (double-buffered, its two accumulator sets spill at 16
-// waves); the other three waves of each SIMD cover the reads, and the
-// config-5 layer took 114.6 us against 120.4-121.4 us with 8 waves,
-// 32-deep slabs through 5 stages and two fragment sets.
+// 128 x 128 tiles run 16 waves.  The 64 x 64 tile reads each stage's
+// fragments just before its MFMAs (one register set: O-proj 21.5 us
+// against 22.1-22.6 us with two, timed with its conversion).  The dual
+// 128 x 128 tile keeps one register set too (with two, its accumulator
+// sets spill at 16 waves); the other three waves of each SIMD cover the
+// reads, and the config-5 layer took 114.6 us against 120.4-121.4 us with
+// 8 waves, 32-deep slabs through 5 stages and two fragment sets.
 #ifndef TA_PIPE_TILES
 TA_GEMM_LDS(m256n256, 256, 256, 64, 2, 4, 2, false)
 TA_GEMM_LDS(m128n128, 128, 128, 64, 4, 4, 4, true)
 TA_GEMM_LDS(m128n64, 128, 64, 64, 4, 2, 4, true)
 TA_GEMM_LDS(m64n128, 64, 128, 64, 2, 4, 4, true)
-TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4, true)
+TA_GEMM_LDS(m64n64, 64, 64, 64, 2, 2, 4, false)
 TA_GEMM_SK(m64n128, 64, 128, 64, 2, 4, 4)
 TA_GEMM_SK(m128n64, 128, 64, 64, 4, 2, 4)
 TA_GEMM_SK(m128n128, 128, 128, 64, 4, 4, 4)
